@@ -1,0 +1,294 @@
+/*
+ * zcgvs_hip.h - C ABI of the MI355X (gfx950) zero-copy search hot path.
+ *
+ * Every entry point takes plain device pointers, sizes and a stream handle and returns a
+ * zcgvs_status code. Nothing here throws, and no C++ or torch type crosses the boundary.
+ * The message describing the most recent failure on the calling thread is returned by
+ * zcgvs_last_error().
+ *
+ * Error contract (mirrors the reference's exception split, include/zcgvs/core/cuda_check.hpp
+ * and src/search/searcher.cpp:91-135):
+ *   ZCGVS_ERR_INVALID_ARGUMENT  - the reference throws std::invalid_argument;
+ *   ZCGVS_ERR_RUNTIME           - the reference throws std::runtime_error (e.g. N > INT32_MAX);
+ *   ZCGVS_ERR_HIP               - a HIP runtime call failed (the reference's CudaError).
+ * Launchers that receive empty work (count <= 0) return ZCGVS_OK without launching, exactly
+ * like the reference launchers (src/cuda/similarity.cu:356-358, topk.cu:143-145).
+ *
+ * Launchers are asynchronous on the given stream, never allocate device memory, never
+ * synchronize, and are safe to record into a HIP graph (zcgvs_graph_begin_capture). The one
+ * exception is zcgvs_memset, which must not be recorded into a graph; use zcgvs_fill_u32.
+ *
+ * Enumerations keep the reference's numeric codes, which are part of its on-disk format:
+ *   metric (include/zcgvs/core/metric.hpp:8-12), dtype (include/zcgvs/core/scalar_type.hpp:12-17).
+ *
+ * Top-k ordering (all selection entry points): score descending, ties broken by the lower
+ * corpus index, i.e. the order std::stable_sort gives in tests/cpp/cpu_reference.hpp:26-34.
+ * -0.0f ranks equal to +0.0f; a NaN score ranks below every other score.
+ */
+#ifndef ZCGVS_HIP_H
+#define ZCGVS_HIP_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+/* ------------------------------------------------------------------------------------------
+ * Status, enums, opaque handles
+ * ---------------------------------------------------------------------------------------- */
+enum zcgvs_status {
+    ZCGVS_OK = 0,
+    ZCGVS_ERR_INVALID_ARGUMENT = 1,
+    ZCGVS_ERR_RUNTIME = 2,
+    ZCGVS_ERR_HIP = 3,
+    ZCGVS_ERR_UNSUPPORTED = 4
+};
+
+/* include/zcgvs/core/metric.hpp:8-12 */
+enum zcgvs_metric { ZCGVS_METRIC_COSINE = 0, ZCGVS_METRIC_DOT = 1, ZCGVS_METRIC_L2 = 2 };
+
+/* include/zcgvs/core/scalar_type.hpp:12-17 */
+enum zcgvs_dtype {
+    ZCGVS_DTYPE_F32 = 0,
+    ZCGVS_DTYPE_F16 = 1,
+    ZCGVS_DTYPE_I8 = 2,
+    ZCGVS_DTYPE_BINARY = 3
+};
+
+/* How an int8 corpus is scored.
+ *  REFERENCE: (int8 * one matrix-wide scale) against a float32 query, accumulated in float32,
+ *             as src/cuda/similarity.cu:59-67 and include/zcgvs/cuda/decode.cuh:24-26 do.
+ *  PER_VECTOR: each row r carries its own scale s_r = max|x_r| / 127; queries are quantized the
+ *             same way on the device; score = (float)(int32 dot) * (s_q * s_r), evaluated in
+ *             exactly that order. No counterpart in the reference (its format has one scale). */
+enum zcgvs_int8_mode { ZCGVS_INT8_REFERENCE = 0, ZCGVS_INT8_PER_VECTOR = 1 };
+
+typedef void* zcgvs_stream_t; /* hipStream_t; NULL is the null stream   */
+typedef void* zcgvs_event_t;  /* hipEvent_t                               */
+typedef void* zcgvs_graph_t;  /* hipGraphExec_t (instantiated graph)      */
+
+/* Message for the most recent non-OK status returned on this thread ("" if none). */
+const char* zcgvs_last_error(void);
+/* Library version string, e.g. "zcgvs-hip 0.1.0 gfx950". */
+const char* zcgvs_version(void);
+
+/* ------------------------------------------------------------------------------------------
+ * Device, memory, streams, events, graphs - the thin runtime layer the C++17 host uses in
+ * place of include/zcgvs/core/{cuda_context,device_buffer,pinned_buffer,cuda_stream}.hpp.
+ * ---------------------------------------------------------------------------------------- */
+typedef struct zcgvs_device_info {
+    char name[256];
+    char arch[64];             /* gcnArchName, e.g. "gfx950:sramecc+:xnack-" */
+    size_t total_memory;       /* bytes */
+    int compute_units;
+    int clock_khz;
+    int memory_clock_khz;
+    int memory_bus_width;      /* bits */
+    int l2_cache_bytes;
+    int major;
+    int minor;
+    /* 2 * memory clock * bus width / 8, the formula of include/zcgvs/core/cuda_context.hpp:20-23 */
+    double peak_bandwidth_gbs;
+} zcgvs_device_info;
+
+int zcgvs_device_count(int* count);
+int zcgvs_set_device(int device);                       /* src/core/cuda_context.cpp:9 */
+int zcgvs_get_device(int* device);
+int zcgvs_device_query(int device, zcgvs_device_info* out); /* src/core/cuda_context.cpp:23-45 */
+int zcgvs_device_synchronize(void);
+
+int zcgvs_malloc(void** ptr, size_t bytes);           /* device_buffer.hpp:40-56 */
+int zcgvs_free(void* ptr);
+int zcgvs_host_alloc(void** ptr, size_t bytes);       /* pinned_buffer.hpp:14-67 */
+int zcgvs_host_free(void* ptr);
+int zcgvs_memcpy_h2d(void* dst, const void* src, size_t bytes, zcgvs_stream_t stream);
+int zcgvs_memcpy_d2h(void* dst, const void* src, size_t bytes, zcgvs_stream_t stream);
+int zcgvs_memcpy_d2d(void* dst, const void* src, size_t bytes, zcgvs_stream_t stream);
+/* Not graph-capture safe (records a memset node); use zcgvs_fill_u32 inside captures. */
+int zcgvs_memset(void* dst, int value, size_t bytes, zcgvs_stream_t stream);
+/* Fills `count` 32-bit words with `value` using a kernel (capture safe). */
+int zcgvs_fill_u32(void* dst, uint32_t value, size_t count, zcgvs_stream_t stream);
+
+int zcgvs_stream_create(zcgvs_stream_t* stream);      /* cuda_stream.hpp:9-43 */
+int zcgvs_stream_destroy(zcgvs_stream_t stream);
+int zcgvs_stream_synchronize(zcgvs_stream_t stream);
+
+int zcgvs_event_create(zcgvs_event_t* event);
+int zcgvs_event_destroy(zcgvs_event_t event);
+int zcgvs_event_record(zcgvs_event_t event, zcgvs_stream_t stream);
+int zcgvs_event_synchronize(zcgvs_event_t event);
+int zcgvs_event_elapsed_ms(float* ms, zcgvs_event_t start, zcgvs_event_t end);
+
+/* Stream capture into an instantiated graph (src/search/searcher.cpp:305-342). Capture uses
+ * the thread-local mode. end_capture instantiates and returns the executable graph. */
+int zcgvs_graph_begin_capture(zcgvs_stream_t stream);
+int zcgvs_graph_end_capture(zcgvs_stream_t stream, zcgvs_graph_t* graph);
+int zcgvs_graph_launch(zcgvs_graph_t graph, zcgvs_stream_t stream);
+int zcgvs_graph_destroy(zcgvs_graph_t graph);
+
+/* ------------------------------------------------------------------------------------------
+ * Kernel launchers. Each one replaces the reference launcher named in its comment, with the
+ * same argument order and meaning, a HIP stream in place of the CUDA stream, and a status code
+ * in place of exceptions.
+ * ---------------------------------------------------------------------------------------- */
+
+/* src/cuda/similarity.cu:345-398 launchSimilarity.
+ * d_scores[q * doc_count + doc] = score of query q against document doc.
+ * d_queries: [batch, dim] float32, or [batch, ceil(dim/32)] packed uint32 words for a BINARY
+ * corpus (bit b of word w = dimension 32w+b, set iff value >= 0). Masked documents (mask byte 0)
+ * score -FLT_MAX. Cosine is a raw dot product (inputs are assumed L2-normalized). L2 scores are
+ * the negated squared distance. Binary scores are (dim - 2*hamming) / dim. */
+int zcgvs_launch_similarity(const void* d_corpus, int dtype, float scale, int doc_count, int dim,
+                            const void* d_queries, int batch, const uint8_t* d_mask, int metric,
+                            float* d_scores, zcgvs_stream_t stream);
+
+/* Same contract as zcgvs_launch_similarity for an int8 corpus in ZCGVS_INT8_PER_VECTOR mode:
+ * d_corpus [doc_count, dim] int8 with d_row_scales [doc_count]; d_queries [batch, dim] int8 with
+ * d_query_scales [batch]. Metric must be COSINE or DOT. No reference counterpart. */
+int zcgvs_launch_similarity_i8i8(const int8_t* d_corpus, const float* d_row_scales,
+                                 int doc_count, int dim, const int8_t* d_queries,
+                                 const float* d_query_scales, int batch, const uint8_t* d_mask,
+                                 int metric, float* d_scores, zcgvs_stream_t stream);
+
+int zcgvs_similarity_query_tile(void);                                /* similarity.cu:309 */
+size_t zcgvs_similarity_shared_bytes(int dtype, int dim, int batch);  /* similarity.cu:337-343 */
+
+/* src/cuda/topk.cu:112-130 sizing helpers. zcgvs_topk_scratch_elements is the per-query element
+ * count of EACH of the four scratch buffers zcgvs_launch_topk takes. */
+int zcgvs_topk_tile_size(void);
+int zcgvs_topk_merge_tile(void);
+int zcgvs_topk_max_k(void);
+int zcgvs_topk_block_count(int doc_count);
+int zcgvs_topk_scratch_elements(int doc_count, int k);
+
+/* src/cuda/topk.cu:132-189 launchTopK. Selects the k best of each [batch, doc_count] score row,
+ * descending, lowest index first on equal scores. Scratch buffers are each
+ * batch * zcgvs_topk_scratch_elements(doc_count, k) elements. k <= zcgvs_topk_max_k() and
+ * k <= doc_count or ZCGVS_ERR_INVALID_ARGUMENT. */
+int zcgvs_launch_topk(const float* d_scores, int doc_count, int k, int batch, int* d_out_indices,
+                      float* d_out_values, float* d_scratch_values_a, int* d_scratch_indices_a,
+                      float* d_scratch_values_b, int* d_scratch_indices_b,
+                      zcgvs_stream_t stream);
+
+/* src/cuda/rescore.cu:83-130 launchGatherRescore / rescoreSharedBytes.
+ * d_values[q * C + slot] = exact score of corpus row d_candidate_indices[q * C + slot] against
+ * float32 query q; an index < 0 or >= doc_count gives -FLT_MAX. BINARY storage is rejected. */
+size_t zcgvs_rescore_shared_bytes(int dim);
+int zcgvs_launch_gather_rescore(const void* d_corpus, int dtype, float scale, int doc_count,
+                                int dim, const float* d_queries, int batch,
+                                const int* d_candidate_indices, int candidate_count, int metric,
+                                float* d_values, zcgvs_stream_t stream);
+
+/* src/cuda/rescore.cu:132-146 launchRemapIndices. */
+int zcgvs_launch_remap_indices(const int* d_candidate_indices, const int* d_local_indices,
+                               int candidate_count, int k, int batch, int* d_out_indices,
+                               zcgvs_stream_t stream);
+
+/* src/cuda/lexical.cu:227-241 launchBm25. Scatter-adds the posting weights of the query's terms
+ * into d_scores (zeroed by the caller). Terms < 0 are skipped, as are documents outside
+ * [0, doc_count); term ids must be below the index's vocabulary size, as in the reference.
+ * Terms are accumulated in slot order, so every document's sum is formed in the same order on
+ * every run. */
+int zcgvs_launch_bm25(const int64_t* d_offsets, const int* d_docs, const float* d_weights,
+                      const int* d_query_terms, int term_count, int doc_count, float* d_scores,
+                      zcgvs_stream_t stream);
+
+/* Batched form of zcgvs_launch_bm25: d_query_terms [batch, term_stride], d_scores
+ * [batch, doc_count] (zeroed by the caller). One launch per term slot instead of one per
+ * (query, slot) as src/search/searcher.cpp:241-249 does. */
+int zcgvs_launch_bm25_batched(const int64_t* d_offsets, const int* d_docs,
+                              const float* d_weights, const int* d_query_terms, int term_stride,
+                              int batch, int doc_count, float* d_scores, zcgvs_stream_t stream);
+
+/* src/cuda/lexical.cu:243-254 launchMaxPositive: *d_max = max(*d_max, max_i values[i]) for
+ * values >= 0 (caller zeroes *d_max). */
+int zcgvs_launch_max_positive(const float* d_values, int count, float* d_max,
+                              zcgvs_stream_t stream);
+
+/* src/cuda/lexical.cu:256-272 launchFuseScores, in place:
+ * dense[i] = weight * dense[i] + (1 - weight) * lexical[i] * (max > 0 ? 1/max : 0). */
+int zcgvs_launch_fuse_scores(float* d_dense, const float* d_lexical, const float* d_lexical_max,
+                             float weight, int count, zcgvs_stream_t stream);
+
+/* src/cuda/convert.cu:332-368 launchConvertF32ToF16 / launchConvertF32ToI8 / launchPackBinary. */
+int zcgvs_launch_convert_f32_to_f16(const float* d_src, void* d_dst_half, size_t count,
+                                    zcgvs_stream_t stream);
+int zcgvs_launch_convert_f32_to_i8(const float* d_src, void* d_dst_int8, size_t count,
+                                   float scale, zcgvs_stream_t stream);
+int zcgvs_launch_pack_binary(const float* d_src, void* d_dst_words, int rows, int dim,
+                             zcgvs_stream_t stream);
+
+/* Per-row symmetric int8 quantization (ZCGVS_INT8_PER_VECTOR): for every row,
+ * s = max|x| / 127 (1.0 for an all-zero row), q = clamp(rint(x * (1/s)), -127, 127).
+ * No reference counterpart; the reciprocal rule is that of src/cuda/convert.cu:25-32. */
+int zcgvs_launch_quantize_rows_i8(const float* d_src, int rows, int dim, int8_t* d_dst,
+                                  float* d_scales, zcgvs_stream_t stream);
+
+/* ------------------------------------------------------------------------------------------
+ * Fused search: the whole device pipeline of src/search/searcher.cpp:209-285 (scan, optional
+ * BM25 fusion, top-k, optional gather rescore + second top-k + remap) without a [batch, N]
+ * score matrix. Only [batch, k] ids and scores are written.
+ * ---------------------------------------------------------------------------------------- */
+typedef struct zcgvs_store_desc {
+    const void* data;          /* [doc_count, row_stride] device rows                         */
+    int64_t doc_count;
+    int dim;
+    int dtype;                 /* enum zcgvs_dtype                                             */
+    float scale;               /* matrix-wide int8 scale (ZCGVS_INT8_REFERENCE)               */
+    const float* row_scales;   /* [doc_count] per-row int8 scales (ZCGVS_INT8_PER_VECTOR)     */
+} zcgvs_store_desc;
+
+typedef struct zcgvs_search_desc {
+    zcgvs_store_desc corpus;   /* primary (scanned) store                                      */
+    zcgvs_store_desc rescore;  /* rescore store; data == NULL disables the rescore stage        */
+    const float* queries;      /* [batch, dim] float32 device queries                           */
+    int batch;
+    int k;                     /* final top-k, 1..zcgvs_topk_max_k()                            */
+    int metric;                /* enum zcgvs_metric                                             */
+    int int8_mode;             /* enum zcgvs_int8_mode (int8 corpus only)                       */
+    const uint8_t* mask;       /* optional [doc_count] allow-mask                               */
+    int rescore_candidates;    /* C; > 0 with rescore.data enables the rescore stage           */
+    /* Hybrid lexical stage (src/search/searcher.cpp:235-259); enabled when query_terms != NULL
+     * and lexical_stride > 0. */
+    const int64_t* lex_offsets;
+    const int* lex_docs;
+    const float* lex_weights;
+    int64_t lex_doc_count;
+    int lex_vocab_size;        /* term ids >= this are skipped                                  */
+    const int* query_terms;    /* [batch, lexical_stride] device term ids, -1 padded           */
+    int lexical_stride;
+    float dense_weight;
+} zcgvs_search_desc;
+
+/* Bytes of device workspace zcgvs_search_topk needs for this descriptor (0 on error). */
+size_t zcgvs_search_workspace_bytes(const zcgvs_search_desc* desc);
+
+/* Runs the fused pipeline. d_out_indices/d_out_values are [batch, k]. The workspace must be
+ * zcgvs_search_workspace_bytes(desc) bytes; its contents need no initialization. Capture safe.
+ * The pipeline bounds its candidate buffers; for inputs whose score order defeats the bound,
+ * the affected queries are flagged in the workspace, and zcgvs_search_overflow reports them
+ * after the stream has completed. */
+int zcgvs_search_topk(const zcgvs_search_desc* desc, void* d_workspace, size_t workspace_bytes,
+                      int* d_out_indices, float* d_out_values, zcgvs_stream_t stream);
+
+/* Device address of the [batch] uint32 overflow flags inside a workspace laid out for `desc`
+ * (non-zero: that query's result is incomplete and must be recomputed exactly, e.g. with
+ * zcgvs_launch_similarity + zcgvs_launch_topk). */
+int zcgvs_search_overflow_flags(const zcgvs_search_desc* desc, void* d_workspace,
+                                uint32_t** d_flags);
+
+/* ------------------------------------------------------------------------------------------
+ * Synthetic data on the device (benchmarks and large parity runs). Row r of a matrix generated
+ * with `seed` depends only on (seed, r): a counter-based splitmix64 stream, Box-Muller in
+ * double precision, rounded to float32, then L2-normalized in float32 in dimension order.
+ * ---------------------------------------------------------------------------------------- */
+int zcgvs_generate_normalized(float* d_out, int64_t rows, int dim, uint64_t seed,
+                              int64_t row_offset, zcgvs_stream_t stream);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* ZCGVS_HIP_H */

@@ -1,0 +1,106 @@
+"""CPU-side checks of the C ABI: the library loads, exports every symbol include/zcgvs_hip.h
+declares, and its host-side argument checks (src/search/searcher.cpp:91-135, topk.cu:146-153,
+similarity.cu:356-358) answer without touching a GPU."""
+
+import re
+from pathlib import Path
+
+import pytest
+
+ROOT = Path(__file__).resolve().parents[1]
+
+
+def declared_symbols():
+    header = (ROOT / "include" / "zcgvs_hip.h").read_text()
+    pattern = r"^(?:const\s+)?[a-z_0-9]+\**\s+\**(zcgvs_[a-z0-9_]+)\s*\("
+    return sorted(set(re.findall(pattern, header, flags=re.MULTILINE)))
+
+
+def test_library_exports_every_declared_symbol(capi):
+    lib = capi.library()
+    names = declared_symbols()
+    assert len(names) >= 50
+    missing = [n for n in names if not hasattr(lib, n)]
+    assert not missing, missing
+    assert set(capi.exported_symbols()) == set(names)
+
+
+def test_version_and_sizing_helpers(capi):
+    lib = capi.library()
+    assert lib.zcgvs_version().decode().startswith("zcgvs-hip")
+    assert lib.zcgvs_topk_max_k() == 1024
+    assert lib.zcgvs_topk_tile_size() == 1024
+    assert lib.zcgvs_similarity_query_tile() == 8
+    assert lib.zcgvs_topk_block_count(5000) == 5
+    assert capi.topk_scratch_elements(5000, 100) >= 5 * 100
+    assert lib.zcgvs_similarity_shared_bytes(capi.F32, 384, 11) == 8 * 384 * 4
+    assert lib.zcgvs_similarity_shared_bytes(capi.BINARY, 384, 3) == 3 * 12 * 4
+    assert lib.zcgvs_rescore_shared_bytes(384) == 384 * 4
+
+
+def test_empty_work_returns_ok_without_a_gpu(capi):
+    # launchers with nothing to do return before touching the device
+    capi.launch_similarity(None, capi.F32, 1.0, 0, 384, None, 1, None, 0, None)
+    capi.launch_topk(None, 0, 10, 1, None, None, None, None, None, None)
+    capi.launch_bm25(None, None, None, None, 0, 100, None)
+
+
+def test_argument_errors_without_a_gpu(capi):
+    with pytest.raises(ValueError, match="exceeds per-tile capacity"):
+        capi.launch_topk(1, 5000, 2000, 1, 1, 1, 1, 1, 1, 1)
+    with pytest.raises(ValueError, match="exceeds candidate count"):
+        capi.launch_topk(1, 50, 100, 1, 1, 1, 1, 1, 1, 1)
+    with pytest.raises(ValueError, match="float32, float16 or int8"):
+        capi.launch_gather_rescore(1, capi.BINARY, 1.0, 10, 32, 1, 1, 1, 1, 0, 1)
+    with pytest.raises(ValueError, match="unknown storage dtype"):
+        capi.launch_similarity(1, 9, 1.0, 10, 32, 1, 1, None, 0, 1)
+    with pytest.raises(ValueError, match="cosine and dot only"):
+        capi.launch_similarity_i8i8(1, 1, 10, 32, 1, 1, 1, None, capi.L2, 1)
+
+
+def _desc(capi, **kw):
+    corpus = capi.store_desc(kw.pop("data", 1 << 20), kw.pop("n", 1000), kw.pop("dim", 64),
+                             kw.pop("dtype", capi.F32), 1.0, kw.pop("row_scales", None))
+    batch = kw.pop("batch", 2)
+    k = kw.pop("k", 10)
+    return capi.search_desc(corpus, 1 << 20, batch, k, **kw)
+
+
+@pytest.mark.parametrize("kw,error,match", [
+    (dict(k=0), ValueError, "k must be positive"),
+    (dict(k=1001), ValueError, "exceeds corpus size"),
+    (dict(n=5000, k=1025), ValueError, "exceeds kernel capacity"),
+    (dict(batch=0), ValueError, "batch must be positive"),
+    (dict(n=2**31), RuntimeError, "exceeds the supported document count"),
+    (dict(metric=7), ValueError, "unknown metric"),
+    (dict(dtype=2, int8_mode=1), ValueError, "row scales"),
+    (dict(dtype=2, int8_mode=1, row_scales=256, metric=2), ValueError, "cosine and dot only"),
+    (dict(rescore_candidates=5), ValueError, "at least k"),
+    (dict(rescore_candidates=2000), ValueError, "exceeds corpus size"),
+    (dict(n=5000, rescore_candidates=2000), ValueError, "exceeds kernel capacity"),
+])
+def test_search_validation_without_a_gpu(capi, kw, error, match):
+    if "rescore_candidates" in kw:
+        kw["rescore"] = capi.store_desc(1 << 21, kw.get("n", 1000), 64, capi.F32)
+    with pytest.raises(error, match=match):
+        capi.search_workspace_bytes(_desc(capi, **kw))
+
+
+def test_search_validation_rescore_store(capi):
+    with pytest.raises(ValueError, match="must not be binary"):
+        capi.search_workspace_bytes(_desc(capi, rescore=capi.store_desc(1 << 21, 1000, 64, capi.BINARY),
+                                          rescore_candidates=100))
+    with pytest.raises(ValueError, match="fewer documents"):
+        capi.search_workspace_bytes(_desc(capi, rescore=capi.store_desc(1 << 21, 999, 64, capi.F32),
+                                          rescore_candidates=100))
+    with pytest.raises(ValueError, match="lexical index holds fewer"):
+        capi.search_workspace_bytes(_desc(capi, query_terms=1 << 22, lexical_stride=4, lex_offsets=1,
+                                          lex_docs=1, lex_weights=1, lex_doc_count=10,
+                                          lex_vocab_size=100))
+
+
+def test_workspace_sizes(capi):
+    # the per-vector int8 configuration: 10M x 768, 256 queries, k = 100
+    size = capi.search_workspace_bytes(_desc(capi, n=10_000_000, dim=768, dtype=capi.I8, batch=256,
+                                             k=100, int8_mode=1, row_scales=256))
+    assert 0 < size < 1 << 30

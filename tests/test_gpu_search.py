@@ -1,0 +1,242 @@
+"""Fused search (zcgvs_search_topk) parity on the GPU against the CPU oracle.
+
+Shapes follow the benchmark configurations at sizes the oracle finishes in seconds; every case
+runs several phases of the scan (the corpus is larger than the first sample), so thresholds,
+segments and merges are all exercised. Integer paths (per-vector int8, Hamming) must match the
+oracle bit for bit, ids and scores; float paths must match ids except at near-ties within the
+float tolerance, and scores within it.
+"""
+
+import numpy as np
+import pytest
+
+import oracle
+from helpers import assert_scores_close, assert_topk_equivalent, float_tolerance, normalized
+
+pytestmark = pytest.mark.gpu
+
+
+def run_search(capi, corpus_dev, n, dim, dtype, queries, k, metric=0, **kw):
+    d_q = capi.DeviceArray.from_host(queries)
+    store = capi.store_desc(corpus_dev, n, dim, dtype, kw.pop("scale", 1.0), kw.pop("row_scales", None))
+    desc = capi.search_desc(store, d_q, queries.shape[0], k, metric, **kw)
+    idx, val, flags = capi.search(desc)
+    assert not flags.any(), "candidate overflow on a random corpus"
+    return idx, val
+
+
+@pytest.mark.parametrize("n,dim,batch,k,metric", [
+    (5183, 384, 1, 10, 0),      # CPU reference configuration (single dense phase)
+    (300_000, 384, 1, 10, 0),   # single-query scan, several phases
+    (200_000, 384, 13, 100, 2), # L2, partial query tile
+])
+def test_fused_f32(gpu, n, dim, batch, k, metric):
+    capi = gpu
+    corpus = normalized(n, dim, 1234)
+    queries = normalized(batch, dim, 4321)
+    idx, val = run_search(capi, capi.DeviceArray.from_host(corpus), n, dim, capi.F32, queries, k, metric)
+    ref = oracle.scores_f32(corpus, queries, metric)
+    assert_topk_equivalent(idx, val, ref, k, float_tolerance(queries, corpus, metric))
+
+
+@pytest.mark.parametrize("batch,k", [(1, 10), (64, 10)])
+def test_fused_f16(gpu, batch, k):
+    capi = gpu
+    n, dim = 250_000, 384
+    corpus = normalized(n, dim, 7)
+    half = oracle.f32_to_f16(corpus)
+    queries = normalized(batch, dim, 8)
+    idx, val = run_search(capi, capi.DeviceArray.from_host(half), n, dim, capi.F16, queries, k)
+    decoded = half.astype(np.float32)
+    ref = oracle.scores_f32(decoded, queries, 0)
+    assert_topk_equivalent(idx, val, ref, k, float_tolerance(queries, decoded, 0))
+
+
+def test_fused_i8_reference_mode_with_mask(gpu):
+    capi = gpu
+    n, dim, batch, k = 150_000, 768, 5, 50
+    corpus = normalized(n, dim, 9)
+    scale = np.float32(1.0 / 127.0)
+    codes = oracle.quantize_i8(corpus, scale)
+    queries = normalized(batch, dim, 10)
+    mask = (np.arange(n) % 3 != 1).astype(np.uint8)
+    idx, val = run_search(capi, capi.DeviceArray.from_host(codes), n, dim, capi.I8, queries, k,
+                          scale=scale, mask=capi.DeviceArray.from_host(mask))
+    decoded = oracle.dequantize_i8(codes, scale)
+    ref = oracle.scores_f32(decoded, queries, 0, mask)
+    assert_topk_equivalent(idx, val, ref, k, float_tolerance(queries, decoded, 0))
+    assert np.all(mask[idx] == 1)
+
+
+@pytest.mark.parametrize("n,dim,batch,k", [
+    (120_000, 768, 256, 100),   # per-vector int8 configuration, MFMA path
+    (70_001, 384, 37, 10),      # partial last tile, partial query group
+    (40_000, 1024, 300, 16),    # two query launches, one n-block per wavefront
+    (30_000, 256, 8, 1024),     # k at capacity
+    (20_000, 96, 9, 25),        # dim outside the MFMA set: VALU int8 x int8 path
+])
+def test_fused_i8i8_bit_exact(gpu, n, dim, batch, k):
+    capi = gpu
+    corpus = normalized(n, dim, n + dim)
+    queries = normalized(batch, dim, batch + 1)
+    codes, rs = oracle.quantize_rows_i8(corpus)
+    qcodes, qs = oracle.quantize_rows_i8(queries)
+    idx, val = run_search(capi, capi.DeviceArray.from_host(codes), n, dim, capi.I8, queries, k,
+                          row_scales=capi.DeviceArray.from_host(rs), int8_mode=capi.INT8_PER_VECTOR)
+    ref = oracle.scores_i8i8(codes, rs, qcodes, qs)
+    assert_topk_equivalent(idx, val, ref, k)
+
+
+def test_fused_i8i8_mask(gpu):
+    capi = gpu
+    n, dim, batch, k = 50_000, 768, 64, 100
+    corpus = normalized(n, dim, 3)
+    queries = normalized(batch, dim, 4)
+    codes, rs = oracle.quantize_rows_i8(corpus)
+    qcodes, qs = oracle.quantize_rows_i8(queries)
+    mask = (np.arange(n) % 2).astype(np.uint8)
+    idx, val = run_search(capi, capi.DeviceArray.from_host(codes), n, dim, capi.I8, queries, k,
+                          row_scales=capi.DeviceArray.from_host(rs), int8_mode=capi.INT8_PER_VECTOR,
+                          mask=capi.DeviceArray.from_host(mask))
+    assert_topk_equivalent(idx, val, oracle.scores_i8i8(codes, rs, qcodes, qs, mask), k)
+
+
+@pytest.mark.parametrize("n,dim,batch,k", [
+    (200_000, 1024, 32, 1000),  # binary configuration shape: massive ties at the top-1000 cut
+    (100_000, 384, 3, 10),
+])
+def test_fused_hamming_bit_exact(gpu, n, dim, batch, k):
+    capi = gpu
+    corpus = normalized(n, dim, 5)
+    bits = oracle.pack_binary(corpus)
+    queries = normalized(batch, dim, 6)
+    idx, val = run_search(capi, capi.DeviceArray.from_host(bits), n, dim, capi.BINARY, queries, k)
+    ref = oracle.scores_hamming(bits, oracle.pack_binary(queries), dim)
+    assert_topk_equivalent(idx, val, ref, k)
+
+
+def test_fused_odd_dim_takes_materialized_path(gpu):
+    capi = gpu
+    n, dim, batch, k = 20_000, 97, 4, 20
+    corpus = normalized(n, dim, 1)
+    half = oracle.f32_to_f16(corpus)
+    queries = normalized(batch, dim, 2)
+    idx, val = run_search(capi, capi.DeviceArray.from_host(half), n, dim, capi.F16, queries, k)
+    decoded = half.astype(np.float32)
+    assert_topk_equivalent(idx, val, oracle.scores_f32(decoded, queries, 0), k,
+                           float_tolerance(queries, decoded, 0))
+
+
+def oracle_rescore_pipeline(coarse_scores, store, queries, c, k):
+    """Coarse top-C, exact rescore of those rows, final top-k by (exact score, corpus id)."""
+    cand, _ = oracle.topk(coarse_scores, c)
+    exact = oracle.rescore(store, queries, cand)
+    out_idx = np.empty((queries.shape[0], k), np.int32)
+    out_val = np.empty((queries.shape[0], k), np.float32)
+    for b in range(queries.shape[0]):
+        order = sorted(range(c), key=lambda i: (-float(exact[b, i]), int(cand[b, i])))[:k]
+        out_idx[b] = cand[b, order]
+        out_val[b] = exact[b, order]
+    return out_idx, out_val
+
+
+def test_rescore_lossless_f16_to_f32(gpu):
+    # tests/cpp/test_pipeline.cu:80-108: an fp16 coarse pass over 512 candidates cannot lose the
+    # true top-10, so the final ids equal the exact CPU top-10.
+    capi = gpu
+    n, dim, k, c, batch = 8192, 256, 10, 512, 4
+    corpus = normalized(n, dim, 31)
+    queries = normalized(batch, dim, 33)
+    half = capi.DeviceArray.from_host(oracle.f32_to_f16(corpus))
+    exact = capi.DeviceArray.from_host(corpus)
+    idx, val = run_search(capi, half, n, dim, capi.F16, queries, k,
+                          rescore=capi.store_desc(exact, n, dim, capi.F32), rescore_candidates=c)
+    ref = oracle.scores_f32(corpus, queries, 0)
+    assert_topk_equivalent(idx, val, ref, k, float_tolerance(queries, corpus, 0))
+
+
+def test_rescore_binary_to_f16(gpu):
+    # binary coarse top-C, exact fp16 rescore, final top-k (the binary+rescore configuration)
+    capi = gpu
+    n, dim, k, c, batch = 100_000, 1024, 10, 1000, 8
+    corpus = normalized(n, dim, 50)
+    queries = normalized(batch, dim, 51)
+    bits = oracle.pack_binary(corpus)
+    half = oracle.f32_to_f16(corpus)
+    idx, val = run_search(capi, capi.DeviceArray.from_host(bits), n, dim, capi.BINARY, queries, k,
+                          rescore=capi.store_desc(capi.DeviceArray.from_host(half), n, dim, capi.F16),
+                          rescore_candidates=c)
+    coarse = oracle.scores_hamming(bits, oracle.pack_binary(queries), dim)
+    decoded = half.astype(np.float32)
+    ref_idx, ref_val = oracle_rescore_pipeline(coarse, decoded, queries, c, k)
+    tol = float_tolerance(queries, decoded, 0)
+    for b in range(batch):
+        for r in range(k):
+            g, e = int(idx[b, r]), int(ref_idx[b, r])
+            if g != e:
+                assert abs(float(ref_val[b, r]) - float(val[b, r])) <= tol[b, g] + tol[b, e]
+            assert abs(float(val[b, r]) - float(oracle.rescore(decoded, queries[b:b + 1],
+                                                               np.array([[g]], np.int32))[0, 0])) <= tol[b, g]
+
+
+def zipf_lexical_index(n, vocab, seed):
+    """Synthetic BM25 index: doc length ~ Poisson(200), terms ~ Zipf(1.1) over ranks 1..V."""
+    rng = np.random.default_rng(seed)
+    lengths = np.maximum(rng.poisson(200, size=n), 1)
+    p = 1.0 / np.arange(1, vocab + 1) ** 1.1
+    p /= p.sum()
+    tokens = rng.choice(vocab, size=int(lengths.sum()), p=p).astype(np.int64)
+    doc_of = np.repeat(np.arange(n, dtype=np.int64), lengths)
+    pair = np.unique(tokens * n + doc_of, return_counts=True)
+    terms, docs = pair[0] // n, pair[0] % n
+    tf = pair[1]
+    df = np.bincount(terms, minlength=vocab)
+    avg = float(lengths.mean())
+    k1, b = 1.2, 0.75
+    norm = k1 * (1.0 - b + b * lengths[docs] / avg)
+    idf = np.log(1.0 + (n - df[terms] + 0.5) / (df[terms] + 0.5))
+    weights = (idf * (tf * (k1 + 1.0)) / (tf + norm)).astype(np.float32)
+    offsets = np.zeros(vocab + 1, np.int64)
+    offsets[1:] = np.cumsum(df)
+    return offsets, docs.astype(np.int32), weights, p
+
+
+def test_hybrid_bm25_fused(gpu):
+    capi = gpu
+    n, vocab, dim, batch, k, w = 60_000, 30_000, 384, 16, 10, 0.5
+    offsets, docs, weights, p = zipf_lexical_index(n, vocab, 12)
+    rng = np.random.default_rng(13)
+    terms = np.stack([rng.choice(vocab, size=8, replace=False, p=p) for _ in range(batch)]).astype(np.int32)
+    corpus = normalized(n, dim, 14)
+    half = oracle.f32_to_f16(corpus)
+    queries = normalized(batch, dim, 15)
+    idx, val = run_search(capi, capi.DeviceArray.from_host(half), n, dim, capi.F16, queries, k,
+                          lex_offsets=capi.DeviceArray.from_host(offsets),
+                          lex_docs=capi.DeviceArray.from_host(docs),
+                          lex_weights=capi.DeviceArray.from_host(weights), lex_doc_count=n,
+                          lex_vocab_size=vocab,
+                          query_terms=capi.DeviceArray.from_host(terms), lexical_stride=8,
+                          dense_weight=w)
+    decoded = half.astype(np.float32)
+    dense = oracle.scores_f32(decoded, queries, 0)
+    fused = np.empty_like(dense)
+    for b in range(batch):
+        lex = oracle.bm25(offsets, docs, weights, terms[b], n)
+        fused[b] = oracle.fuse(dense[b], lex, oracle.max_positive(lex), w)
+    tol = np.float32(w) * float_tolerance(queries, decoded, 0) + 1e-6
+    assert_topk_equivalent(idx, val, fused, k, tol)
+
+
+@pytest.mark.parametrize("bad,match", [
+    (dict(k=0), "k must be positive"),
+    (dict(k=2000), "exceeds kernel capacity"),
+    (dict(batch=0), "batch must be positive"),
+])
+def test_search_validation(gpu, bad, match):
+    capi = gpu
+    store = capi.store_desc(1 << 20, 1000, 64, capi.F32)
+    args = dict(batch=1, k=10)
+    args.update(bad)
+    desc = capi.search_desc(store, 1 << 20, args["batch"], args["k"])
+    with pytest.raises(ValueError, match=match):
+        capi.search_workspace_bytes(desc)

@@ -1,0 +1,256 @@
+"""Pins the CPU oracle before anything is checked against it.
+
+Each check can fail for a plausible mistake in the oracle: the reference's own known answers
+(tests/python/test_formats.py), the reference's own CPU path compiled from its source
+(oracle/_ref, tests/cpp/cpu_reference.hpp), and independent restatements in numpy whose result
+the mathematics fixes (integer matmul, sequential float32 cumulative sums, numpy's IEEE half
+conversion, stable argsort, closed forms).
+"""
+
+import math
+
+import numpy as np
+import pytest
+
+import oracle
+
+RNG = np.random.default_rng(20241201)
+
+
+def normalized(rows, dim, rng=RNG):
+    x = rng.standard_normal((rows, dim)).astype(np.float32)
+    return x / np.linalg.norm(x, axis=1, keepdims=True).astype(np.float32)
+
+
+# ---- known answers of the reference --------------------------------------------------------
+
+def test_pack_binary_known_answer():
+    # tests/python/test_formats.py:36-52: dims 0, 33, 129 set at dim 130 -> words [1, 2, 0, 0, 2]
+    matrix = np.full((1, 130), -1.0, dtype=np.float32)
+    matrix[0, [0, 33, 129]] = 1.0
+    packed = oracle.pack_binary(matrix)
+    assert packed.tolist() == [[1, 2, 0, 0, 2]]
+    assert packed[0, 4] >> 2 == 0  # padding bits stay zero
+
+
+def test_pack_binary_zero_sign_and_nan():
+    # x >= 0 sets the bit: -0.0 sets it, NaN does not (src/cuda/convert.cu:46)
+    packed = oracle.pack_binary(np.array([[-0.0, np.nan, 0.0, -1e-30]], dtype=np.float32))
+    assert packed.tolist() == [[0b0101]]
+
+
+# ---- the reference's own CPU path -----------------------------------------------------------
+
+ref = oracle.ref()
+needs_ref = pytest.mark.skipif(ref is None, reason="reference CPU path was not built here")
+
+
+@needs_ref
+def test_scores_match_reference_cpu_bitwise():
+    import ctypes
+    corpus = normalized(512, 384)
+    query = normalized(1, 384)
+    expected = np.empty(512, dtype=np.float32)
+    ref.ref_cosine_similarity(ctypes.c_void_p(corpus.ctypes.data), 512, 384,
+                              ctypes.c_void_p(query.ctypes.data), ctypes.c_void_p(expected.ctypes.data))
+    got = oracle.scores_f32(corpus, query, oracle.COSINE)[0]
+    assert np.array_equal(got.view(np.uint32), expected.view(np.uint32))
+
+
+@needs_ref
+@pytest.mark.parametrize("quantized", [False, True])
+def test_topk_matches_reference_stable_sort(quantized):
+    import ctypes
+    scores = RNG.uniform(-100, 100, size=5000).astype(np.float32)
+    if quantized:  # heavy ties: only 41 distinct values
+        scores = np.round(scores / 5.0).astype(np.float32)
+    k = 100
+    expected = np.empty(k, dtype=np.int32)
+    ref.ref_topk_indices(ctypes.c_void_p(scores.ctypes.data), scores.size, k,
+                         ctypes.c_void_p(expected.ctypes.data))
+    idx, val = oracle.topk(scores, k)
+    assert idx[0].tolist() == expected.tolist()
+    assert np.array_equal(val[0], scores[expected])
+
+
+@needs_ref
+def test_quantize_dequantize_matches_reference():
+    import ctypes
+    x = RNG.standard_normal(4096).astype(np.float32)
+    # include exact half-way points: (n + 0.5) * scale
+    scale = np.float32(1.0 / 127.0)
+    x[:64] = (np.arange(64, dtype=np.float32) - 32.0 + 0.5) * scale
+    expected = np.empty_like(x)
+    ref.ref_quantize_dequantize_i8(ctypes.c_void_p(x.ctypes.data), x.size, ctypes.c_float(scale),
+                                   ctypes.c_void_p(expected.ctypes.data))
+    got = oracle.quantize_dequantize_i8(x, scale)
+    assert np.array_equal(got.view(np.uint32), expected.view(np.uint32))
+
+
+@needs_ref
+def test_pack_and_hamming_match_reference():
+    import ctypes
+    x = RNG.standard_normal((64, 100)).astype(np.float32)
+    expected = np.empty((64, 4), dtype=np.uint32)
+    ref.ref_pack_binary(ctypes.c_void_p(x.ctypes.data), 64, 100, ctypes.c_void_p(expected.ctypes.data))
+    packed = oracle.pack_binary(x)
+    assert np.array_equal(packed, expected)
+    for i in range(0, 64, 7):
+        h_ref = ref.ref_hamming(ctypes.c_void_p(packed[i].ctypes.data),
+                                ctypes.c_void_p(packed[(i + 1) % 64].ctypes.data), 4)
+        assert oracle.hamming(packed[i], packed[(i + 1) % 64]) == h_ref
+
+
+@needs_ref
+def test_l2_normalize_matches_reference():
+    import ctypes
+    x = RNG.standard_normal((4, 97)).astype(np.float32)
+    got = oracle.l2_normalize(x)
+    for r in range(4):
+        row = x[r].copy()
+        ref.ref_l2_normalize(ctypes.c_void_p(row.ctypes.data), 97)
+        assert np.array_equal(got[r].view(np.uint32), row.view(np.uint32))
+
+
+# ---- independent restatements -------------------------------------------------------------
+
+def _sequential_dot(corpus, query):
+    products = (corpus * query[None, :]).astype(np.float32)
+    return np.cumsum(products, axis=1, dtype=np.float32)[:, -1]
+
+
+@pytest.mark.parametrize("metric", [oracle.COSINE, oracle.DOT, oracle.L2])
+def test_scores_f32_sequential_order(metric):
+    corpus = normalized(300, 97)
+    query = normalized(1, 97)[0]
+    got = oracle.scores_f32(corpus, query, metric)[0]
+    if metric == oracle.L2:
+        diff = (query[None, :] - corpus).astype(np.float32)
+        expected = -np.cumsum((diff * diff).astype(np.float32), axis=1, dtype=np.float32)[:, -1]
+    else:
+        expected = _sequential_dot(corpus, query)
+    assert np.array_equal(got, expected)
+
+
+def test_scores_mask_gives_minus_flt_max():
+    corpus = normalized(50, 16)
+    mask = (np.arange(50) % 2).astype(np.uint8)
+    got = oracle.scores_f32(corpus, corpus[:2], oracle.DOT, mask)
+    assert np.all(got[:, mask == 0] == -np.finfo(np.float32).max)
+    assert np.all(got[:, mask == 1] > -1.1)
+
+
+def test_f16_conversion_matches_ieee():
+    special = np.array([0.0, -0.0, 65504.0, 65520.0, 1e-8, 6.0e-8, 2.0 ** -25, 2.0 ** -24,
+                        3 * 2.0 ** -26, 1.0 + 2.0 ** -11, 1.0 + 3 * 2.0 ** -11, np.inf, -np.inf],
+                       dtype=np.float32)
+    values = np.concatenate([special, RNG.standard_normal(20000).astype(np.float32),
+                             (RNG.standard_normal(5000) * 1e-5).astype(np.float32)])
+    got = oracle.f32_to_f16(values)
+    assert np.array_equal(got.view(np.uint16), values.astype(np.float16).view(np.uint16))
+    back = oracle.f16_to_f32(got)
+    assert np.array_equal(back, got.astype(np.float32))
+
+
+def test_quantize_rows_matches_numpy():
+    x = normalized(64, 768)
+    x[3] = 0.0
+    codes, scales = oracle.quantize_rows_i8(x)
+    peak = np.max(np.abs(x), axis=1)
+    expected_scales = np.where(peak > 0, peak / np.float32(127.0), np.float32(1.0)).astype(np.float32)
+    assert np.array_equal(scales, expected_scales)
+    inverse = (np.float32(1.0) / expected_scales).astype(np.float32)
+    expected = np.clip(np.rint((x * inverse[:, None]).astype(np.float32)), -127, 127).astype(np.int8)
+    assert np.array_equal(codes, expected)
+    assert np.all(np.abs(codes).max(axis=1)[[0, 1, 2]] == 127)
+
+
+def test_i8i8_scores_match_integer_matmul():
+    x = normalized(500, 768)
+    q = normalized(9, 768)
+    codes, rs = oracle.quantize_rows_i8(x)
+    qcodes, qs = oracle.quantize_rows_i8(q)
+    got = oracle.scores_i8i8(codes, rs, qcodes, qs)
+    dot = qcodes.astype(np.int64) @ codes.astype(np.int64).T
+    combined = (qs[:, None] * rs[None, :]).astype(np.float32)
+    expected = (dot.astype(np.float32) * combined).astype(np.float32)
+    assert np.array_equal(got, expected)
+
+
+def test_hamming_closed_forms():
+    x = RNG.standard_normal((3, 1024)).astype(np.float32)
+    packed = oracle.pack_binary(np.concatenate([x, -x]))  # row r+3 is the complement of row r
+    for r in range(3):
+        assert oracle.hamming(packed[r], packed[r]) == 0
+        assert oracle.hamming(packed[r], packed[r + 3]) == 1024
+    scores = oracle.scores_hamming(packed, packed[:1], 1024)[0]
+    assert scores[0] == 1.0 and scores[3] == -1.0
+    h = np.array([oracle.hamming(packed[0], packed[i]) for i in range(6)])
+    assert np.array_equal(scores, ((1024 - 2 * h) / np.float32(1024)).astype(np.float32))
+
+
+@pytest.mark.parametrize("ties", [False, True])
+def test_topk_matches_stable_argsort(ties):
+    scores = RNG.standard_normal((3, 20000)).astype(np.float32)
+    if ties:
+        scores = np.round(scores * 4).astype(np.float32)
+        scores[0, :100] = -0.0  # -0.0 ties with +0.0
+        scores[1, 5:9] = np.nan
+    k = 257
+    idx, val = oracle.topk(scores, k)
+    for b in range(3):
+        key = np.where(np.isnan(scores[b]), np.inf, -scores[b])  # NaN last
+        order = np.argsort(key, kind="stable")[:k]
+        assert idx[b].tolist() == order.tolist()
+
+
+def test_topk_pads_when_k_exceeds_n():
+    idx, val = oracle.topk(np.array([[3.0, 1.0]], dtype=np.float32), 4)
+    assert idx.tolist() == [[0, 1, -1, -1]]
+    assert val[0, 2] == -np.finfo(np.float32).max
+
+
+def test_bm25_weight_formula():
+    for df, tf, length in [(1, 1, 200), (5000, 3, 150), (999999, 12, 400)]:
+        n, avg, k1, b = 1_000_000, 201.5, 1.2, 0.75
+        idf = math.log(1.0 + (n - df + 0.5) / (df + 0.5))
+        expected = np.float32(idf * (tf * (k1 + 1.0)) / (tf + k1 * (1.0 - b + b * length / avg)))
+        assert oracle.bm25_weight(n, df, tf, length, avg, k1, b) == expected
+
+
+def test_bm25_accumulates_in_term_order():
+    offsets = np.array([0, 3, 5, 5, 8], dtype=np.int64)
+    docs = np.array([0, 2, 9, 2, 3, 0, 2, 7], dtype=np.int32)
+    weights = np.array([0.1, 0.2, 0.3, 0.4, 0.5, 0.6, 0.7, 0.8], dtype=np.float32)
+    got = oracle.bm25(offsets, docs, weights, np.array([3, 0, -1, 1], dtype=np.int32), 8)
+    expected = np.zeros(8, dtype=np.float32)
+    for term in (3, 0, 1):
+        for p in range(offsets[term], offsets[term + 1]):
+            if docs[p] < 8:
+                expected[docs[p]] = np.float32(expected[docs[p]] + weights[p])
+    assert np.array_equal(got, expected)
+    assert got[2] == np.float32(np.float32(np.float32(0.7) + np.float32(0.2)) + np.float32(0.4))
+
+
+def test_fuse_formula():
+    dense = RNG.uniform(-1, 1, 1000).astype(np.float32)
+    lexical = RNG.uniform(0, 7, 1000).astype(np.float32)
+    peak = oracle.max_positive(lexical)
+    assert peak == lexical.max()
+    got = oracle.fuse(dense, lexical, peak, 0.6)
+    w = np.float32(0.6)
+    inverse = np.float32(1.0) / np.float32(peak)
+    expected = (w * dense + ((np.float32(1.0) - w) * lexical) * inverse).astype(np.float32)
+    assert np.array_equal(got, expected)
+    assert np.array_equal(oracle.fuse(dense, lexical, 0.0, 0.6), (w * dense).astype(np.float32))
+
+
+def test_rescore_and_remap():
+    store = normalized(100, 64)
+    queries = normalized(2, 64)
+    cand = np.array([[5, -1, 99, 100], [0, 1, 2, 3]], dtype=np.int32)
+    got = oracle.rescore(store, queries, cand)
+    assert got[0, 1] == -np.finfo(np.float32).max and got[0, 3] == -np.finfo(np.float32).max
+    assert got[0, 0] == oracle.scores_f32(store[5:6], queries[0])[0, 0]
+    local = np.array([[2, 0], [3, 7]], dtype=np.int32)
+    assert oracle.remap(cand, local).tolist() == [[99, 5], [3, -1]]

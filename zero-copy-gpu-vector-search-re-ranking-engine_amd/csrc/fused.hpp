@@ -1,0 +1,114 @@
+// Fused scan-and-filter: the pieces shared by the VALU and MFMA scan kernels of the fused search.
+//
+// Phases. The corpus is cut into blocks of `block_rows` rows. A phase visits the blocks whose
+// index is a multiple of `stride` but (when skip > 0) not a multiple of stride * skip, i.e. the
+// phases form a coarse-to-fine interleaved sampling of the whole corpus: phase 0 sees every
+// stride_0-th block, phase 1 every stride_1-th block not yet seen, ..., the last phase every
+// remaining block. Phase 0 writes every key to a fixed slot ("dense"); later phases keep only
+// keys above the per-query threshold, the k-th best key found by the phases before, which is
+// a lower bound of the final k-th best key, so no final hit is ever dropped.
+//
+// Emission. Each workgroup appends its candidates for query q to its own segment
+// seg[(wg * batch + q) << seg_log2 ...], counting with LDS atomics (no global atomics, so the
+// scan's memory pipeline never waits on a returning atomic), and stores its per-query counts
+// when it finishes. A count above the segment capacity is reported as overflow by the merge.
+#pragma once
+
+#include "common.hpp"
+
+namespace zcgvs_hip {
+
+struct PhaseArgs {
+    long long stride = 1;
+    long long skip = 0;
+    long long items = 0;
+    int dense = 0;
+    int block_rows = 64;
+};
+
+struct EmitArgs {
+    const std::uint64_t* tau = nullptr;  // [batch] thresholds (ignored for dense phases)
+    std::uint64_t* dense = nullptr;      // [batch, dense_stride]
+    long long dense_stride = 0;
+    std::uint64_t* seg = nullptr;        // [n_wg, batch, 1 << seg_log2]
+    std::uint32_t* seg_count = nullptr;  // [n_wg, batch]
+    int seg_log2 = 0;
+};
+
+// First block of work item j of a phase.
+__device__ __forceinline__ long long phaseBlock(long long j, long long stride, long long skip) {
+    if (skip == 0) {
+        return j * stride;
+    }
+    return (j + j / (skip - 1) + 1) * stride;
+}
+
+// Work items of a phase over `blocks` blocks.
+inline long long phaseItems(long long blocks, long long stride, long long skip) {
+    const long long multiples = (blocks + stride - 1) / stride;
+    if (skip == 0) {
+        return multiples;
+    }
+    return multiples - (multiples + skip - 1) / skip;
+}
+
+// Appends `key` to query q's segment of this workgroup (lds_count: this workgroup's per-query
+// counts for the launch's query range, indexed by q - q_offset).
+__device__ __forceinline__ void appendCandidate(const EmitArgs& emit, std::uint32_t* lds_count,
+                                                int q, int q_offset, int batch,
+                                                std::uint64_t key) {
+    const std::uint32_t slot = atomicAdd(&lds_count[q - q_offset], 1u);
+    if (slot < (1u << emit.seg_log2)) {
+        emit.seg[((static_cast<std::size_t>(blockIdx.x) * batch + q) << emit.seg_log2) + slot] = key;
+    }
+}
+
+// Hybrid fusion of src/cuda/lexical.cu:67-74 for one (query, row): w * dense + ((1 - w) * lex) *
+// inverse, as separate IEEE operations in the reference's operand order.
+__device__ __forceinline__ float fuseHybrid(float dense, float lexical, float weight,
+                                            float inverse) {
+#pragma clang fp contract(off)
+    const float a = weight * dense;
+    const float b = (1.0f - weight) * lexical;
+    const float c = b * inverse;
+    return a + c;
+}
+
+// ---- internal launch interfaces ------------------------------------------------------------
+
+struct ScanArgs {
+    const void* corpus = nullptr;
+    long long doc_count = 0;
+    int dim = 0;
+    int dtype = 0;               // zcgvs_dtype; I8 with row_scales != nullptr = per-vector mode
+    float scale = 1.0f;
+    const float* row_scales = nullptr;
+    const void* queries = nullptr;  // f32 [batch, dim] | packed words [batch, W] | int8 [batch, dim]
+    const float* query_scales = nullptr;
+    int batch = 0;
+    int metric = 0;
+    const std::uint8_t* mask = nullptr;
+    const float* lexical = nullptr;      // [batch, doc_count] or null
+    const float* lexical_max = nullptr;  // [batch]
+    float dense_weight = 1.0f;
+};
+
+// Rows per work item and workgroup count used by the VALU scan for this corpus/batch.
+struct ValuShape {
+    int lanes = 1;
+    int block_rows = 64;
+    int workgroups = 1;
+    int query_group = 1;  // queries staged per launch
+};
+ValuShape valuShape(const ScanArgs& scan);
+int launchValuScan(const ScanArgs& scan, const PhaseArgs& phase, const EmitArgs& emit,
+                   int workgroups, hipStream_t stream);
+
+// The int8 x int8 MFMA scan (per-vector mode, dim in {256, 384, 512, 768, 1024}).
+bool mfmaSupported(const ScanArgs& scan);
+constexpr int kMfmaBlockRows = 64;
+int mfmaWorkgroups();
+int launchMfmaScan(const ScanArgs& scan, const PhaseArgs& phase, const EmitArgs& emit,
+                   int workgroups, hipStream_t stream);
+
+}  // namespace zcgvs_hip

@@ -1,0 +1,26 @@
+// Internal interfaces between the fused search and the rescore / lexical / conversion kernels.
+#pragma once
+
+#include "common.hpp"
+
+namespace zcgvs_hip {
+
+// Exact score of the corpus row named by each candidate key ([batch, candidate_count] selection
+// keys; key 0 = no candidate) against float32 query q, written back as (score, corpus id) keys
+// (0 for "no candidate").
+int launchRescoreKeys(const void* corpus, int dtype, float scale, int doc_count, int dim,
+                      const float* queries, int batch, const std::uint64_t* candidate_keys,
+                      int candidate_count, int metric, std::uint64_t* out_keys,
+                      hipStream_t stream);
+
+// BM25 over the CSR index for [batch, term_stride] term slots into lexical [batch, doc_count]
+// (zeroed first by this call), then the per-query maximum into lexical_max [batch].
+int launchLexicalScores(const std::int64_t* offsets, const int* docs, const float* weights,
+                        int vocab_size, const int* query_terms, int term_stride, int batch,
+                        int doc_count, float* lexical, float* lexical_max, hipStream_t stream);
+
+// Per-row int8 quantization used for the queries of the per-vector int8 mode.
+int launchQuantizeRows(const float* src, int rows, int dim, std::int8_t* dst, float* scales,
+                       hipStream_t stream);
+
+}  // namespace zcgvs_hip

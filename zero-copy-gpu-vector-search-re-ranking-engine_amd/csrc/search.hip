@@ -1,0 +1,574 @@
+// Fused search pipeline (zcgvs_search_topk): the device stages of src/search/searcher.cpp:209-285
+// without the [batch, N] score matrix.
+//
+//   1. query preparation: sign packing for a binary corpus (searcher.cpp:215-218), per-row int8
+//      quantization for the per-vector int8 mode;
+//   2. optional BM25 scores and their per-query maximum (hybrid, searcher.cpp:235-259);
+//   3. phased scan-and-filter (fused.hpp) with a per-query merge after every phase; the scan
+//      selects `width` = rescore_candidates (rescore on) or k keys per query;
+//   4. optional exact gather rescore of those candidates and a final top-k, whose keys carry the
+//      corpus id, which subsumes the reference's remap (searcher.cpp:261-278).
+//
+// Shapes the fused kernels do not take (rows that are not whole 16-byte chunks, very wide rows)
+// run the materialized launchers instead: zcgvs_launch_similarity into a workspace score matrix,
+// then zcgvs_launch_topk, exactly the reference's stage order.
+#include <hip/hip_runtime.h>
+
+#include <algorithm>
+#include <string>
+#include <vector>
+
+#include "common.hpp"
+#include "fused.hpp"
+#include "rescore.hpp"
+#include "select.hpp"
+
+namespace zcgvs_hip {
+
+bool valuSupported(const ScanArgs& scan);
+
+namespace {
+
+constexpr std::size_t kAlign = 256;
+constexpr long long kPhaseGrowth = 64;
+
+std::size_t alignUp(std::size_t value) { return (value + kAlign - 1) / kAlign * kAlign; }
+
+int ceilLog2(long long value) {
+    int bits = 0;
+    while ((1LL << bits) < value) {
+        ++bits;
+    }
+    return bits;
+}
+
+struct Layout {
+    std::size_t total = 0;
+    std::size_t add(std::size_t bytes) {
+        const std::size_t offset = total;
+        total += alignUp(std::max<std::size_t>(bytes, 1));
+        return offset;
+    }
+};
+
+struct Plan {
+    int status = ZCGVS_OK;
+    std::string error;
+
+    bool binary = false;
+    bool per_vector = false;
+    bool hybrid = false;
+    bool rescore = false;
+    bool materialized = false;
+    bool use_mfma = false;
+    int width = 0;  // keys selected by the scan stage
+    int block_rows = 64;
+    int workgroups = 1;
+    int seg_log2 = 5;
+    long long dense_stride = 0;
+    std::vector<PhaseArgs> phases;
+
+    // workspace offsets
+    std::size_t qbits = 0, qi8 = 0, qscale = 0, lex = 0, lexmax = 0, dense = 0, seg = 0,
+                segcnt = 0, keys = 0, tau = 0, overflow = 0, rescored = 0, scores = 0, lexmat = 0,
+                topk_a = 0, topk_b = 0, topk_c = 0, topk_d = 0, cand_idx = 0, cand_val = 0,
+                local_idx = 0, rescore_val = 0, lexmax_m = 0;
+    std::size_t total = 0;
+};
+
+Plan fail(int status, const std::string& message) {
+    Plan plan;
+    plan.status = status;
+    plan.error = message;
+    return plan;
+}
+
+// Argument checks of src/search/searcher.cpp:91-135, plus the descriptor's own consistency.
+Plan validate(const zcgvs_search_desc& d) {
+    const zcgvs_store_desc& c = d.corpus;
+    if (c.data == nullptr || d.queries == nullptr) {
+        return fail(ZCGVS_ERR_INVALID_ARGUMENT, "zcgvs: corpus and queries must be device pointers");
+    }
+    if (c.dim <= 0) {
+        return fail(ZCGVS_ERR_INVALID_ARGUMENT, "zcgvs: corpus dim must be positive");
+    }
+    if (!validDtype(c.dtype)) {
+        return fail(ZCGVS_ERR_INVALID_ARGUMENT, "zcgvs: unknown corpus dtype");
+    }
+    if (!validMetric(d.metric)) {
+        return fail(ZCGVS_ERR_INVALID_ARGUMENT, "zcgvs: unknown metric");
+    }
+    if (d.batch <= 0) {
+        return fail(ZCGVS_ERR_INVALID_ARGUMENT, "zcgvs: batch must be positive");
+    }
+    if (d.k <= 0) {
+        return fail(ZCGVS_ERR_INVALID_ARGUMENT, "zcgvs: k must be positive");
+    }
+    if (c.doc_count > static_cast<std::int64_t>(INT32_MAX)) {
+        return fail(ZCGVS_ERR_RUNTIME, "zcgvs: corpus exceeds the supported document count");
+    }
+    if (c.doc_count <= 0) {
+        return fail(ZCGVS_ERR_INVALID_ARGUMENT, "zcgvs: corpus is empty");
+    }
+    if (d.k > c.doc_count) {
+        return fail(ZCGVS_ERR_INVALID_ARGUMENT, "zcgvs: k=" + std::to_string(d.k) +
+                                                    " exceeds corpus size " +
+                                                    std::to_string(c.doc_count));
+    }
+    if (d.k > kMaxK) {
+        return fail(ZCGVS_ERR_INVALID_ARGUMENT, "zcgvs: k=" + std::to_string(d.k) +
+                                                    " exceeds kernel capacity " +
+                                                    std::to_string(kMaxK));
+    }
+    Plan plan;
+    plan.binary = c.dtype == ZCGVS_DTYPE_BINARY;
+    plan.per_vector = c.dtype == ZCGVS_DTYPE_I8 && d.int8_mode == ZCGVS_INT8_PER_VECTOR;
+    if (c.dtype == ZCGVS_DTYPE_I8 && d.int8_mode != ZCGVS_INT8_REFERENCE &&
+        d.int8_mode != ZCGVS_INT8_PER_VECTOR) {
+        return fail(ZCGVS_ERR_INVALID_ARGUMENT, "zcgvs: unknown int8 mode");
+    }
+    if (plan.per_vector) {
+        if (c.row_scales == nullptr) {
+            return fail(ZCGVS_ERR_INVALID_ARGUMENT,
+                        "zcgvs: per-vector int8 mode needs the corpus row scales");
+        }
+        if (d.metric == ZCGVS_METRIC_L2) {
+            return fail(ZCGVS_ERR_INVALID_ARGUMENT,
+                        "zcgvs: per-vector int8 mode supports cosine and dot only");
+        }
+    }
+    plan.rescore = d.rescore.data != nullptr && d.rescore_candidates > 0;
+    if (plan.rescore) {
+        if (d.rescore_candidates < d.k) {
+            return fail(ZCGVS_ERR_INVALID_ARGUMENT, "zcgvs: rescore_candidates must be at least k");
+        }
+        if (d.rescore_candidates > c.doc_count) {
+            return fail(ZCGVS_ERR_INVALID_ARGUMENT, "zcgvs: rescore_candidates exceeds corpus size");
+        }
+        if (d.rescore_candidates > kMaxK) {
+            return fail(ZCGVS_ERR_INVALID_ARGUMENT,
+                        "zcgvs: rescore_candidates=" + std::to_string(d.rescore_candidates) +
+                            " exceeds kernel capacity " + std::to_string(kMaxK));
+        }
+        if (d.rescore.dtype == ZCGVS_DTYPE_BINARY || !validDtype(d.rescore.dtype)) {
+            return fail(ZCGVS_ERR_INVALID_ARGUMENT, "zcgvs: rescore store must not be binary");
+        }
+        if (d.rescore.dim != c.dim) {
+            return fail(ZCGVS_ERR_INVALID_ARGUMENT, "zcgvs: rescore store dim does not match the corpus");
+        }
+        if (d.rescore.doc_count < c.doc_count) {
+            return fail(ZCGVS_ERR_INVALID_ARGUMENT,
+                        "zcgvs: rescore store holds fewer documents than the corpus");
+        }
+    }
+    plan.hybrid = d.query_terms != nullptr && d.lexical_stride > 0;
+    if (plan.hybrid) {
+        if (d.lex_offsets == nullptr || d.lex_docs == nullptr || d.lex_weights == nullptr) {
+            return fail(ZCGVS_ERR_INVALID_ARGUMENT, "zcgvs: lexical index pointers are null");
+        }
+        if (d.lex_vocab_size <= 0) {
+            return fail(ZCGVS_ERR_INVALID_ARGUMENT, "zcgvs: lexical vocabulary size must be positive");
+        }
+        if (d.lex_doc_count < c.doc_count) {
+            return fail(ZCGVS_ERR_INVALID_ARGUMENT,
+                        "zcgvs: lexical index holds fewer documents than the corpus");
+        }
+    }
+    return plan;
+}
+
+ScanArgs scanArgsOf(const zcgvs_search_desc& d, const Plan& plan, std::uint8_t* ws) {
+    ScanArgs scan;
+    scan.corpus = d.corpus.data;
+    scan.doc_count = d.corpus.doc_count;
+    scan.dim = d.corpus.dim;
+    scan.dtype = d.corpus.dtype;
+    scan.scale = d.corpus.scale;
+    scan.batch = d.batch;
+    scan.metric = d.metric;
+    scan.mask = d.mask;
+    scan.queries = d.queries;
+    if (plan.per_vector) {
+        scan.row_scales = d.corpus.row_scales;
+        scan.queries = ws != nullptr ? ws + plan.qi8 : nullptr;
+        scan.query_scales = ws != nullptr ? reinterpret_cast<const float*>(ws + plan.qscale) : nullptr;
+    }
+    if (plan.binary) {
+        scan.queries = ws != nullptr ? ws + plan.qbits : nullptr;
+    }
+    if (plan.hybrid) {
+        scan.lexical = ws != nullptr ? reinterpret_cast<const float*>(ws + plan.lex) : nullptr;
+        scan.lexical_max = ws != nullptr ? reinterpret_cast<const float*>(ws + plan.lexmax) : nullptr;
+        scan.dense_weight = d.dense_weight;
+    }
+    return scan;
+}
+
+Plan makePlan(const zcgvs_search_desc& d) {
+    Plan plan = validate(d);
+    if (plan.status != ZCGVS_OK) {
+        return plan;
+    }
+    const long long n = d.corpus.doc_count;
+    const int batch = d.batch;
+    const int dim = d.corpus.dim;
+    plan.width = plan.rescore ? d.rescore_candidates : d.k;
+
+    // Probe the scan engine with a dummy aligned pointer set (alignment is re-checked at run).
+    ScanArgs probe = scanArgsOf(d, plan, nullptr);
+    if (plan.per_vector || plan.binary) {
+        probe.queries = reinterpret_cast<const void*>(static_cast<std::uintptr_t>(kAlign));
+    }
+    if (plan.per_vector) {
+        probe.query_scales = reinterpret_cast<const float*>(static_cast<std::uintptr_t>(kAlign));
+    }
+    if (plan.hybrid) {
+        probe.lexical = reinterpret_cast<const float*>(static_cast<std::uintptr_t>(kAlign));
+    }
+    plan.use_mfma = mfmaSupported(probe);
+    plan.materialized = !plan.use_mfma && !valuSupported(probe);
+    if (plan.per_vector && plan.materialized && dim % 16 != 0) {
+        return fail(ZCGVS_ERR_INVALID_ARGUMENT,
+                    "zcgvs: per-vector int8 mode needs dim % 16 == 0 and a 16-byte aligned corpus");
+    }
+
+    Layout layout;
+    if (plan.binary) {
+        plan.qbits = layout.add(static_cast<std::size_t>(batch) * binaryWords(dim) * 4);
+    }
+    if (plan.per_vector) {
+        plan.qi8 = layout.add(static_cast<std::size_t>(batch) * dim);
+        plan.qscale = layout.add(static_cast<std::size_t>(batch) * 4);
+    }
+    plan.overflow = layout.add(static_cast<std::size_t>(batch) * 4);
+
+    if (plan.materialized) {
+        // Reference-order pipeline over a workspace score matrix.
+        const std::size_t elements = static_cast<std::size_t>(batch) * n;
+        plan.scores = layout.add(elements * 4);
+        if (plan.hybrid) {
+            plan.lexmat = layout.add(elements * 4);
+            plan.lexmax_m = layout.add(static_cast<std::size_t>(batch) * 4);
+        }
+        const std::size_t scratch = static_cast<std::size_t>(batch) *
+                                    zcgvs_topk_scratch_elements(static_cast<int>(n), plan.width) * 4;
+        plan.topk_a = layout.add(scratch);
+        plan.topk_b = layout.add(scratch);
+        plan.topk_c = layout.add(scratch);
+        plan.topk_d = layout.add(scratch);
+        if (plan.rescore) {
+            const std::size_t cands = static_cast<std::size_t>(batch) * plan.width;
+            plan.cand_idx = layout.add(cands * 4);
+            plan.cand_val = layout.add(cands * 4);
+            plan.rescore_val = layout.add(cands * 4);
+            plan.local_idx = layout.add(static_cast<std::size_t>(batch) * d.k * 4);
+            // C candidates per query need their own top-k scratch.
+            const std::size_t s2 = static_cast<std::size_t>(batch) *
+                                   zcgvs_topk_scratch_elements(plan.width, d.k) * 4;
+            if (s2 > scratch) {
+                return fail(ZCGVS_ERR_RUNTIME, "zcgvs: rescore scratch sizing");
+            }
+        }
+        plan.total = layout.total;
+        return plan;
+    }
+
+    if (plan.use_mfma) {
+        plan.block_rows = kMfmaBlockRows;
+        plan.workgroups = mfmaWorkgroups();
+    } else {
+        const ValuShape shape = valuShape(probe);
+        plan.block_rows = shape.block_rows;
+        plan.workgroups = shape.workgroups;
+    }
+
+    // Phase schedule: phase 0 samples ~max(16 * width, 4096) rows densely; each later phase
+    // visits up to kPhaseGrowth times as many blocks as all phases before it.
+    const long long blocks = (n + plan.block_rows - 1) / plan.block_rows;
+    const long long target_rows = std::max<long long>(16LL * plan.width, 4096);
+    const long long blocks0 = (target_rows + plan.block_rows - 1) / plan.block_rows;
+    long long stride = 1;
+    while ((blocks + 2 * stride - 1) / (2 * stride) >= blocks0) {
+        stride *= 2;
+    }
+    PhaseArgs first;
+    first.stride = stride;
+    first.skip = 0;
+    first.items = phaseItems(blocks, stride, 0);
+    first.dense = 1;
+    first.block_rows = plan.block_rows;
+    plan.phases.push_back(first);
+    long long growth = 1;
+    while (stride > 1) {
+        const long long next = std::max<long long>(1, stride / kPhaseGrowth);
+        PhaseArgs phase;
+        phase.stride = next;
+        phase.skip = stride / next;
+        phase.items = phaseItems(blocks, next, phase.skip);
+        phase.dense = 0;
+        phase.block_rows = plan.block_rows;
+        growth = std::max(growth, phase.skip);
+        plan.phases.push_back(phase);
+        stride = next;
+    }
+    plan.dense_stride = first.items * plan.block_rows;
+    // Segment capacity: 4x the expected candidates per (workgroup, query) of the widest phase.
+    const long long expected = (static_cast<long long>(plan.width) * growth) / plan.workgroups;
+    plan.seg_log2 = std::max(5, ceilLog2(4 * expected + 16));
+
+    if (plan.hybrid) {
+        plan.lex = layout.add(static_cast<std::size_t>(batch) * n * 4);
+        plan.lexmax = layout.add(static_cast<std::size_t>(batch) * 4);
+    }
+    plan.dense = layout.add(static_cast<std::size_t>(batch) * plan.dense_stride * 8);
+    if (plan.phases.size() > 1) {
+        plan.seg = layout.add((static_cast<std::size_t>(plan.workgroups) * batch << plan.seg_log2) * 8);
+        plan.segcnt = layout.add(static_cast<std::size_t>(plan.workgroups) * batch * 4);
+    }
+    plan.keys = layout.add(static_cast<std::size_t>(batch) * plan.width * 8);
+    plan.tau = layout.add(static_cast<std::size_t>(batch) * 8);
+    if (plan.rescore) {
+        plan.rescored = layout.add(static_cast<std::size_t>(batch) * plan.width * 8);
+    }
+    plan.total = layout.total;
+    return plan;
+}
+
+template <typename T>
+T* at(std::uint8_t* ws, std::size_t offset) {
+    return reinterpret_cast<T*>(ws + offset);
+}
+
+int runMaterialized(const zcgvs_search_desc& d, const Plan& plan, std::uint8_t* ws, int* out_idx,
+                    float* out_val, hipStream_t stream) {
+    const int n = static_cast<int>(d.corpus.doc_count);
+    const int batch = d.batch;
+    float* scores = at<float>(ws, plan.scores);
+    int status = ZCGVS_OK;
+    zcgvs_stream_t s = stream;
+    if (plan.per_vector) {
+        status = zcgvs_launch_similarity_i8i8(static_cast<const std::int8_t*>(d.corpus.data),
+                                              d.corpus.row_scales, n, d.corpus.dim,
+                                              at<std::int8_t>(ws, plan.qi8),
+                                              at<float>(ws, plan.qscale), batch, d.mask, d.metric,
+                                              scores, s);
+    } else {
+        const void* queries = plan.binary ? static_cast<const void*>(ws + plan.qbits)
+                                          : static_cast<const void*>(d.queries);
+        status = zcgvs_launch_similarity(d.corpus.data, d.corpus.dtype, d.corpus.scale, n,
+                                         d.corpus.dim, queries, batch, d.mask, d.metric, scores, s);
+    }
+    if (status != ZCGVS_OK) {
+        return status;
+    }
+    if (plan.hybrid) {
+        float* lexical = at<float>(ws, plan.lexmat);
+        float* lexmax = at<float>(ws, plan.lexmax_m);
+        status = launchLexicalScores(d.lex_offsets, d.lex_docs, d.lex_weights, d.lex_vocab_size, d.query_terms,
+                                     d.lexical_stride, batch, n, lexical, lexmax, stream);
+        if (status != ZCGVS_OK) {
+            return status;
+        }
+        for (int q = 0; q < batch; ++q) {
+            status = zcgvs_launch_fuse_scores(scores + static_cast<std::size_t>(q) * n,
+                                              lexical + static_cast<std::size_t>(q) * n,
+                                              lexmax + q, d.dense_weight, n, s);
+            if (status != ZCGVS_OK) {
+                return status;
+            }
+        }
+    }
+    float* sa = at<float>(ws, plan.topk_a);
+    int* ia = at<int>(ws, plan.topk_b);
+    float* sb = at<float>(ws, plan.topk_c);
+    int* ib = at<int>(ws, plan.topk_d);
+    if (!plan.rescore) {
+        return zcgvs_launch_topk(scores, n, d.k, batch, out_idx, out_val, sa, ia, sb, ib, s);
+    }
+    const int c = plan.width;
+    int* cand_idx = at<int>(ws, plan.cand_idx);
+    float* cand_val = at<float>(ws, plan.cand_val);
+    float* rescored = at<float>(ws, plan.rescore_val);
+    int* local = at<int>(ws, plan.local_idx);
+    status = zcgvs_launch_topk(scores, n, c, batch, cand_idx, cand_val, sa, ia, sb, ib, s);
+    if (status != ZCGVS_OK) {
+        return status;
+    }
+    status = zcgvs_launch_gather_rescore(d.rescore.data, d.rescore.dtype, d.rescore.scale,
+                                         static_cast<int>(d.rescore.doc_count), d.corpus.dim,
+                                         d.queries, batch, cand_idx, c, d.metric, rescored, s);
+    if (status != ZCGVS_OK) {
+        return status;
+    }
+    status = zcgvs_launch_topk(rescored, c, d.k, batch, local, out_val, sa, ia, sb, ib, s);
+    if (status != ZCGVS_OK) {
+        return status;
+    }
+    return zcgvs_launch_remap_indices(cand_idx, local, c, d.k, batch, out_idx, s);
+}
+
+__global__ void zeroWordsKernel(std::uint32_t* __restrict__ dst, std::size_t count) {
+    const std::size_t stride = static_cast<std::size_t>(gridDim.x) * blockDim.x;
+    for (std::size_t i = static_cast<std::size_t>(blockIdx.x) * blockDim.x + threadIdx.x;
+         i < count; i += stride) {
+        dst[i] = 0u;
+    }
+}
+
+}  // namespace
+
+}  // namespace zcgvs_hip
+
+using namespace zcgvs_hip;
+
+extern "C" {
+
+std::size_t zcgvs_search_workspace_bytes(const zcgvs_search_desc* desc) {
+    if (desc == nullptr) {
+        setError(ZCGVS_ERR_INVALID_ARGUMENT, "zcgvs: descriptor must not be null");
+        return 0;
+    }
+    const Plan plan = makePlan(*desc);
+    if (plan.status != ZCGVS_OK) {
+        setError(plan.status, plan.error);
+        return 0;
+    }
+    clearError();
+    return plan.total;
+}
+
+int zcgvs_search_overflow_flags(const zcgvs_search_desc* desc, void* d_workspace,
+                                std::uint32_t** d_flags) {
+    if (desc == nullptr || d_flags == nullptr || d_workspace == nullptr) {
+        return setError(ZCGVS_ERR_INVALID_ARGUMENT, "zcgvs: null argument");
+    }
+    const Plan plan = makePlan(*desc);
+    if (plan.status != ZCGVS_OK) {
+        return setError(plan.status, plan.error);
+    }
+    *d_flags = reinterpret_cast<std::uint32_t*>(static_cast<std::uint8_t*>(d_workspace) + plan.overflow);
+    return clearError();
+}
+
+int zcgvs_search_topk(const zcgvs_search_desc* desc, void* d_workspace, std::size_t workspace_bytes,
+                      int* d_out_indices, float* d_out_values, zcgvs_stream_t stream) {
+    if (desc == nullptr) {
+        return setError(ZCGVS_ERR_INVALID_ARGUMENT, "zcgvs: descriptor must not be null");
+    }
+    const zcgvs_search_desc& d = *desc;
+    const Plan plan = makePlan(d);
+    if (plan.status != ZCGVS_OK) {
+        return setError(plan.status, plan.error);
+    }
+    if (d_workspace == nullptr || workspace_bytes < plan.total) {
+        return setError(ZCGVS_ERR_INVALID_ARGUMENT,
+                        "zcgvs: workspace of " + std::to_string(workspace_bytes) +
+                            " bytes is smaller than the " + std::to_string(plan.total) + " needed");
+    }
+    if (d_out_indices == nullptr || d_out_values == nullptr) {
+        return setError(ZCGVS_ERR_INVALID_ARGUMENT, "zcgvs: output pointers must not be null");
+    }
+    std::uint8_t* ws = static_cast<std::uint8_t*>(d_workspace);
+    const hipStream_t s = toStream(stream);
+    const int batch = d.batch;
+    const int dim = d.corpus.dim;
+    int status = ZCGVS_OK;
+
+    zeroWordsKernel<<<1, 256, 0, s>>>(at<std::uint32_t>(ws, plan.overflow), static_cast<std::size_t>(batch));
+    ZCGVS_LAUNCH_CHECK("zero flags");
+
+    // 1. queries
+    if (plan.binary) {
+        status = zcgvs_launch_pack_binary(d.queries, ws + plan.qbits, batch, dim, stream);
+    } else if (plan.per_vector) {
+        status = launchQuantizeRows(d.queries, batch, dim, at<std::int8_t>(ws, plan.qi8),
+                                    at<float>(ws, plan.qscale), s);
+    }
+    if (status != ZCGVS_OK) {
+        return status;
+    }
+
+    if (plan.materialized) {
+        status = runMaterialized(d, plan, ws, d_out_indices, d_out_values, s);
+        return status == ZCGVS_OK ? clearError() : status;
+    }
+
+    // 2. lexical scores
+    if (plan.hybrid) {
+        status = launchLexicalScores(d.lex_offsets, d.lex_docs, d.lex_weights, d.lex_vocab_size, d.query_terms,
+                                     d.lexical_stride, batch, static_cast<int>(d.corpus.doc_count),
+                                     at<float>(ws, plan.lex), at<float>(ws, plan.lexmax), s);
+        if (status != ZCGVS_OK) {
+            return status;
+        }
+    }
+
+    // 3. phased scan + merge
+    const ScanArgs scan = scanArgsOf(d, plan, ws);
+    if (plan.use_mfma && !mfmaSupported(scan)) {
+        return setError(ZCGVS_ERR_INVALID_ARGUMENT, "zcgvs: corpus or queries are not 16-byte aligned");
+    }
+    EmitArgs emit;
+    emit.tau = at<std::uint64_t>(ws, plan.tau);
+    emit.dense = at<std::uint64_t>(ws, plan.dense);
+    emit.dense_stride = plan.dense_stride;
+    emit.seg = plan.phases.size() > 1 ? at<std::uint64_t>(ws, plan.seg) : nullptr;
+    emit.seg_count = plan.phases.size() > 1 ? at<std::uint32_t>(ws, plan.segcnt) : nullptr;
+    emit.seg_log2 = plan.seg_log2;
+    std::uint64_t* keys = at<std::uint64_t>(ws, plan.keys);
+    std::uint64_t* tau = at<std::uint64_t>(ws, plan.tau);
+    std::uint32_t* overflow = at<std::uint32_t>(ws, plan.overflow);
+
+    for (std::size_t p = 0; p < plan.phases.size(); ++p) {
+        const PhaseArgs& phase = plan.phases[p];
+        status = plan.use_mfma ? launchMfmaScan(scan, phase, emit, plan.workgroups, s)
+                               : launchValuScan(scan, phase, emit, plan.workgroups, s);
+        if (status != ZCGVS_OK) {
+            return status;
+        }
+        MergeInputs in;
+        if (p == 0) {
+            in.dense = emit.dense;
+            in.n_dense = phase.items * phase.block_rows;
+            in.dense_stride = plan.dense_stride;
+        } else {
+            in.prev = keys;
+            in.k_prev = plan.width;
+            in.seg = emit.seg;
+            in.seg_count = emit.seg_count;
+            in.n_seg = plan.workgroups;
+            in.seg_log2 = plan.seg_log2;
+        }
+        const bool last = p + 1 == plan.phases.size();
+        const bool write_out = last && !plan.rescore;
+        status = launchSelectMerge(in, plan.width, batch, keys, tau, overflow,
+                                   write_out ? d_out_indices : nullptr,
+                                   write_out ? d_out_values : nullptr, s);
+        if (status != ZCGVS_OK) {
+            return status;
+        }
+    }
+
+    // 4. rescore
+    if (plan.rescore) {
+        std::uint64_t* rescored = at<std::uint64_t>(ws, plan.rescored);
+        status = launchRescoreKeys(d.rescore.data, d.rescore.dtype, d.rescore.scale,
+                                   static_cast<int>(std::min<std::int64_t>(d.rescore.doc_count, INT32_MAX)),
+                                   dim, d.queries, batch, keys, plan.width, d.metric, rescored, s);
+        if (status != ZCGVS_OK) {
+            return status;
+        }
+        MergeInputs in;
+        in.dense = rescored;
+        in.n_dense = plan.width;
+        in.dense_stride = plan.width;
+        status = launchSelectMerge(in, d.k, batch, keys, nullptr, nullptr, d_out_indices,
+                                   d_out_values, s);
+        if (status != ZCGVS_OK) {
+            return status;
+        }
+    }
+    return clearError();
+}
+
+}  // extern "C"

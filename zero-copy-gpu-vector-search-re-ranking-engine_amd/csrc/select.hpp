@@ -1,0 +1,136 @@
+// Exact top-k selection on 64-bit keys (see common.hpp for the key layout).
+//
+// The k best keys of a set are found by a most-significant-digit radix select: histograms of
+// successive digits (11, 11, 10 bits of the score, then 11, 11, 10 bits of the index part) narrow
+// down the bucket that holds the k-th best key. Once a bucket's population equals the number of
+// keys still needed, every key >= that bucket's lower edge is selected, which is exactly k keys
+// because keys are unique. The selected keys are then sorted descending with a bitonic network.
+#pragma once
+
+#include "common.hpp"
+
+namespace zcgvs_hip {
+
+constexpr int kSelectBins = 2048;
+constexpr int kSelectPasses = 6;
+constexpr int kSelectThreads = 256;
+constexpr int kMaxK = 1024;
+
+__host__ __device__ constexpr int selectDigitWidth(int pass) {
+    return (pass % 3 == 2) ? 10 : 11;
+}
+
+// Bits of the key decided before `pass`.
+__host__ __device__ constexpr int selectBitsBefore(int pass) {
+    return pass == 0 ? 0 : pass == 1 ? 11 : pass == 2 ? 22 : pass == 3 ? 32 : pass == 4 ? 43 : 54;
+}
+
+struct SelectState {
+    std::uint64_t prefix;  // decided high bits, right-aligned
+    std::uint32_t bits;    // number of decided bits
+    std::uint32_t need;    // keys still to take from inside the prefix bucket
+    std::uint32_t done;    // threshold is final
+    std::uint32_t arrived; // blocks finished with the current pass (multi-block form)
+    std::uint32_t count;   // keys collected
+    std::uint32_t pad;
+};
+
+__device__ __forceinline__ std::uint64_t selectThreshold(const SelectState& s) {
+    return s.bits >= 64 ? s.prefix : (s.prefix << (64 - s.bits));
+}
+
+// Given a full histogram of the current digit, pick the bucket holding the need-th best key and
+// update the state. Runs on one block of kSelectThreads threads; `scratch` is LDS of
+// kSelectThreads u32. The histogram may be in LDS or global memory (read with plain loads; the
+// caller makes it visible first).
+__device__ inline void selectPickBucket(const std::uint32_t* hist, int width, SelectState* state,
+                                        std::uint32_t* scratch) {
+    const int bins = 1 << width;
+    const int per_thread = bins / kSelectThreads;  // 8 or 4
+    const int t = threadIdx.x;
+    // Thread t owns the t-th group of bins counted from the top.
+    const int top = bins - per_thread * t;  // exclusive upper bin
+    std::uint32_t local = 0;
+    for (int b = top - 1; b >= top - per_thread; --b) {
+        local += hist[b];
+    }
+    scratch[t] = local;
+    __syncthreads();
+    // Inclusive scan over threads (from the top bins down), Hillis-Steele.
+    for (int offset = 1; offset < kSelectThreads; offset <<= 1) {
+        const std::uint32_t add = t >= offset ? scratch[t - offset] : 0u;
+        __syncthreads();
+        scratch[t] += add;
+        __syncthreads();
+    }
+    const std::uint32_t need = state->need;
+    const std::uint32_t before = t == 0 ? 0u : scratch[t - 1];
+    const std::uint32_t through = scratch[t];
+    __syncthreads();
+    if (before < need && need <= through) {
+        std::uint32_t above = before;
+        for (int b = top - 1; b >= top - per_thread; --b) {
+            const std::uint32_t h = hist[b];
+            if (above + h >= need) {
+                const std::uint32_t remaining = need - above;
+                state->prefix = (state->prefix << width) | static_cast<std::uint64_t>(b);
+                state->bits += static_cast<std::uint32_t>(width);
+                state->need = remaining;
+                state->done = (h == remaining || state->bits >= 64) ? 1u : 0u;
+                break;
+            }
+            above += h;
+        }
+    }
+    __syncthreads();
+}
+
+// Sorts `n` (a power of two, <= 2 * kSelectThreads * 2) keys in LDS, descending.
+__device__ inline void bitonicSortDescending(std::uint64_t* keys, int n) {
+    for (int size = 2; size <= n; size <<= 1) {
+        for (int stride = size >> 1; stride > 0; stride >>= 1) {
+            for (int i = threadIdx.x; i < n / 2; i += blockDim.x) {
+                const int lo = 2 * i - (i & (stride - 1));
+                const int hi = lo + stride;
+                const bool descending = (lo & size) == 0;
+                const std::uint64_t a = keys[lo];
+                const std::uint64_t b = keys[hi];
+                if ((a < b) == descending) {
+                    keys[lo] = b;
+                    keys[hi] = a;
+                }
+            }
+            __syncthreads();
+        }
+    }
+}
+
+// ---- host-side internal API used by the fused search -----------------------------------------
+
+// Inputs of one per-query merge. For query q the candidate set is the union of
+//   prev[q][0..k_prev)                       the selection kept from earlier phases,
+//   dense[q * dense_stride + 0..n_dense)     keys written at fixed slots (key 0 = empty slot),
+//   seg[((s * batch + q) << seg_log2) + j]   for every segment s < n_seg and
+//                                            j < min(seg_count[s * batch + q], 1 << seg_log2),
+// where each segment is the private append buffer of one workgroup of a scan launch.
+struct MergeInputs {
+    const std::uint64_t* prev = nullptr;
+    int k_prev = 0;
+    const std::uint64_t* dense = nullptr;
+    long long n_dense = 0;
+    long long dense_stride = 0;
+    const std::uint64_t* seg = nullptr;
+    const std::uint32_t* seg_count = nullptr;
+    int n_seg = 0;
+    int seg_log2 = 0;
+};
+
+// Selects the best k keys of each query's candidate set; writes them sorted descending to
+// out_keys[q][0..k), sets threshold[q] to the k-th best key (0 if fewer than k keys exist) and
+// sets overflow[q] when a segment count exceeded its capacity. When out_index/out_score are
+// non-null the selection is also written as (index, score) pairs [batch, k].
+int launchSelectMerge(const MergeInputs& in, int k, int batch, std::uint64_t* out_keys,
+                      std::uint64_t* threshold, std::uint32_t* overflow, int* out_index,
+                      float* out_score, hipStream_t stream);
+
+}  // namespace zcgvs_hip

@@ -1,0 +1,400 @@
+// Top-k selection: zcgvs_launch_topk (src/cuda/topk.cu:132-189 launchTopK) over a materialized
+// [batch, doc_count] score matrix, and the per-query candidate merge used by the fused search.
+//
+// The reference sorts 1024-score tiles with a bitonic network and merges tile winners
+// recursively; ties fall wherever the network puts them. Here the selection is an exact radix
+// select on unique 64-bit keys (select.hpp), so the result is the stable (score desc, index asc)
+// order of tests/cpp/cpu_reference.hpp:26-34 on every run. Each pass reads the scores once; the
+// block that finishes a pass last picks the bucket (no host round trip, capture safe).
+#include <hip/hip_runtime.h>
+
+#include <algorithm>
+
+#include "common.hpp"
+#include "select.hpp"
+
+namespace zcgvs_hip {
+
+namespace {
+
+constexpr int kTileSize = 1024;      // reference tile (topk.cu:17), kept for the sizing helpers
+constexpr int kMergeTile = 4096;     // reference merge tile (topk.cu:18)
+constexpr int kStateWords = 16;      // SelectState, padded
+constexpr int kMinScratchElements = kStateWords + kSelectBins + 16;
+
+struct TopKScratch {
+    __host__ __device__ SelectState* state(int q) const {
+        return reinterpret_cast<SelectState*>(base + static_cast<std::size_t>(q) * stride);
+    }
+    __host__ __device__ std::uint32_t* hist(int q) const {
+        return base + static_cast<std::size_t>(q) * stride + kStateWords;
+    }
+    std::uint32_t* base;
+    std::size_t stride;  // u32 words per query
+};
+
+struct KeyScratch {
+    __host__ __device__ std::uint64_t* keys(int q) const {
+        return reinterpret_cast<std::uint64_t*>(base + static_cast<std::size_t>(q) * stride);
+    }
+    std::uint32_t* base;
+    std::size_t stride;  // u32 words per query (even)
+};
+
+__global__ void topkInitKernel(TopKScratch scratch, int k) {
+    const int q = blockIdx.x;
+    std::uint32_t* hist = scratch.hist(q);
+    for (int i = threadIdx.x; i < kSelectBins; i += blockDim.x) {
+        hist[i] = 0u;
+    }
+    if (threadIdx.x == 0) {
+        SelectState* s = scratch.state(q);
+        s->prefix = 0ull;
+        s->bits = 0u;
+        s->need = static_cast<std::uint32_t>(k);
+        s->done = 0u;
+        s->arrived = 0u;
+        s->count = 0u;
+    }
+}
+
+__global__ __launch_bounds__(kSelectThreads) void topkHistKernel(const float* __restrict__ scores,
+                                                                 int doc_count, int pass,
+                                                                 TopKScratch scratch) {
+    __shared__ std::uint32_t lds_hist[kSelectBins];
+    __shared__ std::uint32_t lds_scan[kSelectThreads];
+    __shared__ SelectState lds_state;
+    __shared__ int is_last;
+
+    const int q = blockIdx.y;
+    SelectState* state = scratch.state(q);
+    if (threadIdx.x == 0) {
+        lds_state = *state;
+    }
+    for (int i = threadIdx.x; i < kSelectBins; i += blockDim.x) {
+        lds_hist[i] = 0u;
+    }
+    __syncthreads();
+    if (lds_state.done) {
+        return;
+    }
+    const int width = selectDigitWidth(pass);
+    const std::uint32_t bits = lds_state.bits;
+    const std::uint64_t prefix = lds_state.prefix;
+    const int shift = 64 - static_cast<int>(bits) - width;
+    const std::uint64_t digit_mask = (1ull << width) - 1ull;
+    const float* row = scores + static_cast<std::size_t>(q) * doc_count;
+    for (long long i = static_cast<long long>(blockIdx.x) * blockDim.x + threadIdx.x;
+         i < doc_count; i += static_cast<long long>(gridDim.x) * blockDim.x) {
+        const std::uint64_t key = makeKey(row[i], static_cast<std::uint32_t>(i));
+        if (bits == 0u || (key >> (64 - bits)) == prefix) {
+            atomicAdd(&lds_hist[(key >> shift) & digit_mask], 1u);
+        }
+    }
+    __syncthreads();
+    std::uint32_t* hist = scratch.hist(q);
+    for (int b = threadIdx.x; b < (1 << width); b += blockDim.x) {
+        if (lds_hist[b] != 0u) {
+            atomicAdd(&hist[b], lds_hist[b]);
+        }
+    }
+    __threadfence();
+    __syncthreads();
+    if (threadIdx.x == 0) {
+        const std::uint32_t ticket = atomicAdd(&state->arrived, 1u);
+        is_last = (ticket == gridDim.x - 1) ? 1 : 0;
+    }
+    __syncthreads();
+    if (!is_last) {
+        return;
+    }
+    __threadfence();
+    for (int b = threadIdx.x; b < (1 << width); b += blockDim.x) {
+        lds_hist[b] = __hip_atomic_load(&hist[b], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        hist[b] = 0u;
+    }
+    __syncthreads();
+    selectPickBucket(lds_hist, width, &lds_state, lds_scan);
+    if (threadIdx.x == 0) {
+        lds_state.arrived = 0u;
+        *state = lds_state;
+    }
+    __threadfence();
+}
+
+__global__ __launch_bounds__(kSelectThreads) void topkCollectKernel(
+    const float* __restrict__ scores, int doc_count, int k, TopKScratch scratch, KeyScratch out) {
+    const int q = blockIdx.y;
+    SelectState* state = scratch.state(q);
+    const std::uint64_t threshold = selectThreshold(*state);
+    std::uint64_t* keys = out.keys(q);
+    const float* row = scores + static_cast<std::size_t>(q) * doc_count;
+    for (long long i = static_cast<long long>(blockIdx.x) * blockDim.x + threadIdx.x;
+         i < doc_count; i += static_cast<long long>(gridDim.x) * blockDim.x) {
+        const std::uint64_t key = makeKey(row[i], static_cast<std::uint32_t>(i));
+        if (key >= threshold) {
+            const std::uint32_t slot = atomicAdd(&state->count, 1u);
+            if (slot < static_cast<std::uint32_t>(k)) {  // exactly k keys pass; guard anyway
+                keys[slot] = key;
+            }
+        }
+    }
+}
+
+__global__ __launch_bounds__(kSelectThreads) void topkSortKernel(TopKScratch scratch,
+                                                                 KeyScratch in, int k,
+                                                                 int* __restrict__ out_index,
+                                                                 float* __restrict__ out_score) {
+    __shared__ std::uint64_t lds_keys[kMaxK];
+    const int q = blockIdx.x;
+    const std::uint32_t count = min(scratch.state(q)->count, static_cast<std::uint32_t>(kMaxK));
+    int padded = 1;
+    while (padded < k) {
+        padded <<= 1;
+    }
+    const std::uint64_t* keys = in.keys(q);
+    for (int i = threadIdx.x; i < padded; i += blockDim.x) {
+        lds_keys[i] = i < static_cast<int>(count) ? keys[i] : 0ull;
+    }
+    __syncthreads();
+    bitonicSortDescending(lds_keys, padded);
+    for (int i = threadIdx.x; i < k; i += blockDim.x) {
+        const std::size_t o = static_cast<std::size_t>(q) * k + i;
+        writeHit(lds_keys[i], &out_index[o], &out_score[o]);
+    }
+}
+
+// ---- candidate merge (one block per query) -----------------------------------------------------
+
+constexpr int kMaxSegments = 4096;
+
+// Applies f to every non-zero key of query q's candidate set (see MergeInputs).
+template <typename F>
+__device__ __forceinline__ void forEachCandidate(const MergeInputs& in, int q, int batch,
+                                                 const std::uint32_t* seg_valid, F&& f) {
+    if (in.prev != nullptr) {
+        const std::uint64_t* prev = in.prev + static_cast<std::size_t>(q) * in.k_prev;
+        for (int i = threadIdx.x; i < in.k_prev; i += blockDim.x) {
+            const std::uint64_t key = prev[i];
+            if (key != 0ull) {
+                f(key);
+            }
+        }
+    }
+    if (in.dense != nullptr) {
+        const std::uint64_t* dense = in.dense + static_cast<std::size_t>(q) * in.dense_stride;
+        for (long long i = threadIdx.x; i < in.n_dense; i += blockDim.x) {
+            const std::uint64_t key = dense[i];
+            if (key != 0ull) {
+                f(key);
+            }
+        }
+    }
+    if (in.seg != nullptr) {
+        const long long total = static_cast<long long>(in.n_seg) << in.seg_log2;
+        const long long mask = (1LL << in.seg_log2) - 1;
+        for (long long i = threadIdx.x; i < total; i += blockDim.x) {
+            const int s = static_cast<int>(i >> in.seg_log2);
+            const long long j = i & mask;
+            if (j < static_cast<long long>(seg_valid[s])) {
+                const std::uint64_t key =
+                    in.seg[((static_cast<std::size_t>(s) * batch + q) << in.seg_log2) + j];
+                if (key != 0ull) {
+                    f(key);
+                }
+            }
+        }
+    }
+}
+
+__global__ __launch_bounds__(kSelectThreads) void selectMergeKernel(
+    MergeInputs in, int k, int batch, std::uint64_t* __restrict__ out_keys,
+    std::uint64_t* __restrict__ threshold, std::uint32_t* __restrict__ overflow,
+    int* __restrict__ out_index, float* __restrict__ out_score) {
+    __shared__ std::uint32_t lds_hist[kSelectBins];
+    __shared__ std::uint32_t lds_scan[kSelectThreads];
+    __shared__ std::uint64_t lds_keys[kMaxK];
+    __shared__ std::uint32_t lds_seg[kMaxSegments];
+    __shared__ SelectState lds_state;
+    __shared__ std::uint32_t lds_valid;
+    __shared__ std::uint32_t lds_overflow;
+
+    const int q = blockIdx.x;
+    if (threadIdx.x == 0) {
+        lds_valid = 0u;
+        lds_overflow = 0u;
+    }
+    __syncthreads();
+    const std::uint32_t cap = 1u << in.seg_log2;
+    for (int s = threadIdx.x; s < in.n_seg; s += blockDim.x) {
+        const std::uint32_t c = in.seg_count[static_cast<std::size_t>(s) * batch + q];
+        lds_seg[s] = min(c, cap);
+        if (c > cap) {
+            lds_overflow = 1u;
+        }
+    }
+    __syncthreads();
+
+    std::uint32_t mine = 0;
+    forEachCandidate(in, q, batch, lds_seg, [&](std::uint64_t) { ++mine; });
+    atomicAdd(&lds_valid, mine);
+    if (threadIdx.x == 0) {
+        lds_state.prefix = 0ull;
+        lds_state.bits = 0u;
+        lds_state.need = static_cast<std::uint32_t>(k);
+        lds_state.count = 0u;
+    }
+    __syncthreads();
+    const std::uint32_t n_valid = lds_valid;
+    if (threadIdx.x == 0) {
+        lds_state.done = n_valid <= static_cast<std::uint32_t>(k) ? 1u : 0u;
+    }
+    __syncthreads();
+
+    for (int pass = 0; pass < kSelectPasses && !lds_state.done; ++pass) {
+        const int width = selectDigitWidth(pass);
+        for (int i = threadIdx.x; i < (1 << width); i += blockDim.x) {
+            lds_hist[i] = 0u;
+        }
+        __syncthreads();
+        const std::uint32_t bits = lds_state.bits;
+        const std::uint64_t prefix = lds_state.prefix;
+        const int shift = 64 - static_cast<int>(bits) - width;
+        const std::uint64_t digit_mask = (1ull << width) - 1ull;
+        forEachCandidate(in, q, batch, lds_seg, [&](std::uint64_t key) {
+            if (bits == 0u || (key >> (64 - bits)) == prefix) {
+                atomicAdd(&lds_hist[(key >> shift) & digit_mask], 1u);
+            }
+        });
+        __syncthreads();
+        selectPickBucket(lds_hist, width, &lds_state, lds_scan);
+    }
+
+    const std::uint64_t cut = n_valid <= static_cast<std::uint32_t>(k) ? 1ull : selectThreshold(lds_state);
+    forEachCandidate(in, q, batch, lds_seg, [&](std::uint64_t key) {
+        if (key >= cut) {
+            const std::uint32_t slot = atomicAdd(&lds_state.count, 1u);
+            if (slot < static_cast<std::uint32_t>(kMaxK)) {
+                lds_keys[slot] = key;
+            }
+        }
+    });
+    __syncthreads();
+    const std::uint32_t taken = min(lds_state.count, static_cast<std::uint32_t>(k));
+    int padded = 1;
+    while (padded < k) {
+        padded <<= 1;
+    }
+    for (int i = static_cast<int>(taken) + threadIdx.x; i < padded; i += blockDim.x) {
+        lds_keys[i] = 0ull;
+    }
+    __syncthreads();
+    bitonicSortDescending(lds_keys, padded);
+
+    std::uint64_t* dst = out_keys + static_cast<std::size_t>(q) * k;
+    for (int i = threadIdx.x; i < k; i += blockDim.x) {
+        dst[i] = lds_keys[i];
+        if (out_index != nullptr) {
+            const std::size_t o = static_cast<std::size_t>(q) * k + i;
+            writeHit(lds_keys[i], &out_index[o], &out_score[o]);
+        }
+    }
+    if (threadIdx.x == 0) {
+        if (threshold != nullptr) {
+            threshold[q] = taken >= static_cast<std::uint32_t>(k) ? lds_keys[k - 1] : 0ull;
+        }
+        if (lds_overflow != 0u && overflow != nullptr) {
+            overflow[q] = 1u;
+        }
+    }
+}
+
+int topkScratchElements(int doc_count, int k) {
+    if (doc_count <= 0 || k <= 0) {
+        return 0;
+    }
+    const long long reference = static_cast<long long>((doc_count + kTileSize - 1) / kTileSize) * k;
+    const long long needed = std::max<long long>(kMinScratchElements, 2LL * k + 16);
+    return static_cast<int>(std::max(reference, needed));
+}
+
+}  // namespace
+
+int launchSelectMerge(const MergeInputs& in, int k, int batch, std::uint64_t* out_keys,
+                      std::uint64_t* threshold, std::uint32_t* overflow, int* out_index,
+                      float* out_score, hipStream_t stream) {
+    if (in.n_seg > kMaxSegments) {
+        return setError(ZCGVS_ERR_RUNTIME, "zcgvs select: too many candidate segments");
+    }
+    selectMergeKernel<<<batch, kSelectThreads, 0, stream>>>(in, k, batch, out_keys, threshold,
+                                                            overflow, out_index, out_score);
+    ZCGVS_LAUNCH_CHECK("select merge");
+    return ZCGVS_OK;
+}
+
+}  // namespace zcgvs_hip
+
+using namespace zcgvs_hip;
+
+extern "C" {
+
+int zcgvs_topk_tile_size(void) { return kTileSize; }
+int zcgvs_topk_merge_tile(void) { return kMergeTile; }
+int zcgvs_topk_max_k(void) { return kMaxK; }
+
+int zcgvs_topk_block_count(int doc_count) {
+    if (doc_count <= 0) {
+        return 0;
+    }
+    return (doc_count + kTileSize - 1) / kTileSize;
+}
+
+int zcgvs_topk_scratch_elements(int doc_count, int k) { return topkScratchElements(doc_count, k); }
+
+int zcgvs_launch_topk(const float* d_scores, int doc_count, int k, int batch, int* d_out_indices,
+                      float* d_out_values, float* d_scratch_values_a, int* d_scratch_indices_a,
+                      float* d_scratch_values_b, int* d_scratch_indices_b,
+                      zcgvs_stream_t stream) {
+    (void)d_scratch_values_b;
+    (void)d_scratch_indices_b;
+    if (k <= 0 || doc_count <= 0 || batch <= 0) {
+        return clearError();
+    }
+    if (k > kMaxK) {
+        return setError(ZCGVS_ERR_INVALID_ARGUMENT,
+                        "zcgvs top-k: k=" + std::to_string(k) + " exceeds per-tile capacity " +
+                            std::to_string(kMaxK));
+    }
+    if (k > doc_count) {
+        return setError(ZCGVS_ERR_INVALID_ARGUMENT,
+                        "zcgvs top-k: k=" + std::to_string(k) + " exceeds candidate count " +
+                            std::to_string(doc_count));
+    }
+    if (d_scores == nullptr || d_out_indices == nullptr || d_out_values == nullptr ||
+        d_scratch_values_a == nullptr || d_scratch_indices_a == nullptr) {
+        return setError(ZCGVS_ERR_INVALID_ARGUMENT, "zcgvs top-k: null device pointer");
+    }
+    const std::size_t elements = static_cast<std::size_t>(topkScratchElements(doc_count, k));
+    TopKScratch scratch{reinterpret_cast<std::uint32_t*>(d_scratch_values_a), elements & ~std::size_t(1)};
+    KeyScratch keys{reinterpret_cast<std::uint32_t*>(d_scratch_indices_a), elements & ~std::size_t(1)};
+    const hipStream_t s = toStream(stream);
+
+    const long long per_query_blocks = (static_cast<long long>(doc_count) + 8191) / 8192;
+    const long long budget = std::max(1LL, 4LL * deviceComputeUnits() / batch);
+    const unsigned tiles = static_cast<unsigned>(std::max(1LL, std::min(per_query_blocks, budget)));
+    const dim3 grid(tiles, static_cast<unsigned>(batch));
+
+    topkInitKernel<<<batch, kSelectThreads, 0, s>>>(scratch, k);
+    ZCGVS_LAUNCH_CHECK("top-k init");
+    for (int pass = 0; pass < kSelectPasses; ++pass) {
+        topkHistKernel<<<grid, kSelectThreads, 0, s>>>(d_scores, doc_count, pass, scratch);
+        ZCGVS_LAUNCH_CHECK("top-k histogram");
+    }
+    topkCollectKernel<<<grid, kSelectThreads, 0, s>>>(d_scores, doc_count, k, scratch, keys);
+    ZCGVS_LAUNCH_CHECK("top-k collect");
+    topkSortKernel<<<batch, kSelectThreads, 0, s>>>(scratch, keys, k, d_out_indices, d_out_values);
+    ZCGVS_LAUNCH_CHECK("top-k sort");
+    return clearError();
+}
+
+}  // extern "C"
