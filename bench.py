@@ -1,0 +1,282 @@
+#!/usr/bin/env python3
+"""Benchmark of the zero-copy search hot path on one MI355X.
+
+A step is one fused search of a resident query batch against a resident corpus (the device
+pipeline of src/search/searcher.cpp:209-285: scan, selection, optional rescore), timed with HIP
+events on the stream it runs on. Inputs are synthetic (seeded, generated on the device) and in
+HBM before timing starts; only [batch, k] ids and scores are produced.
+
+Default workload (the per-vector int8 configuration): 10,000,000 x 768 int8 rows, per-row scale
+max|x|/127, 256 queries quantized the same way on the device, k = 100, int8 MFMA contraction.
+Other workloads: --workload {int8-10m, f32-1m-b1, f16-1m-b1, f32-1m-b64, f16-1m-b64,
+binary-50m, cpu-ref}.
+
+Prints one JSON line: queries/s over the timed steps, p50 step latency, the scan kernel's
+roofline (algorithmic bytes / scan time, from events around the scan launches), and the CPU
+oracle timed on a bounded sample of the same queries on this host (with a full-size parity
+check of the sampled queries against the GPU result).
+"""
+
+from __future__ import annotations
+
+import argparse
+import json
+import os
+import statistics
+import sys
+import time
+from pathlib import Path
+
+import numpy as np
+
+ROOT = Path(__file__).resolve().parent
+sys.path.insert(0, str(ROOT))
+
+from __graft_entry__ import load_package  # noqa: E402
+
+HBM_PEAK_GBS = 8000.0          # MI355X HBM3E, published
+INT8_MFMA_PEAK_TOPS = 5000.0   # MI355X dense int8 MFMA, published
+CORPUS_SEED = 1234
+QUERY_SEED = 4321
+
+WORKLOADS = {
+    "int8-10m": dict(kind="i8i8", n=10_000_000, dim=768, batch=256, k=100,
+                     name="per-vector int8 10M x 768, batch 256, k=100"),
+    "f32-1m-b1": dict(kind="f32", n=1_000_000, dim=384, batch=1, k=10,
+                      name="float32 1M x 384, batch 1, k=10"),
+    "f16-1m-b1": dict(kind="f16", n=1_000_000, dim=384, batch=1, k=10,
+                      name="float16 1M x 384, batch 1, k=10"),
+    "f32-1m-b64": dict(kind="f32", n=1_000_000, dim=384, batch=64, k=10,
+                       name="float32 1M x 384, batch 64, k=10"),
+    "f16-1m-b64": dict(kind="f16", n=1_000_000, dim=384, batch=64, k=10,
+                       name="float16 1M x 384, batch 64, k=10"),
+    "binary-50m": dict(kind="binary", n=50_000_000, dim=1024, batch=32, k=10, candidates=1000,
+                       name="binary 50M x 1024 + float16 rescore of 1000, batch 32, k=10"),
+    "cpu-ref": dict(kind="f32", n=5183, dim=384, batch=1, k=10,
+                    name="float32 5,183 x 384, batch 1, k=10"),
+}
+
+
+def log(*args):
+    print("[bench]", *args, file=sys.stderr, flush=True)
+
+
+def build_inputs(capi, w):
+    """Corpus, queries and search descriptor on the device."""
+    n, dim, batch = w["n"], w["dim"], w["batch"]
+    kind = w["kind"]
+    keep = {}
+    chunk = max(1, min(n, (2 << 30) // (dim * 4)))
+    stage = capi.DeviceArray((chunk, dim), np.float32)
+    if kind == "i8i8":
+        corpus = capi.DeviceArray((n, dim), np.int8)
+        scales = capi.DeviceArray(n, np.float32)
+        keep["scales"] = scales
+    elif kind == "f32":
+        corpus = capi.DeviceArray((n, dim), np.float32)
+    elif kind == "f16":
+        corpus = capi.DeviceArray((n, dim), np.float16)
+    else:
+        corpus = capi.DeviceArray((n, (dim + 31) // 32), np.uint32)
+        rescore = capi.DeviceArray((n, dim), np.float16)
+        keep["rescore"] = rescore
+    for start in range(0, n, chunk):
+        rows = min(chunk, n - start)
+        capi.generate_normalized(stage, rows, dim, CORPUS_SEED, start)
+        if kind == "i8i8":
+            capi.launch_quantize_rows_i8(stage, rows, dim, corpus.ptr + start * dim, scales.ptr + start * 4)
+        elif kind == "f32":
+            capi.call("zcgvs_memcpy_d2d", corpus.ptr + start * dim * 4, stage.ptr, rows * dim * 4, None)
+        elif kind == "f16":
+            capi.launch_convert_f32_to_f16(stage, corpus.ptr + start * dim * 2, rows * dim)
+        else:
+            words = (dim + 31) // 32
+            capi.launch_pack_binary(stage, corpus.ptr + start * words * 4, rows, dim)
+            capi.launch_convert_f32_to_f16(stage, rescore.ptr + start * dim * 2, rows * dim)
+        capi.synchronize()
+    stage.free()
+    queries = capi.DeviceArray((batch, dim), np.float32)
+    capi.generate_normalized(queries, batch, dim, QUERY_SEED, 0)
+    capi.synchronize()
+    dtype = {"i8i8": capi.I8, "f32": capi.F32, "f16": capi.F16, "binary": capi.BINARY}[kind]
+    store = capi.store_desc(corpus, n, dim, dtype, 1.0, keep.get("scales"))
+    extra = {}
+    if kind == "i8i8":
+        extra["int8_mode"] = capi.INT8_PER_VECTOR
+    if kind == "binary":
+        extra["rescore"] = capi.store_desc(keep["rescore"], n, dim, capi.F16)
+        extra["rescore_candidates"] = w["candidates"]
+    desc = capi.search_desc(store, queries, batch, w["k"], capi.COSINE, **extra)
+    return desc, corpus, queries, keep
+
+
+def algorithmic_bytes(w):
+    n, dim, batch = w["n"], w["dim"], w["batch"]
+    per_row = {"i8i8": dim + 4, "f32": dim * 4, "f16": dim * 2, "binary": (dim + 31) // 32 * 4}[w["kind"]]
+    return n * per_row + batch * dim * 4
+
+
+def cpu_baseline(capi, w, corpus, keep, queries, gpu_idx, gpu_val, budget_s):
+    """The CPU oracle on a bounded sample of the same queries over the full corpus."""
+    import oracle
+
+    n, dim, batch, k = w["n"], w["dim"], w["batch"], w["k"]
+    kind = w["kind"]
+    log("copying corpus to host for the CPU baseline")
+    host_q = queries.to_host()
+    if kind == "i8i8":
+        codes = corpus.to_host()
+        row_scales = keep["scales"].to_host()
+    elif kind == "f16":
+        decoded = corpus.to_host().astype(np.float32)
+    elif kind == "f32":
+        decoded = corpus.to_host()
+    else:
+        return None, None
+
+    def run(rows):
+        if kind == "i8i8":
+            qcodes, qscales = oracle.quantize_rows_i8(host_q[rows])
+            scores = oracle.scores_i8i8(codes, row_scales, qcodes, qscales)
+        else:
+            scores = oracle.scores_f32(decoded, host_q[rows], oracle.COSINE)
+        return oracle.topk(scores, k)
+
+    t0 = time.perf_counter()
+    run([0])
+    one = time.perf_counter() - t0
+    sample = int(max(1, min(batch, 64, budget_s / max(one, 1e-6))))
+    rows = list(range(sample))
+    t0 = time.perf_counter()
+    ref_idx, ref_val = run(rows)
+    elapsed = time.perf_counter() - t0
+    if kind == "i8i8":
+        equal = bool(np.array_equal(ref_idx, gpu_idx[:sample]) and np.array_equal(ref_val, gpu_val[:sample]))
+    else:
+        equal = bool(np.array_equal(ref_idx, gpu_idx[:sample]))
+    baseline = {
+        "value": sample / elapsed,
+        "unit": "queries/s",
+        "cores": oracle.threads(),
+        "kind": "port",
+        "sample": f"first {sample} of the {batch} queries against all {n:,} rows "
+                  f"(oracle scores + stable top-{k}), {elapsed:.1f} s",
+    }
+    parity = {"queries_checked": sample, "bit_exact" if kind == "i8i8" else "ids_equal": equal}
+    return baseline, parity
+
+
+def main(argv=None) -> int:
+    parser = argparse.ArgumentParser(description=__doc__, formatter_class=argparse.RawDescriptionHelpFormatter)
+    parser.add_argument("--gpus", type=int, default=1)
+    parser.add_argument("--steps", type=int, default=20)
+    parser.add_argument("--warmup", type=int, default=5)
+    parser.add_argument("--workload", choices=sorted(WORKLOADS), default="int8-10m")
+    parser.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
+    parser.add_argument("--cpu-budget", type=float, default=12.0, help="seconds of CPU sample work")
+    args = parser.parse_args(argv)
+    if args.gpus != 1:
+        print(f"bench.py: this build runs on one GPU; --gpus {args.gpus} is not supported "
+              "(the corpus would shard by rows, with one gather of batch*k hits per GPU)",
+              file=sys.stderr)
+        return 2
+
+    load_package()
+    from zcgvs_amd import capi
+
+    if capi.device_count() <= 0:
+        raise SystemExit("bench.py: no HIP device")
+    info = capi.device_info(0)
+    w = WORKLOADS[args.workload]
+    log(f"device {info.name.decode()} {info.arch.decode()} CUs={info.compute_units}; workload {w['name']}")
+
+    desc, corpus, queries, keep = build_inputs(capi, w)
+    size = capi.search_workspace_bytes(desc)
+    workspace = capi.DeviceArray(size, np.uint8)
+    out_idx = capi.DeviceArray((w["batch"], w["k"]), np.int32)
+    out_val = capi.DeviceArray((w["batch"], w["k"]), np.float32)
+    stream = capi.Stream()
+    log(f"inputs resident; workspace {size / 2**20:.1f} MiB")
+
+    for _ in range(args.warmup):
+        capi.search_topk(desc, workspace, size, out_idx, out_val, stream)
+    stream.synchronize()
+
+    max_phases = 8
+    starts = [capi.Event() for _ in range(args.steps)]
+    ends = [capi.Event() for _ in range(args.steps)]
+    scan_events = [[capi.Event() for _ in range(2 * max_phases)] for _ in range(args.steps)]
+    capi.synchronize()
+    t0 = time.perf_counter()
+    phases = 0
+    for step in range(args.steps):
+        starts[step].record(stream)
+        phases = capi.search_topk_profiled(desc, workspace, size, out_idx, out_val, stream,
+                                           scan_events[step], max_phases)
+        ends[step].record(stream)
+    stream.synchronize()
+    capi.synchronize()
+    wall = time.perf_counter() - t0
+
+    step_ms = [starts[i].elapsed_ms(ends[i]) for i in range(args.steps)]
+    used = min(phases, max_phases)
+    scan_ms = [sum(scan_events[i][2 * p].elapsed_ms(scan_events[i][2 * p + 1]) for p in range(used))
+               for i in range(args.steps)]
+    flags = np.empty(w["batch"], dtype=np.uint32)
+    capi.call("zcgvs_memcpy_d2h", flags.ctypes.data, capi.search_overflow_flags(desc, workspace),
+              flags.nbytes, None)
+    capi.synchronize()
+    if flags.any():
+        log(f"WARNING: {int(flags.sum())} queries overflowed their candidate buffers")
+    gpu_idx, gpu_val = out_idx.to_host(), out_val.to_host()
+
+    batch = w["batch"]
+    value = batch * args.steps / wall
+    mean_scan = statistics.mean(scan_ms) if used else float("nan")
+    bytes_step = algorithmic_bytes(w)
+    achieved = bytes_step / (mean_scan * 1e-3) / 1e9 if used else None
+    result = {
+        "metric": "queries/sec + p50 latency (N=10M d=768 int8, k=100); scan HBM GB/s",
+        "value": round(value, 2),
+        "unit": "queries/s",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": round(wall * 1e3 / args.steps, 4),
+        "p50_ms": round(statistics.median(step_ms), 4),
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": {"i8i8": "int8", "f32": "f32", "f16": "f16", "binary": "u32"}[w["kind"]],
+        "data": "synthetic (seeded N(0,1) rows, L2-normalized, generated on the device)",
+        "config": {"workload": w["name"], "N": w["n"], "dim": w["dim"], "batch": batch, "k": w["k"],
+                   "scan_phases": phases},
+        "roofline": {
+            "bound": "hbm",
+            "achieved": round(achieved, 1) if achieved else None,
+            "peak": HBM_PEAK_GBS,
+            "unit": "GB/s",
+            "frac": round(achieved / HBM_PEAK_GBS, 4) if achieved else None,
+            "traffic": None,
+            "kernel": "scan (all phase launches of one step)",
+            "kernel_ms": round(mean_scan, 4) if used else None,
+        },
+    }
+    if w["kind"] == "i8i8":
+        ops = 2.0 * w["n"] * w["dim"] * batch
+        tops = ops / (mean_scan * 1e-3) / 1e12
+        result["mfma"] = {"achieved": round(tops, 1), "peak": INT8_MFMA_PEAK_TOPS, "unit": "TOP/s",
+                          "frac": round(tops / INT8_MFMA_PEAK_TOPS, 4)}
+    if flags.any():
+        result["overflow_queries"] = int(flags.sum())
+    if not args.no_cpu:
+        baseline, parity = cpu_baseline(capi, w, corpus, keep, queries, gpu_idx, gpu_val, args.cpu_budget)
+        result["cpu_baseline"] = baseline
+        if parity is not None:
+            result["parity"] = parity
+    print(json.dumps(result), flush=True)
+    return 0
+
+
+if __name__ == "__main__":
+    raise SystemExit(main())

@@ -273,6 +273,16 @@ size_t zcgvs_search_workspace_bytes(const zcgvs_search_desc* desc);
 int zcgvs_search_topk(const zcgvs_search_desc* desc, void* d_workspace, size_t workspace_bytes,
                       int* d_out_indices, float* d_out_values, zcgvs_stream_t stream);
 
+/* Measurement hook: zcgvs_search_topk that also records events[2p] and events[2p + 1] on `stream`
+ * immediately before and after the scan launches of phase p, for p < max_phases, and returns the
+ * number of phases in *phases. The events must have been created with zcgvs_event_create. Not
+ * meant for graph capture. No reference counterpart (the reference times the whole pipeline with
+ * one event pair, src/search/searcher.cpp:358-365). */
+int zcgvs_search_topk_profiled(const zcgvs_search_desc* desc, void* d_workspace,
+                               size_t workspace_bytes, int* d_out_indices, float* d_out_values,
+                               zcgvs_stream_t stream, zcgvs_event_t* events, int max_phases,
+                               int* phases);
+
 /* Device address of the [batch] uint32 overflow flags inside a workspace laid out for `desc`
  * (non-zero: that query's result is incomplete and must be recomputed exactly, e.g. with
  * zcgvs_launch_similarity + zcgvs_launch_topk). */

@@ -41,6 +41,7 @@ def lib() -> ctypes.CDLL:
         _lib = ctypes.CDLL(str(LIB_PATH))
         _lib.zo_hamming.restype = ctypes.c_int
         _lib.zo_max_positive.restype = ctypes.c_float
+        _lib.zo_threads.restype = ctypes.c_int
         _lib.zo_bm25_weight.restype = ctypes.c_float
         _lib.zo_bm25_weight.argtypes = [ctypes.c_int64, ctypes.c_int64, ctypes.c_int32,
                                         ctypes.c_double, ctypes.c_double, ctypes.c_double,
@@ -230,3 +231,8 @@ def fuse(dense, lexical, lexical_max, weight) -> np.ndarray:
 def bm25_weight(doc_count, df, tf, length, average_length, k1=1.2, b=0.75) -> float:
     return float(lib().zo_bm25_weight(doc_count, df, tf, float(length), float(average_length),
                                       float(k1), float(b)))
+
+
+def threads() -> int:
+    """OpenMP threads the parallel score loops use."""
+    return int(lib().zo_threads())

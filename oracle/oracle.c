@@ -354,8 +354,10 @@ static int zo_hit_compare(const void* a, const void* b) {
  * (tests/cpp/cpu_reference.hpp:26-34). Slots past n are (-1, -FLT_MAX) (src/cuda/topk.cu:49-50). */
 void zo_topk(const float* scores, int64_t n, int batch, int k, int32_t* out_index,
              float* out_score) {
-    zo_hit* heap = (zo_hit*)malloc(sizeof(zo_hit) * (size_t)(k > 0 ? k : 1));
+    /* Queries are independent; the parallel loop changes no result. */
+#pragma omp parallel for schedule(dynamic, 1)
     for (int q = 0; q < batch; ++q) {
+        zo_hit* heap = (zo_hit*)malloc(sizeof(zo_hit) * (size_t)(k > 0 ? k : 1));
         const float* row = scores + (int64_t)q * n;
         int size = 0;
         for (int64_t i = 0; i < n; ++i) {
@@ -375,8 +377,8 @@ void zo_topk(const float* scores, int64_t n, int batch, int k, int32_t* out_inde
             out_index[(int64_t)q * k + i] = i < size ? (int32_t)heap[i].index : -1;
             out_score[(int64_t)q * k + i] = i < size ? heap[i].score : -FLT_MAX;
         }
+        free(heap);
     }
-    free(heap);
 }
 
 /* ---------------------------------------------------------------------------------------- */
@@ -459,4 +461,16 @@ float zo_bm25_weight(int64_t doc_count, int64_t df, int32_t tf, double length,
     const double idf = log(1.0 + ((double)doc_count - (double)df + 0.5) / ((double)df + 0.5));
     const double weight = idf * ((double)tf * (k1 + 1.0)) / ((double)tf + normalizer);
     return (float)weight;
+}
+
+/* Threads the OpenMP loops above use (1 when built without OpenMP). */
+#ifdef _OPENMP
+#include <omp.h>
+#endif
+int zo_threads(void) {
+#ifdef _OPENMP
+    return omp_get_max_threads();
+#else
+    return 1;
+#endif
 }

@@ -104,3 +104,38 @@ def test_workspace_sizes(capi):
     size = capi.search_workspace_bytes(_desc(capi, n=10_000_000, dim=768, dtype=capi.I8, batch=256,
                                              k=100, int8_mode=1, row_scales=256))
     assert 0 < size < 1 << 30
+
+
+def test_descriptors_keep_their_buffers_alive(capi):
+    # A descriptor stores raw device addresses. The buffers passed to the descriptor builders
+    # must stay referenced by the descriptor, or a temporary DeviceArray would be freed
+    # (hipFree) before the kernels that read it run.
+    import gc
+    import weakref
+
+    class Owner:  # stands in for a DeviceArray: any object with a device address
+        def __init__(self, address):
+            self.address = address
+
+        def __int__(self):
+            return self.address
+
+    refs = []
+
+    def make(address):
+        owner = Owner(address)
+        refs.append(weakref.ref(owner))
+        return owner
+
+    corpus = capi.store_desc(make(1 << 20), 100, 64, capi.F32, 1.0, make(1 << 21))
+    rescore = capi.store_desc(make(1 << 22), 100, 64, capi.F16)
+    desc = capi.search_desc(corpus, make(1 << 23), 1, 10, rescore=rescore, rescore_candidates=20,
+                            mask=make(1 << 24), query_terms=make(1 << 25), lex_offsets=make(1 << 26),
+                            lex_docs=make(1 << 27), lex_weights=make(1 << 28))
+    del corpus, rescore
+    gc.collect()
+    assert all(r() is not None for r in refs), "a descriptor dropped a buffer it points at"
+    assert desc.corpus.data == 1 << 20 and desc.rescore.data == 1 << 22
+    del desc
+    gc.collect()
+    assert all(r() is None for r in refs)

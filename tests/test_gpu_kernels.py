@@ -95,9 +95,8 @@ def test_similarity_i8i8_bit_exact(gpu):
     assert np.array_equal(d_rs.to_host(), rs)
     mask = (np.arange(N) % 5 != 0).astype(np.uint8)
     scores = capi.DeviceArray((B, N), np.float32)
-    capi.launch_similarity_i8i8(d_codes, d_rs, N, 768, capi.DeviceArray.from_host(qcodes),
-                                capi.DeviceArray.from_host(qs), B, capi.DeviceArray.from_host(mask),
-                                capi.COSINE, scores)
+    d_qcodes, d_qs, d_mask = (capi.DeviceArray.from_host(a) for a in (qcodes, qs, mask))
+    capi.launch_similarity_i8i8(d_codes, d_rs, N, 768, d_qcodes, d_qs, B, d_mask, capi.COSINE, scores)
     capi.synchronize()
     assert np.array_equal(scores.to_host(), oracle.scores_i8i8(codes, rs, qcodes, qs, mask))
 
@@ -145,15 +144,17 @@ def test_gather_rescore_and_remap(gpu, dtype):
     cand = rng.integers(-2, n + 2, size=(batch, count)).astype(np.int32)
     values = capi.DeviceArray((batch, count), np.float32)
     d_cand = capi.DeviceArray.from_host(cand)
-    capi.launch_gather_rescore(store, dtype, INT8_SCALE, n, dim, capi.DeviceArray.from_host(queries),
-                               batch, d_cand, count, capi.COSINE, values)
+    d_queries = capi.DeviceArray.from_host(queries)
+    capi.launch_gather_rescore(store, dtype, INT8_SCALE, n, dim, d_queries, batch, d_cand, count,
+                               capi.COSINE, values)
     capi.synchronize()
     expected = oracle.rescore(decoded, queries, cand)
     tol = np.take_along_axis(float_tolerance(queries, decoded, 0), np.clip(cand, 0, n - 1), 1)
     assert_scores_close(values.to_host(), expected, tol)
     local = rng.integers(-1, count + 1, size=(batch, 10)).astype(np.int32)
     out = capi.DeviceArray((batch, 10), np.int32)
-    capi.launch_remap_indices(d_cand, capi.DeviceArray.from_host(local), count, 10, batch, out)
+    d_local = capi.DeviceArray.from_host(local)
+    capi.launch_remap_indices(d_cand, d_local, count, 10, batch, out)
     capi.synchronize()
     assert np.array_equal(out.to_host(), oracle.remap(cand, local))
 
@@ -189,7 +190,8 @@ def test_lexical_bm25_max_fuse_bit_exact(gpu):
     lexical = capi.DeviceArray(n, np.float32, zero=True)
     peak = capi.DeviceArray(1, np.float32, zero=True)
     d_dense = capi.DeviceArray.from_host(dense)
-    capi.launch_bm25(d_off, d_docs, d_w, capi.DeviceArray.from_host(terms), terms.size, n, lexical)
+    d_terms = capi.DeviceArray.from_host(terms)
+    capi.launch_bm25(d_off, d_docs, d_w, d_terms, terms.size, n, lexical)
     capi.launch_max_positive(lexical, n, peak)
     capi.launch_fuse_scores(d_dense, lexical, peak, 0.6, n)
     capi.synchronize()
@@ -206,8 +208,8 @@ def test_lexical_batched(gpu):
     rng = np.random.default_rng(8)
     terms = rng.integers(-1, vocab, size=(batch, stride)).astype(np.int32)
     lexical = capi.DeviceArray((batch, n), np.float32, zero=True)
-    capi.launch_bm25_batched(*(capi.DeviceArray.from_host(a) for a in (offsets, docs, weights, terms)),
-                             stride, batch, n, lexical)
+    inputs = [capi.DeviceArray.from_host(a) for a in (offsets, docs, weights, terms)]
+    capi.launch_bm25_batched(*inputs, stride, batch, n, lexical)
     capi.synchronize()
     got = lexical.to_host()
     for b in range(batch):

@@ -234,7 +234,7 @@ def test_hybrid_bm25_fused(gpu):
 ])
 def test_search_validation(gpu, bad, match):
     capi = gpu
-    store = capi.store_desc(1 << 20, 1000, 64, capi.F32)
+    store = capi.store_desc(1 << 20, 5000, 64, capi.F32)
     args = dict(batch=1, k=10)
     args.update(bad)
     desc = capi.search_desc(store, 1 << 20, args["batch"], args["k"])

@@ -103,6 +103,8 @@ _SIGNATURES = {
     "zcgvs_search_workspace_bytes": (_sz, [ctypes.POINTER(SearchDesc)]),
     "zcgvs_search_topk": (_i32, [ctypes.POINTER(SearchDesc), _vp, _sz, _vp, _vp, _vp]),
     "zcgvs_search_overflow_flags": (_i32, [ctypes.POINTER(SearchDesc), _vp, ctypes.POINTER(_vp)]),
+    "zcgvs_search_topk_profiled": (_i32, [ctypes.POINTER(SearchDesc), _vp, _sz, _vp, _vp, _vp,
+                                          ctypes.POINTER(_vp), _i32, ctypes.POINTER(_i32)]),
     "zcgvs_generate_normalized": (_i32, [_vp, _i64, _i32, _u64, _i64, _vp]),
 }
 
@@ -345,18 +347,33 @@ def generate_normalized(out, rows, dim, seed, row_offset=0, stream=None):
 
 # ---- fused search --------------------------------------------------------------------------
 
+def _keep_alive(desc, *owners):
+    """Descriptors hold raw device addresses; keep the Python objects that own that memory alive
+    for as long as the descriptor lives, so a temporary DeviceArray passed to a descriptor
+    builder is not freed (hipFree) while a kernel still reads it."""
+    keep = getattr(desc, "_owners", [])
+    keep.extend(o for o in owners if o is not None and not isinstance(o, int))
+    desc._owners = keep
+    return desc
+
+
 def store_desc(data=None, doc_count=0, dim=0, dtype=F32, scale=1.0, row_scales=None) -> StoreDesc:
-    return StoreDesc(ptr(data), doc_count, dim, dtype, scale, ptr(row_scales))
+    return _keep_alive(StoreDesc(ptr(data), doc_count, dim, dtype, scale, ptr(row_scales)),
+                       data, row_scales)
 
 
 def search_desc(corpus: StoreDesc, queries, batch, k, metric=COSINE, *, int8_mode=INT8_REFERENCE,
                 mask=None, rescore: StoreDesc | None = None, rescore_candidates=0, lex_offsets=None,
                 lex_docs=None, lex_weights=None, lex_doc_count=0, lex_vocab_size=0, query_terms=None,
                 lexical_stride=0, dense_weight=1.0) -> SearchDesc:
-    return SearchDesc(corpus, rescore if rescore is not None else StoreDesc(), ptr(queries), batch, k,
+    desc = SearchDesc(corpus, rescore if rescore is not None else StoreDesc(), ptr(queries), batch, k,
                       metric, int8_mode, ptr(mask), rescore_candidates, ptr(lex_offsets), ptr(lex_docs),
                       ptr(lex_weights), lex_doc_count, lex_vocab_size, ptr(query_terms), lexical_stride,
                       dense_weight)
+    # the nested StoreDesc fields are copied by value: carry their owners over as well
+    return _keep_alive(desc, *getattr(corpus, "_owners", []),
+                       *(getattr(rescore, "_owners", []) if rescore is not None else []),
+                       queries, mask, lex_offsets, lex_docs, lex_weights, query_terms)
 
 
 def search_workspace_bytes(desc: SearchDesc) -> int:
@@ -373,6 +390,16 @@ def search_workspace_bytes(desc: SearchDesc) -> int:
 def search_topk(desc: SearchDesc, workspace, workspace_bytes, out_idx, out_val, stream=None) -> None:
     call("zcgvs_search_topk", ctypes.byref(desc), ptr(workspace), workspace_bytes, ptr(out_idx),
          ptr(out_val), getattr(stream, "handle", stream))
+
+
+def search_topk_profiled(desc: SearchDesc, workspace, workspace_bytes, out_idx, out_val, stream,
+                         events: list, max_phases: int) -> int:
+    """zcgvs_search_topk recording events[2p], events[2p+1] around the scan of phase p."""
+    handles = (_vp * (2 * max_phases))(*[e.handle for e in events])
+    phases = _i32(0)
+    call("zcgvs_search_topk_profiled", ctypes.byref(desc), ptr(workspace), workspace_bytes, ptr(out_idx),
+         ptr(out_val), getattr(stream, "handle", stream), handles, max_phases, ctypes.byref(phases))
+    return phases.value
 
 
 def search_overflow_flags(desc: SearchDesc, workspace) -> int:

@@ -450,8 +450,11 @@ int zcgvs_search_overflow_flags(const zcgvs_search_desc* desc, void* d_workspace
     return clearError();
 }
 
-int zcgvs_search_topk(const zcgvs_search_desc* desc, void* d_workspace, std::size_t workspace_bytes,
-                      int* d_out_indices, float* d_out_values, zcgvs_stream_t stream) {
+namespace {
+
+int searchTopk(const zcgvs_search_desc* desc, void* d_workspace, std::size_t workspace_bytes,
+               int* d_out_indices, float* d_out_values, zcgvs_stream_t stream,
+               zcgvs_event_t* events, int max_phases, int* phases_out) {
     if (desc == nullptr) {
         return setError(ZCGVS_ERR_INVALID_ARGUMENT, "zcgvs: descriptor must not be null");
     }
@@ -489,6 +492,9 @@ int zcgvs_search_topk(const zcgvs_search_desc* desc, void* d_workspace, std::siz
     }
 
     if (plan.materialized) {
+        if (phases_out != nullptr) {
+            *phases_out = 0;
+        }
         status = runMaterialized(d, plan, ws, d_out_indices, d_out_values, s);
         return status == ZCGVS_OK ? clearError() : status;
     }
@@ -519,12 +525,22 @@ int zcgvs_search_topk(const zcgvs_search_desc* desc, void* d_workspace, std::siz
     std::uint64_t* tau = at<std::uint64_t>(ws, plan.tau);
     std::uint32_t* overflow = at<std::uint32_t>(ws, plan.overflow);
 
+    if (phases_out != nullptr) {
+        *phases_out = static_cast<int>(plan.phases.size());
+    }
     for (std::size_t p = 0; p < plan.phases.size(); ++p) {
         const PhaseArgs& phase = plan.phases[p];
+        const bool timed = events != nullptr && static_cast<int>(p) < max_phases;
+        if (timed) {
+            ZCGVS_HIP_RETURN(hipEventRecord(reinterpret_cast<hipEvent_t>(events[2 * p]), s));
+        }
         status = plan.use_mfma ? launchMfmaScan(scan, phase, emit, plan.workgroups, s)
                                : launchValuScan(scan, phase, emit, plan.workgroups, s);
         if (status != ZCGVS_OK) {
             return status;
+        }
+        if (timed) {
+            ZCGVS_HIP_RETURN(hipEventRecord(reinterpret_cast<hipEvent_t>(events[2 * p + 1]), s));
         }
         MergeInputs in;
         if (p == 0) {
@@ -569,6 +585,22 @@ int zcgvs_search_topk(const zcgvs_search_desc* desc, void* d_workspace, std::siz
         }
     }
     return clearError();
+}
+
+}  // namespace
+
+int zcgvs_search_topk(const zcgvs_search_desc* desc, void* d_workspace, std::size_t workspace_bytes,
+                      int* d_out_indices, float* d_out_values, zcgvs_stream_t stream) {
+    return searchTopk(desc, d_workspace, workspace_bytes, d_out_indices, d_out_values, stream,
+                      nullptr, 0, nullptr);
+}
+
+int zcgvs_search_topk_profiled(const zcgvs_search_desc* desc, void* d_workspace,
+                               std::size_t workspace_bytes, int* d_out_indices,
+                               float* d_out_values, zcgvs_stream_t stream, zcgvs_event_t* events,
+                               int max_phases, int* phases) {
+    return searchTopk(desc, d_workspace, workspace_bytes, d_out_indices, d_out_values, stream,
+                      events, max_phases, phases);
 }
 
 }  // extern "C"
