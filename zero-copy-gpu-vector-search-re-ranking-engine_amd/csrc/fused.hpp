@@ -35,12 +35,15 @@ struct EmitArgs {
     int seg_log2 = 0;
 };
 
-// First block of work item j of a phase.
+// First block of work item j of a phase: the j-th multiple of `stride` that is not a multiple
+// of stride * skip. Item counts and skips stay below 2^31, so the division is 32-bit.
 __device__ __forceinline__ long long phaseBlock(long long j, long long stride, long long skip) {
     if (skip == 0) {
         return j * stride;
     }
-    return (j + j / (skip - 1) + 1) * stride;
+    const std::uint32_t j32 = static_cast<std::uint32_t>(j);
+    const std::uint32_t visited = j32 + j32 / static_cast<std::uint32_t>(skip - 1) + 1u;
+    return static_cast<long long>(visited) * stride;
 }
 
 // Work items of a phase over `blocks` blocks.

@@ -207,6 +207,35 @@ __device__ __forceinline__ void forEachCandidate(const MergeInputs& in, int q, i
     }
 }
 
+// Appends `key` (when `take`) to the LDS array with one LDS atomic per wavefront. Every lane of
+// the wavefront must call it (uniform control flow).
+__device__ __forceinline__ void pushCompacted(std::uint64_t key, bool take, std::uint64_t* dst,
+                                              std::uint32_t* count, std::uint32_t capacity) {
+    const std::uint64_t ballot = __ballot(take);
+    if (ballot == 0ull) {
+        return;
+    }
+    const int lane = threadIdx.x & (kWave - 1);
+    const int leader = __ffsll(static_cast<unsigned long long>(ballot)) - 1;
+    std::uint32_t base = 0u;
+    if (lane == leader) {
+        base = atomicAdd(count, static_cast<std::uint32_t>(__popcll(ballot)));
+    }
+    base = __shfl(base, leader, kWave);
+    if (take) {
+        const std::uint32_t slot =
+            base + static_cast<std::uint32_t>(__popcll(ballot & ((1ull << lane) - 1ull)));
+        if (slot < capacity) {
+            dst[slot] = key;
+        }
+    }
+}
+
+// Candidate sets of up to kSelectLdsKeys keys are first compacted into LDS, so the radix passes
+// read LDS instead of re-walking the segments in global memory; larger sets take the same
+// passes over global memory.
+constexpr std::uint32_t kSelectLdsKeys = 12288;
+
 __global__ __launch_bounds__(kSelectThreads) void selectMergeKernel(
     MergeInputs in, int k, int batch, std::uint64_t* __restrict__ out_keys,
     std::uint64_t* __restrict__ threshold, std::uint32_t* __restrict__ overflow,
@@ -215,6 +244,7 @@ __global__ __launch_bounds__(kSelectThreads) void selectMergeKernel(
     __shared__ std::uint32_t lds_scan[kSelectThreads];
     __shared__ std::uint64_t lds_keys[kMaxK];
     __shared__ std::uint32_t lds_seg[kMaxSegments];
+    __shared__ std::uint64_t lds_cand[kSelectLdsKeys];
     __shared__ SelectState lds_state;
     __shared__ std::uint32_t lds_valid;
     __shared__ std::uint32_t lds_overflow;
@@ -223,6 +253,10 @@ __global__ __launch_bounds__(kSelectThreads) void selectMergeKernel(
     if (threadIdx.x == 0) {
         lds_valid = 0u;
         lds_overflow = 0u;
+        lds_state.prefix = 0ull;
+        lds_state.bits = 0u;
+        lds_state.need = static_cast<std::uint32_t>(k);
+        lds_state.count = 0u;
     }
     __syncthreads();
     const std::uint32_t cap = 1u << in.seg_log2;
@@ -235,21 +269,56 @@ __global__ __launch_bounds__(kSelectThreads) void selectMergeKernel(
     }
     __syncthreads();
 
-    std::uint32_t mine = 0;
-    forEachCandidate(in, q, batch, lds_seg, [&](std::uint64_t) { ++mine; });
-    atomicAdd(&lds_valid, mine);
-    if (threadIdx.x == 0) {
-        lds_state.prefix = 0ull;
-        lds_state.bits = 0u;
-        lds_state.need = static_cast<std::uint32_t>(k);
-        lds_state.count = 0u;
+    // ---- compaction of the non-zero keys (uniform loops: every lane reaches pushCompacted) ----
+    if (in.prev != nullptr) {
+        const std::uint64_t* prev = in.prev + static_cast<std::size_t>(q) * in.k_prev;
+        for (int i0 = 0; i0 < in.k_prev; i0 += blockDim.x) {
+            const int i = i0 + threadIdx.x;
+            const std::uint64_t key = i < in.k_prev ? prev[i] : 0ull;
+            pushCompacted(key, key != 0ull, lds_cand, &lds_valid, kSelectLdsKeys);
+        }
+    }
+    if (in.dense != nullptr) {
+        const std::uint64_t* dense = in.dense + static_cast<std::size_t>(q) * in.dense_stride;
+        for (long long i0 = 0; i0 < in.n_dense; i0 += blockDim.x) {
+            const long long i = i0 + threadIdx.x;
+            const std::uint64_t key = i < in.n_dense ? dense[i] : 0ull;
+            pushCompacted(key, key != 0ull, lds_cand, &lds_valid, kSelectLdsKeys);
+        }
+    }
+    if (in.seg != nullptr) {
+        const long long total = static_cast<long long>(in.n_seg) << in.seg_log2;
+        const long long slot_mask = (1LL << in.seg_log2) - 1;
+        for (long long i0 = 0; i0 < total; i0 += blockDim.x) {
+            const long long i = i0 + threadIdx.x;
+            std::uint64_t key = 0ull;
+            if (i < total) {
+                const int s = static_cast<int>(i >> in.seg_log2);
+                const long long j = i & slot_mask;
+                if (j < static_cast<long long>(lds_seg[s])) {
+                    key = in.seg[((static_cast<std::size_t>(s) * batch + q) << in.seg_log2) + j];
+                }
+            }
+            pushCompacted(key, key != 0ull, lds_cand, &lds_valid, kSelectLdsKeys);
+        }
     }
     __syncthreads();
     const std::uint32_t n_valid = lds_valid;
+    const bool in_lds = n_valid <= kSelectLdsKeys;
     if (threadIdx.x == 0) {
         lds_state.done = n_valid <= static_cast<std::uint32_t>(k) ? 1u : 0u;
     }
     __syncthreads();
+
+    auto forEachKey = [&](auto&& f) {
+        if (in_lds) {
+            for (std::uint32_t i = threadIdx.x; i < n_valid; i += blockDim.x) {
+                f(lds_cand[i]);
+            }
+        } else {
+            forEachCandidate(in, q, batch, lds_seg, f);
+        }
+    };
 
     for (int pass = 0; pass < kSelectPasses && !lds_state.done; ++pass) {
         const int width = selectDigitWidth(pass);
@@ -261,7 +330,7 @@ __global__ __launch_bounds__(kSelectThreads) void selectMergeKernel(
         const std::uint64_t prefix = lds_state.prefix;
         const int shift = 64 - static_cast<int>(bits) - width;
         const std::uint64_t digit_mask = (1ull << width) - 1ull;
-        forEachCandidate(in, q, batch, lds_seg, [&](std::uint64_t key) {
+        forEachKey([&](std::uint64_t key) {
             if (bits == 0u || (key >> (64 - bits)) == prefix) {
                 atomicAdd(&lds_hist[(key >> shift) & digit_mask], 1u);
             }
@@ -271,7 +340,7 @@ __global__ __launch_bounds__(kSelectThreads) void selectMergeKernel(
     }
 
     const std::uint64_t cut = n_valid <= static_cast<std::uint32_t>(k) ? 1ull : selectThreshold(lds_state);
-    forEachCandidate(in, q, batch, lds_seg, [&](std::uint64_t key) {
+    forEachKey([&](std::uint64_t key) {
         if (key >= cut) {
             const std::uint32_t slot = atomicAdd(&lds_state.count, 1u);
             if (slot < static_cast<std::uint32_t>(kMaxK)) {
