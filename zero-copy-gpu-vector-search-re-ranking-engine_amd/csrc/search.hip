@@ -69,6 +69,7 @@ struct Plan {
     std::vector<PhaseArgs> phases;
 
     // workspace offsets
+    std::size_t mscales = 0;  // MFMA path: row scales padded to whole tiles, NaN = masked/padding
     std::size_t qbits = 0, qi8 = 0, qscale = 0, lex = 0, lexmax = 0, dense = 0, seg = 0,
                 segcnt = 0, keys = 0, tau = 0, overflow = 0, rescored = 0, scores = 0, lexmat = 0,
                 topk_a = 0, topk_b = 0, topk_c = 0, topk_d = 0, cand_idx = 0, cand_val = 0,
@@ -190,6 +191,10 @@ ScanArgs scanArgsOf(const zcgvs_search_desc& d, const Plan& plan, std::uint8_t* 
     scan.queries = d.queries;
     if (plan.per_vector) {
         scan.row_scales = d.corpus.row_scales;
+        if (plan.use_mfma) {
+            scan.row_scales = ws != nullptr ? reinterpret_cast<const float*>(ws + plan.mscales) : nullptr;
+            scan.mask = nullptr;
+        }
         scan.queries = ws != nullptr ? ws + plan.qi8 : nullptr;
         scan.query_scales = ws != nullptr ? reinterpret_cast<const float*>(ws + plan.qscale) : nullptr;
     }
@@ -221,6 +226,7 @@ Plan makePlan(const zcgvs_search_desc& d) {
     }
     if (plan.per_vector) {
         probe.query_scales = reinterpret_cast<const float*>(static_cast<std::uintptr_t>(kAlign));
+        probe.mask = nullptr;  // an allow-mask is merged into the row scales for the MFMA scan
     }
     if (plan.hybrid) {
         probe.lexical = reinterpret_cast<const float*>(static_cast<std::uintptr_t>(kAlign));
@@ -239,6 +245,10 @@ Plan makePlan(const zcgvs_search_desc& d) {
     if (plan.per_vector) {
         plan.qi8 = layout.add(static_cast<std::size_t>(batch) * dim);
         plan.qscale = layout.add(static_cast<std::size_t>(batch) * 4);
+        if (plan.use_mfma) {
+            const long long tiles = (n + kMfmaBlockRows - 1) / kMfmaBlockRows;
+            plan.mscales = layout.add(static_cast<std::size_t>(tiles) * kMfmaBlockRows * 4);
+        }
     }
     plan.overflow = layout.add(static_cast<std::size_t>(batch) * 4);
 
@@ -407,6 +417,19 @@ int runMaterialized(const zcgvs_search_desc& d, const Plan& plan, std::uint8_t* 
     return zcgvs_launch_remap_indices(cand_idx, local, c, d.k, batch, out_idx, s);
 }
 
+// The MFMA scan's row scales: the corpus scales padded to `padded` rows, with NaN (its
+// masked-row marker) for rows the allow-mask excludes and for the padding.
+__global__ void mergeMaskedScalesKernel(const float* __restrict__ scales,
+                                        const std::uint8_t* __restrict__ mask, long long n,
+                                        long long padded, float* __restrict__ out) {
+    const long long stride = static_cast<long long>(gridDim.x) * blockDim.x;
+    for (long long i = static_cast<long long>(blockIdx.x) * blockDim.x + threadIdx.x; i < padded;
+         i += stride) {
+        const bool allowed = i < n && (mask == nullptr || mask[i] != 0);
+        out[i] = allowed ? scales[i] : __uint_as_float(0x7FC00000u);
+    }
+}
+
 __global__ void zeroWordsKernel(std::uint32_t* __restrict__ dst, std::size_t count) {
     const std::size_t stride = static_cast<std::size_t>(gridDim.x) * blockDim.x;
     for (std::size_t i = static_cast<std::size_t>(blockIdx.x) * blockDim.x + threadIdx.x;
@@ -510,6 +533,13 @@ int searchTopk(const zcgvs_search_desc* desc, void* d_workspace, std::size_t wor
     }
 
     // 3. phased scan + merge
+    if (plan.use_mfma) {
+        const long long n = d.corpus.doc_count;
+        const long long padded = (n + kMfmaBlockRows - 1) / kMfmaBlockRows * kMfmaBlockRows;
+        mergeMaskedScalesKernel<<<static_cast<unsigned>(std::min<long long>(8192, (padded + 255) / 256)), 256, 0, s>>>(
+            d.corpus.row_scales, d.mask, n, padded, at<float>(ws, plan.mscales));
+        ZCGVS_LAUNCH_CHECK("merge mask");
+    }
     const ScanArgs scan = scanArgsOf(d, plan, ws);
     if (plan.use_mfma && !mfmaSupported(scan)) {
         return setError(ZCGVS_ERR_INVALID_ARGUMENT, "zcgvs: corpus or queries are not 16-byte aligned");
