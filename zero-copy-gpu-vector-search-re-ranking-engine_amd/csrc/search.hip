@@ -30,7 +30,7 @@ bool valuSupported(const ScanArgs& scan);
 namespace {
 
 constexpr std::size_t kAlign = 256;
-constexpr long long kPhaseGrowth = 64;
+constexpr long long kPhaseGrowth = 8;
 
 std::size_t alignUp(std::size_t value) { return (value + kAlign - 1) / kAlign * kAlign; }
 

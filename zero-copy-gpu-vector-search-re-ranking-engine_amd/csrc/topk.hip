@@ -207,33 +207,11 @@ __device__ __forceinline__ void forEachCandidate(const MergeInputs& in, int q, i
     }
 }
 
-// Appends `key` (when `take`) to the LDS array with one LDS atomic per wavefront. Every lane of
-// the wavefront must call it (uniform control flow).
-__device__ __forceinline__ void pushCompacted(std::uint64_t key, bool take, std::uint64_t* dst,
-                                              std::uint32_t* count, std::uint32_t capacity) {
-    const std::uint64_t ballot = __ballot(take);
-    if (ballot == 0ull) {
-        return;
-    }
-    const int lane = threadIdx.x & (kWave - 1);
-    const int leader = __ffsll(static_cast<unsigned long long>(ballot)) - 1;
-    std::uint32_t base = 0u;
-    if (lane == leader) {
-        base = atomicAdd(count, static_cast<std::uint32_t>(__popcll(ballot)));
-    }
-    base = __shfl(base, leader, kWave);
-    if (take) {
-        const std::uint32_t slot =
-            base + static_cast<std::uint32_t>(__popcll(ballot & ((1ull << lane) - 1ull)));
-        if (slot < capacity) {
-            dst[slot] = key;
-        }
-    }
-}
-
-// Candidate sets of up to kSelectLdsKeys keys are first compacted into LDS, so the radix passes
+// Candidate sets of up to kSelectLdsKeys keys are first gathered into LDS, so the radix passes
 // read LDS instead of re-walking the segments in global memory; larger sets take the same
-// passes over global memory.
+// passes over global memory. The gather needs no load results to place a key: previous keys
+// and dense keys are copied as they lie (zero keys are skipped later), and segment j of
+// segment s goes to offset[s] + j, from the exclusive scan of the segment counts.
 constexpr std::uint32_t kSelectLdsKeys = 12288;
 
 __global__ __launch_bounds__(kSelectThreads) void selectMergeKernel(
@@ -243,14 +221,16 @@ __global__ __launch_bounds__(kSelectThreads) void selectMergeKernel(
     __shared__ std::uint32_t lds_hist[kSelectBins];
     __shared__ std::uint32_t lds_scan[kSelectThreads];
     __shared__ std::uint64_t lds_keys[kMaxK];
-    __shared__ std::uint32_t lds_seg[kMaxSegments];
+    __shared__ std::uint32_t lds_seg[kMaxSegments];     // valid count per segment
+    __shared__ std::uint32_t lds_offset[kMaxSegments];  // exclusive scan of lds_seg
     __shared__ std::uint64_t lds_cand[kSelectLdsKeys];
     __shared__ SelectState lds_state;
     __shared__ std::uint32_t lds_valid;
     __shared__ std::uint32_t lds_overflow;
 
     const int q = blockIdx.x;
-    if (threadIdx.x == 0) {
+    const int t = threadIdx.x;
+    if (t == 0) {
         lds_valid = 0u;
         lds_overflow = 0u;
         lds_state.prefix = 0ull;
@@ -260,7 +240,7 @@ __global__ __launch_bounds__(kSelectThreads) void selectMergeKernel(
     }
     __syncthreads();
     const std::uint32_t cap = 1u << in.seg_log2;
-    for (int s = threadIdx.x; s < in.n_seg; s += blockDim.x) {
+    for (int s = t; s < in.n_seg; s += blockDim.x) {
         const std::uint32_t c = in.seg_count[static_cast<std::size_t>(s) * batch + q];
         lds_seg[s] = min(c, cap);
         if (c > cap) {
@@ -268,61 +248,93 @@ __global__ __launch_bounds__(kSelectThreads) void selectMergeKernel(
         }
     }
     __syncthreads();
+    // Exclusive scan of the segment counts: thread t owns a contiguous run of segments.
+    const int per_thread = (in.n_seg + kSelectThreads - 1) / kSelectThreads;
+    std::uint32_t run = 0u;
+    for (int i = 0; i < per_thread; ++i) {
+        const int s = t * per_thread + i;
+        run += s < in.n_seg ? lds_seg[s] : 0u;
+    }
+    lds_scan[t] = run;
+    __syncthreads();
+    for (int offset = 1; offset < kSelectThreads; offset <<= 1) {
+        const std::uint32_t add = t >= offset ? lds_scan[t - offset] : 0u;
+        __syncthreads();
+        lds_scan[t] += add;
+        __syncthreads();
+    }
+    std::uint32_t acc = t == 0 ? 0u : lds_scan[t - 1];
+    for (int i = 0; i < per_thread; ++i) {
+        const int s = t * per_thread + i;
+        if (s < in.n_seg) {
+            lds_offset[s] = acc;
+            acc += lds_seg[s];
+        }
+    }
+    const std::uint32_t seg_total = lds_scan[kSelectThreads - 1];
+    const std::uint32_t k_prev = in.prev != nullptr ? static_cast<std::uint32_t>(in.k_prev) : 0u;
+    const std::uint32_t n_dense = in.dense != nullptr ? static_cast<std::uint32_t>(in.n_dense) : 0u;
+    const std::uint64_t gathered = static_cast<std::uint64_t>(k_prev) + n_dense + seg_total;
+    const bool in_lds = gathered <= kSelectLdsKeys;
+    __syncthreads();
 
-    // ---- compaction of the non-zero keys (uniform loops: every lane reaches pushCompacted) ----
-    if (in.prev != nullptr) {
-        const std::uint64_t* prev = in.prev + static_cast<std::size_t>(q) * in.k_prev;
-        for (int i0 = 0; i0 < in.k_prev; i0 += blockDim.x) {
-            const int i = i0 + threadIdx.x;
-            const std::uint64_t key = i < in.k_prev ? prev[i] : 0ull;
-            pushCompacted(key, key != 0ull, lds_cand, &lds_valid, kSelectLdsKeys);
+    if (in_lds) {
+        if (k_prev > 0u) {
+            const std::uint64_t* prev = in.prev + static_cast<std::size_t>(q) * in.k_prev;
+            for (std::uint32_t i = t; i < k_prev; i += blockDim.x) {
+                lds_cand[i] = prev[i];
+            }
         }
-    }
-    if (in.dense != nullptr) {
-        const std::uint64_t* dense = in.dense + static_cast<std::size_t>(q) * in.dense_stride;
-        for (long long i0 = 0; i0 < in.n_dense; i0 += blockDim.x) {
-            const long long i = i0 + threadIdx.x;
-            const std::uint64_t key = i < in.n_dense ? dense[i] : 0ull;
-            pushCompacted(key, key != 0ull, lds_cand, &lds_valid, kSelectLdsKeys);
+        if (n_dense > 0u) {
+            const std::uint64_t* dense = in.dense + static_cast<std::size_t>(q) * in.dense_stride;
+            for (std::uint32_t i = t; i < n_dense; i += blockDim.x) {
+                lds_cand[k_prev + i] = dense[i];
+            }
         }
-    }
-    if (in.seg != nullptr) {
-        const long long total = static_cast<long long>(in.n_seg) << in.seg_log2;
-        const long long slot_mask = (1LL << in.seg_log2) - 1;
-        for (long long i0 = 0; i0 < total; i0 += blockDim.x) {
-            const long long i = i0 + threadIdx.x;
-            std::uint64_t key = 0ull;
-            if (i < total) {
+        if (in.seg != nullptr) {
+            const std::uint32_t base = k_prev + n_dense;
+            const long long total = static_cast<long long>(in.n_seg) << in.seg_log2;
+            const long long slot_mask = (1LL << in.seg_log2) - 1;
+#pragma unroll 4
+            for (long long i = t; i < total; i += blockDim.x) {
                 const int s = static_cast<int>(i >> in.seg_log2);
-                const long long j = i & slot_mask;
-                if (j < static_cast<long long>(lds_seg[s])) {
-                    key = in.seg[((static_cast<std::size_t>(s) * batch + q) << in.seg_log2) + j];
+                const std::uint32_t j = static_cast<std::uint32_t>(i & slot_mask);
+                if (j < lds_seg[s]) {
+                    lds_cand[base + lds_offset[s] + j] =
+                        in.seg[((static_cast<std::size_t>(s) * batch + q) << in.seg_log2) + j];
                 }
             }
-            pushCompacted(key, key != 0ull, lds_cand, &lds_valid, kSelectLdsKeys);
         }
-    }
-    __syncthreads();
-    const std::uint32_t n_valid = lds_valid;
-    const bool in_lds = n_valid <= kSelectLdsKeys;
-    if (threadIdx.x == 0) {
-        lds_state.done = n_valid <= static_cast<std::uint32_t>(k) ? 1u : 0u;
     }
     __syncthreads();
 
     auto forEachKey = [&](auto&& f) {
         if (in_lds) {
-            for (std::uint32_t i = threadIdx.x; i < n_valid; i += blockDim.x) {
-                f(lds_cand[i]);
+            const std::uint32_t n = static_cast<std::uint32_t>(gathered);
+            for (std::uint32_t i = t; i < n; i += blockDim.x) {
+                const std::uint64_t key = lds_cand[i];
+                if (key != 0ull) {
+                    f(key);
+                }
             }
         } else {
             forEachCandidate(in, q, batch, lds_seg, f);
         }
     };
 
+    std::uint32_t mine = 0u;
+    forEachKey([&](std::uint64_t) { ++mine; });
+    atomicAdd(&lds_valid, mine);
+    __syncthreads();
+    const std::uint32_t n_valid = lds_valid;
+    if (t == 0) {
+        lds_state.done = n_valid <= static_cast<std::uint32_t>(k) ? 1u : 0u;
+    }
+    __syncthreads();
+
     for (int pass = 0; pass < kSelectPasses && !lds_state.done; ++pass) {
         const int width = selectDigitWidth(pass);
-        for (int i = threadIdx.x; i < (1 << width); i += blockDim.x) {
+        for (int i = t; i < (1 << width); i += blockDim.x) {
             lds_hist[i] = 0u;
         }
         __syncthreads();
@@ -354,21 +366,21 @@ __global__ __launch_bounds__(kSelectThreads) void selectMergeKernel(
     while (padded < k) {
         padded <<= 1;
     }
-    for (int i = static_cast<int>(taken) + threadIdx.x; i < padded; i += blockDim.x) {
+    for (int i = static_cast<int>(taken) + t; i < padded; i += blockDim.x) {
         lds_keys[i] = 0ull;
     }
     __syncthreads();
     bitonicSortDescending(lds_keys, padded);
 
     std::uint64_t* dst = out_keys + static_cast<std::size_t>(q) * k;
-    for (int i = threadIdx.x; i < k; i += blockDim.x) {
+    for (int i = t; i < k; i += blockDim.x) {
         dst[i] = lds_keys[i];
         if (out_index != nullptr) {
             const std::size_t o = static_cast<std::size_t>(q) * k + i;
             writeHit(lds_keys[i], &out_index[o], &out_score[o]);
         }
     }
-    if (threadIdx.x == 0) {
+    if (t == 0) {
         if (threshold != nullptr) {
             threshold[q] = taken >= static_cast<std::uint32_t>(k) ? lds_keys[k - 1] : 0ull;
         }
