@@ -6,8 +6,14 @@
 //
 // Work split. A workgroup is 8 wavefronts, two per SIMD. Wavefront w keeps the int8 rows of its
 // 32 queries in registers for the whole launch, as v_mfma_i32_32x32x32_i8 B operands
-// (query-stationary), so one workgroup covers 256 queries; the two wavefronts of a SIMD hide each
-// other's LDS latency and epilogue work behind their MFMAs.
+// (query-stationary), so one workgroup covers 256 queries.
+//
+// Skew. Of the two wavefronts of a SIMD (chosen at start-up from the hardware SIMD id) one leads
+// and one lags: after the tile barrier the leader multiplies tile t and then filters it, while
+// the lagger first filters tile t - 1 and then multiplies tile t. So each wavefront's VALU filter
+// work runs while the other keeps the SIMD's matrix core busy. A filter that passes owes an exact
+// pass; that pass runs right after the next barrier, before that step's tile copies are issued,
+// so candidate stores never sit behind later tile copies in the vmcnt order.
 //
 // Corpus streaming. Tiles of 64 rows go from HBM straight into a ring of LDS buffers with
 // global_load_lds_dwordx4 (no staging registers), kDepth - 1 tiles ahead of the one being
@@ -22,19 +28,22 @@
 // every dimension exactly once whatever order the hardware walks K in. D: lane l holds column
 // l % 32 (the query) and rows 8 * (r / 4) + 4 * (l / 32) + r % 4 for its 16 results r.
 //
-// LDS tile layout: row r at r * dim bytes; its 16-byte slot s is stored at slot s ^ (r & 7), so
-// the rows one A-operand read touches spread over the banks. The copy instruction writes 64
-// consecutive LDS slots, so each lane computes which global 16 bytes belong to its LDS slot.
+// LDS tile layout: row r at r * dim bytes; its 16-byte slot s is stored at slot s ^ swizzle(r).
+// The LDS serves 64 banks x 4 bytes per clock, and ds_read_b128 serves 16 lanes at a time; the 16
+// lanes of one A-operand read hit 16 consecutive rows at the same slot, so swizzle(r) must send
+// those rows to 16 different 16-byte bank groups: r & 15 when a row is a whole number of bank
+// periods (dim % 256 == 0), (r >> 1) & 7 when it is an odd number of half periods (dim 384). A
+// swizzle of r & 7 leaves a 2-way conflict that halves the read rate. The copy instruction writes
+// 64 consecutive LDS slots, so each lane computes which global 16 bytes belong to its LDS slot.
 //
-// Row scales ride along inside the same ring slot (16 lanes of one more 16-byte copy per tile;
-// keeping every copy inside one LDS object keeps the compiler from waiting on the in-flight
-// copies before each LDS read). They come from a workspace copy of the scales padded to whole
-// tiles, in which masked and padding rows hold NaN; such a row scores -FLT_MAX.
+// Row scales travel in a ring of their own, one deeper than the tile ring, so the scales of tile
+// t - 1 stay readable through step t. They come from a workspace copy of the scales padded to
+// whole tiles, in which masked and padding rows hold NaN; such a row scores -FLT_MAX.
 //
-// Epilogue of a threshold phase: per lane the largest (float)dot * s_r of the tile is compared
-// with the query's threshold score minus a relative margin of 2^-20 (far above the few-ulp
-// difference between that product order and the exact score's); only when some lane passes is
-// the exact score, its key and the key comparison evaluated.
+// Filter of a threshold phase: per lane the largest (float)dot * s_r of the tile is compared with
+// the query's threshold score minus a relative margin of 2^-20 (far above the few-ulp difference
+// between that product order and the exact score's); only when some lane passes is the exact
+// score, its key and the key comparison evaluated.
 #include <hip/hip_runtime.h>
 
 #include <algorithm>
@@ -66,18 +75,44 @@ __device__ __forceinline__ std::uint32_t ldsAddress(const void* p) {
 // One global_load_lds_dwordx4: every active lane copies 16 bytes from `src` to LDS at
 // lds_base + 16 * lane. Issued as inline assembly so that the compiler, which cannot tell the
 // ring slots apart, does not make every later LDS read wait for all copies in flight; the
-// kernel orders the copies itself (vmcnt waits + barriers). M0 carries the LDS base.
+// kernel orders the copies itself (vmcnt waits + barriers). M0 carries the LDS base (bound as
+// an operand, so the compiler writes it); the s_nop is the wait state an M0 write needs before
+// an LDS DMA instruction.
 __device__ __forceinline__ void copyToLds(const void* src, std::uint32_t lds_base) {
-    asm volatile("s_mov_b32 m0, %1\n\ts_nop 0\n\tglobal_load_lds_dwordx4 %0, off"
+    asm volatile("s_nop 0\n\tglobal_load_lds_dwordx4 %0, off"
                  :
-                 : "v"(src), "s"(lds_base)
-                 : "memory", "m0");
+                 : "v"(src), "{m0}"(lds_base)
+                 : "memory");
 }
 
 // s_waitcnt that waits until at most n vector-memory operations of this wavefront are pending
 // (expcnt and lgkmcnt fields at their "no wait" maxima).
 __device__ constexpr int vmcntOnly(int n) {
     return (n & 0xF) | (0x7 << 4) | (0xF << 8) | ((n >> 4) << 14);
+}
+
+// Waits until at most `later * kPerTile` copies are pending (later <= kMaxLater, wave-uniform).
+template <int kPerTile, int kMaxLater>
+__device__ __forceinline__ void waitTiles(int later) {
+    if constexpr (kMaxLater >= 2) {
+        if (later >= 2) {
+            __builtin_amdgcn_s_waitcnt(vmcntOnly(2 * kPerTile));
+            return;
+        }
+    }
+    if constexpr (kMaxLater >= 1) {
+        if (later == 1) {
+            __builtin_amdgcn_s_waitcnt(vmcntOnly(kPerTile));
+            return;
+        }
+    }
+    __builtin_amdgcn_s_waitcnt(vmcntOnly(0));
+}
+
+// SIMD of the calling wavefront (HW_ID register, SIMD_ID field: bits 5:4).
+__device__ __forceinline__ int simdId() {
+    constexpr int kHwId = 4;
+    return __builtin_amdgcn_s_getreg(((2 - 1) << 11) | (4 << 6) | kHwId) & 3;
 }
 
 template <int kKSteps, bool kDense>
@@ -87,13 +122,21 @@ void mfmaScanKernel(ScanArgs scan, PhaseArgs phase, EmitArgs emit, int q_offset,
     constexpr int kSlotsPerRow = kDim / 16;
     constexpr int kTileBytes = kRows * kDim;
     constexpr int kDepth = 3 * kTileBytes <= static_cast<int>(kRingBudget) ? 3 : 2;
+    constexpr int kScaleDepth = kDepth + 1;
     constexpr int kCopies = kRows * kSlotsPerRow / (kWave * kWaves);  // 16-byte copies per lane
     static_assert(kRows * kSlotsPerRow % (kWave * kWaves) == 0, "tile must split over the waves");
     static_assert(kSlotsPerRow % 8 == 0, "swizzle stays inside a row");
+    // swizzle period in slots (the swizzle permutes slots inside aligned groups of this size)
+    constexpr int kSwzSlots = kSlotsPerRow % 16 == 0 ? 16 : 8;
+    auto swizzle = [](int row) {
+        return kSlotsPerRow % 16 == 0 ? (row & 15) : (kSlotsPerRow % 16 == 8 ? ((row >> 1) & 7) : (row & 7));
+    };
+    static_assert(2 * (kCopies + 1) < 64, "copies in flight fit the vmcnt counter");
 
-    constexpr int kSlotBytes = kTileBytes + kRows * 4;  // tile, then its 64 row scales
-    __shared__ __attribute__((aligned(16))) std::uint8_t ring[kDepth][kSlotBytes];
+    __shared__ __attribute__((aligned(16))) std::uint8_t ring[kDepth][kTileBytes];
+    __shared__ __attribute__((aligned(16))) float scale_ring[kScaleDepth][kRows];
     __shared__ std::uint32_t lds_count[kQueriesPerLaunch];
+    __shared__ std::uint32_t lds_simd[4];
 
     const int tid = threadIdx.x;
     const int lane = tid & (kWave - 1);
@@ -132,33 +175,52 @@ void mfmaScanKernel(ScanArgs scan, PhaseArgs phase, EmitArgs emit, int q_offset,
     for (int i = tid; i < kQueriesPerLaunch; i += kThreads) {
         lds_count[i] = 0u;
     }
+    if (tid < 4) {
+        lds_simd[tid] = 0u;
+    }
 
-    // ---- per-lane copy plan: LDS slot P of the tile holds global slot (P % spr) ^ (row & 7) ----
-    int copy_row[kCopies];
-    int copy_col[kCopies];
+    // ---- per-lane copy plan: LDS slot P of the tile holds global slot (P % spr) ^ swizzle(row).
+    //      The tile-relative source offsets (< 64 KiB) are kept two to a register. ----
+    static_assert(kTileBytes <= 65536, "copy offsets fit 16 bits");
+    constexpr int kPacked = (kCopies + 1) / 2;
+    std::uint32_t copy_pk[kPacked];
+#pragma unroll
+    for (int i = 0; i < kPacked; ++i) {
+        copy_pk[i] = 0u;
+    }
 #pragma unroll
     for (int i = 0; i < kCopies; ++i) {
         const int p = (wave * kCopies + i) * kWave + lane;
         const int row = p / kSlotsPerRow;
         const int ls = p - row * kSlotsPerRow;
-        copy_row[i] = row;
-        copy_col[i] = (ls ^ (row & 7)) * 16;
+        copy_pk[i / 2] |= static_cast<std::uint32_t>(row * kDim + (ls ^ swizzle(row)) * 16) << (16 * (i % 2));
     }
-    auto issue = [&](long long item, int slot) {
+    auto issue = [&](long long item, int slot, int sslot) {
         const long long row0 = phaseBlock(item, phase.stride, phase.skip) * kRows;
-        const int valid_rows = static_cast<int>(min(static_cast<long long>(kRows), doc_count - row0));
         const std::uint8_t* base = corpus + static_cast<std::size_t>(row0) * kDim;
         const std::uint32_t slot_base = ldsAddress(&ring[slot][0]);
+        if (row0 + kRows <= doc_count) {
 #pragma unroll
-        for (int i = 0; i < kCopies; ++i) {
-            const int row = min(copy_row[i], valid_rows - 1);  // tail rows re-read the last row
-            copyToLds(base + row * kDim + copy_col[i],
-                      __builtin_amdgcn_readfirstlane(slot_base + (wave * kCopies + i) * kWave * 16));
+            for (int i = 0; i < kCopies; ++i) {
+                const int off = static_cast<int>((copy_pk[i / 2] >> (16 * (i % 2))) & 0xFFFFu);
+                copyToLds(base + off,
+                          __builtin_amdgcn_readfirstlane(slot_base + (wave * kCopies + i) * kWave * 16));
+            }
+        } else {
+            // tail tile: rows past the corpus re-read its last row (their scales are NaN)
+            const int last = static_cast<int>(doc_count - row0) - 1;
+#pragma unroll
+            for (int i = 0; i < kCopies; ++i) {
+                const int off = static_cast<int>((copy_pk[i / 2] >> (16 * (i % 2))) & 0xFFFFu);
+                const int row = off / kDim;
+                copyToLds(base + off - (row - min(row, last)) * kDim,
+                          __builtin_amdgcn_readfirstlane(slot_base + (wave * kCopies + i) * kWave * 16));
+            }
         }
         if (wave == 0 && lane < kRows / 4) {
             // the padded scale copy makes rows row0 .. row0 + 63 readable for every tile
             copyToLds(scan.row_scales + row0 + 4 * lane,
-                      __builtin_amdgcn_readfirstlane(slot_base + kTileBytes));
+                      __builtin_amdgcn_readfirstlane(ldsAddress(&scale_ring[sslot][0])));
         }
     };
 
@@ -169,63 +231,101 @@ void mfmaScanKernel(ScanArgs scan, PhaseArgs phase, EmitArgs emit, int q_offset,
     for (int d = 0; d < kDepth - 1; ++d) {
         const long long ahead = item + d * stride_items;
         if (ahead < phase.items) {
-            issue(ahead, d);
+            issue(ahead, d, d);
         }
     }
-    __syncthreads();  // lds_count initialization visible
+    __syncthreads();  // lds_count and lds_simd initialization visible
 
-    const int a_base0 = col * kDim;
-    const int a_base1 = (32 + col) * kDim;
-    const int swz = col & 7;
-
-    int slot = 0;
-    for (; item < phase.items; item += stride_items) {
-        // Wait for this wavefront's copies of the current tile: the ones issued after it belong
-        // to the (at most kDepth - 2) later tiles already in flight.
-        const long long in_flight = min(static_cast<long long>(kDepth - 2),
-                                        (phase.items - 1 - item) / stride_items);
-        if (in_flight >= 2) {
-            __builtin_amdgcn_s_waitcnt(vmcntOnly(2 * kCopies));
-        } else if (in_flight == 1) {
-            __builtin_amdgcn_s_waitcnt(vmcntOnly(kCopies));
+    // Waits for this wavefront's copies of tile `item` (the ones issued after it belong to the at
+    // most kDepth - 2 later tiles already in flight) and meets the other wavefronts.
+    auto arrive = [&](long long it) {
+        int later = 0;
+#pragma unroll
+        for (int d = 1; d <= kDepth - 2; ++d) {
+            later += it + d * stride_items < phase.items ? 1 : 0;
+        }
+        if (wave == 0) {
+            waitTiles<kCopies + 1, kDepth - 2>(later);
         } else {
-            __builtin_amdgcn_s_waitcnt(vmcntOnly(0));
+            waitTiles<kCopies, kDepth - 2>(later);
         }
         __builtin_amdgcn_s_barrier();
         asm volatile("" ::: "memory");  // no LDS access moves above the barrier
-        {
-            // Refill the buffer every wavefront finished reading before the barrier.
-            const long long ahead = item + (kDepth - 1) * stride_items;
-            if (ahead < phase.items) {
-                issue(ahead, (slot + kDepth - 1) % kDepth);
+    };
+    // Refills the ring slot every wavefront finished reading before the barrier.
+    auto refill = [&](long long it, int slot, int sslot) {
+        const long long ahead = it + (kDepth - 1) * stride_items;
+        if (ahead < phase.items) {
+            issue(ahead, slot == 0 ? kDepth - 1 : slot - 1,
+                  sslot + kDepth - 1 >= kScaleDepth ? sslot + kDepth - 1 - kScaleDepth : sslot + kDepth - 1);
+        }
+    };
+
+    // A-fragment addresses. Slot 2 ks + half of row col sits at slot (2 ks + half) ^ swizzle(col)
+    // = kSwzSlots (ks / kPeriod) + ((2 (ks % kPeriod) + half) ^ swizzle(col)) with kPeriod =
+    // kSwzSlots / 2 k-steps: kPeriod lane-dependent byte offsets; the rest is an immediate (and 32
+    // dim bytes for rows 32..63, whose swizzle equals that of rows 0..31).
+    constexpr int kPeriod = kSwzSlots / 2;
+    std::uint32_t a_off[kPeriod];
+#pragma unroll
+    for (int m = 0; m < kPeriod; ++m) {
+        a_off[m] = static_cast<std::uint32_t>(col * kDim + 16 * ((2 * m + half) ^ swizzle(col)));
+    }
+    // acc0 = rows 0..31 of the tile x the wavefront's 32 queries, acc1 = rows 32..63. The A
+    // fragments run kAhead k-steps ahead of the MFMAs that use them, and the schedule is pinned
+    // (reads, then per k-step two MFMAs and the reads kAhead steps further on) so an MFMA never
+    // waits on an LDS read issued just before it.
+    constexpr int kAhead = kKSteps < 3 ? kKSteps : 3;
+    auto multiply = [&](const std::uint8_t* tile, v16i& acc0, v16i& acc1) {
+        const std::uint8_t* lane_tile[kPeriod];
+#pragma unroll
+        for (int m = 0; m < kPeriod; ++m) {
+            lane_tile[m] = tile + a_off[m];
+        }
+        auto fragment = [&](int ks, int half_rows) {
+            return *reinterpret_cast<const v4i*>(lane_tile[ks % kPeriod] + 16 * kSwzSlots * (ks / kPeriod) +
+                                                 half_rows * 32 * kDim);
+        };
+        acc0 = v16i{};
+        acc1 = v16i{};
+        v4i a[kAhead + 1][2];
+#pragma unroll
+        for (int ks = 0; ks < kAhead; ++ks) {
+            a[ks][0] = fragment(ks, 0);
+            a[ks][1] = fragment(ks, 1);
+        }
+#pragma unroll
+        for (int ks = 0; ks < kKSteps; ++ks) {
+            if (ks + kAhead < kKSteps) {
+                a[(ks + kAhead) % (kAhead + 1)][0] = fragment(ks + kAhead, 0);
+                a[(ks + kAhead) % (kAhead + 1)][1] = fragment(ks + kAhead, 1);
+            }
+            acc0 = __builtin_amdgcn_mfma_i32_32x32x32_i8(a[ks % (kAhead + 1)][0], qf[ks], acc0, 0, 0, 0);
+            acc1 = __builtin_amdgcn_mfma_i32_32x32x32_i8(a[ks % (kAhead + 1)][1], qf[ks], acc1, 0, 0, 0);
+        }
+        // pinned order: 2 * kAhead LDS reads, then per k-step 2 MFMAs (+ 2 reads while any remain)
+        __builtin_amdgcn_sched_group_barrier(0x100, 2 * kAhead, 0);
+#pragma unroll
+        for (int ks = 0; ks < kKSteps; ++ks) {
+            __builtin_amdgcn_sched_group_barrier(0x008, 2, 0);
+            if (ks + kAhead < kKSteps) {
+                __builtin_amdgcn_sched_group_barrier(0x100, 2, 0);
             }
         }
-        const long long row0 = phaseBlock(item, phase.stride, phase.skip) * kRows;
+    };
 
-        if (wave_active) {
-            v16i acc0 = {};
-            v16i acc1 = {};
-            const std::uint8_t* tile = ring[slot];
-            v4i a_cur0 = *reinterpret_cast<const v4i*>(tile + a_base0 + ((half ^ swz) << 4));
-            v4i a_cur1 = *reinterpret_cast<const v4i*>(tile + a_base1 + ((half ^ swz) << 4));
-#pragma unroll
-            for (int ks = 0; ks < kKSteps; ++ks) {
-                v4i a_next0 = a_cur0;
-                v4i a_next1 = a_cur1;
-                if (ks + 1 < kKSteps) {
-                    const int s = ((2 * (ks + 1) + half) ^ swz) << 4;
-                    a_next0 = *reinterpret_cast<const v4i*>(tile + a_base0 + s);
-                    a_next1 = *reinterpret_cast<const v4i*>(tile + a_base1 + s);
-                }
-                acc0 = __builtin_amdgcn_mfma_i32_32x32x32_i8(a_cur0, qf[ks], acc0, 0, 0, 0);
-                acc1 = __builtin_amdgcn_mfma_i32_32x32x32_i8(a_cur1, qf[ks], acc1, 0, 0, 0);
-                a_cur0 = a_next0;
-                a_cur1 = a_next1;
-            }
-
-            // ---- epilogue ----
-            const float* scales = reinterpret_cast<const float*>(tile + kTileBytes);
-            if constexpr (kDense) {
+    int slot = 0;
+    int sslot = 0;
+    if constexpr (kDense) {
+        for (; item < phase.items; item += stride_items) {
+            arrive(item);
+            refill(item, slot, sslot);
+            if (wave_active) {
+                v16i acc0;
+                v16i acc1;
+                multiply(ring[slot], acc0, acc1);
+                const long long row0 = phaseBlock(item, phase.stride, phase.skip) * kRows;
+                const float* scales = scale_ring[sslot];
                 if (q_valid) {
                     std::uint64_t* dst = emit.dense + static_cast<std::size_t>(q) * emit.dense_stride + item * kRows;
 #pragma unroll
@@ -246,53 +346,105 @@ void mfmaScanKernel(ScanArgs scan, PhaseArgs phase, EmitArgs emit, int q_offset,
                         }
                     }
                 }
-            } else {
-                float best = -INFINITY;
+            }
+            slot = slot + 1 == kDepth ? 0 : slot + 1;
+            sslot = sslot + 1 == kScaleDepth ? 0 : sslot + 1;
+        }
+    } else {
+        // leader election: the first wavefront to arrive on each SIMD leads
+        bool lead = true;
+        {
+            std::uint32_t rank = 0u;
+            if (lane == 0) {
+                rank = atomicAdd(&lds_simd[simdId()], 1u);
+            }
+            lead = __builtin_amdgcn_readfirstlane(rank) == 0u;
+        }
+
+        // Filter: does any row of the tile in (acc0, acc1) reach this lane's threshold?
+        auto filter = [&](const v16i& acc0, const v16i& acc1, const float* scales) {
+            float best = -INFINITY;
 #pragma unroll
-                for (int mb = 0; mb < 2; ++mb) {
+            for (int mb = 0; mb < 2; ++mb) {
 #pragma unroll
-                    for (int g = 0; g < 4; ++g) {
-                        const int rl0 = mb * 32 + 8 * g + 4 * half;
-                        const float4 rs = *reinterpret_cast<const float4*>(scales + rl0);
-                        const float rsv[4] = {rs.x, rs.y, rs.z, rs.w};
+                for (int g = 0; g < 4; ++g) {
+                    const float4 rs = *reinterpret_cast<const float4*>(scales + mb * 32 + 8 * g + 4 * half);
+                    const float rsv[4] = {rs.x, rs.y, rs.z, rs.w};
 #pragma unroll
-                        for (int j = 0; j < 4; ++j) {
-                            const int dot = mb == 0 ? acc0[4 * g + j] : acc1[4 * g + j];
-                            best = fmaxf(best, static_cast<float>(dot) * rsv[j]);  // NaN (masked) ignored
-                        }
+                    for (int j = 0; j < 4; ++j) {
+                        const int dot = mb == 0 ? acc0[4 * g + j] : acc1[4 * g + j];
+                        best = fmaxf(best, static_cast<float>(dot) * rsv[j]);  // NaN (masked) ignored
                     }
                 }
-                const bool pass = q_valid && best * qscale >= tau_floor;
-                if (__any(pass)) {
+            }
+            return q_valid && best * qscale >= tau_floor;
+        };
+        // Exact scores and keys of the tile in (acc0, acc1); keys above the threshold are appended.
+        auto exact = [&](const v16i& acc0, const v16i& acc1, const float* scales, long long row0) {
+            // Tile-relative rows in 32 bits; the empty asm keeps the compiler from hoisting the
+            // 32 per-row constants out of the scan loop into registers.
+            int hb = 4 * half;
+            asm volatile("" : "+v"(hb));
+            const int valid_rows = static_cast<int>(min(static_cast<long long>(kRows), doc_count - row0));
+            const std::uint32_t row_base = static_cast<std::uint32_t>(row0);
 #pragma unroll
-                    for (int mb = 0; mb < 2; ++mb) {
+            for (int mb = 0; mb < 2; ++mb) {
 #pragma unroll
-                        for (int g = 0; g < 4; ++g) {
-                            const int rl0 = mb * 32 + 8 * g + 4 * half;
-                            const float4 rs = *reinterpret_cast<const float4*>(scales + rl0);
-                            const float rsv[4] = {rs.x, rs.y, rs.z, rs.w};
+                for (int g = 0; g < 4; ++g) {
+                    const int rl0 = mb * 32 + 8 * g + hb;
+                    const float4 rs = *reinterpret_cast<const float4*>(scales + rl0);
+                    const float rsv[4] = {rs.x, rs.y, rs.z, rs.w};
 #pragma unroll
-                            for (int j = 0; j < 4; ++j) {
-                                const long long row = row0 + rl0 + j;
-                                const int dot = mb == 0 ? acc0[4 * g + j] : acc1[4 * g + j];
-                                const float combined = qscale * rsv[j];
-                                const float score = rsv[j] == rsv[j] ? static_cast<float>(dot) * combined : kMaskedScore;
-                                if (q_valid && row < doc_count && score >= tau_floor) {
-                                    const std::uint64_t key = makeKey(score, static_cast<std::uint32_t>(row));
-                                    if (key > tau) {
-                                        appendCandidate(emit, lds_count, q, q_offset, batch, key);
-                                    }
-                                }
+                    for (int j = 0; j < 4; ++j) {
+                        const int rl = rl0 + j;
+                        const int dot = mb == 0 ? acc0[4 * g + j] : acc1[4 * g + j];
+                        const float combined = qscale * rsv[j];
+                        const float score = rsv[j] == rsv[j] ? static_cast<float>(dot) * combined : kMaskedScore;
+                        if (q_valid && rl < valid_rows && score >= tau_floor) {
+                            const std::uint64_t key = makeKey(score, row_base + static_cast<std::uint32_t>(rl));
+                            if (key > tau) {
+                                appendCandidate(emit, lds_count, q, q_offset, batch, key);
                             }
                         }
                     }
                 }
             }
-        }
-        slot = (slot + 1) % kDepth;
-    }
+        };
 
-    if constexpr (!kDense) {
+        v16i acc0 = {};
+        v16i acc1 = {};
+        long long acc_row0 = -1;  // first row of the tile in (acc0, acc1); -1 = none yet
+        int acc_sslot = 0;
+        bool owed = false;        // the tile in (acc0, acc1) passed its filter: exact pass owed
+        for (; item < phase.items; item += stride_items) {
+            arrive(item);
+            if (wave_active && !lead && acc_row0 >= 0) {
+                owed = filter(acc0, acc1, scale_ring[acc_sslot]);
+            }
+            if (__any(owed)) {
+                exact(acc0, acc1, scale_ring[acc_sslot], acc_row0);
+            }
+            owed = false;
+            refill(item, slot, sslot);
+            if (wave_active) {
+                multiply(ring[slot], acc0, acc1);
+                acc_row0 = phaseBlock(item, phase.stride, phase.skip) * kRows;
+                acc_sslot = sslot;
+                if (lead) {
+                    owed = filter(acc0, acc1, scale_ring[sslot]);
+                }
+            }
+            slot = slot + 1 == kDepth ? 0 : slot + 1;
+            sslot = sslot + 1 == kScaleDepth ? 0 : sslot + 1;
+        }
+        // the last tile
+        if (wave_active && !lead && acc_row0 >= 0) {
+            owed = filter(acc0, acc1, scale_ring[acc_sslot]);
+        }
+        if (__any(owed)) {
+            exact(acc0, acc1, scale_ring[acc_sslot], acc_row0);
+        }
+
         __syncthreads();
         for (int i = tid; i < q_count; i += kThreads) {
             emit.seg_count[static_cast<std::size_t>(blockIdx.x) * batch + q_offset + i] = lds_count[i];
