@@ -110,10 +110,35 @@ def build_inputs(capi, w):
     return desc, corpus, queries, keep
 
 
-def algorithmic_bytes(w):
-    n, dim, batch = w["n"], w["dim"], w["batch"]
-    per_row = {"i8i8": dim + 4, "f32": dim * 4, "f16": dim * 2, "binary": (dim + 31) // 32 * 4}[w["kind"]]
-    return n * per_row + batch * dim * 4
+def row_bytes(w):
+    """Algorithmic HBM bytes per corpus row a scan reads (row + its per-row scale)."""
+    dim = w["dim"]
+    return {"i8i8": dim + 4, "f32": dim * 4, "f16": dim * 2, "binary": (dim + 31) // 32 * 4}[w["kind"]]
+
+
+def query_bytes(w):
+    """Bytes of the (device-prepared) queries one scan launch reads."""
+    dim, batch = w["dim"], w["batch"]
+    return {"i8i8": batch * (dim + 4), "f32": batch * dim * 4, "f16": batch * dim * 4,
+            "binary": batch * (dim + 31) // 32 * 4}[w["kind"]]
+
+
+def measured_traffic(workload, kernel):
+    """HBM bytes per launch of `kernel` from the calibrated FETCH_SIZE + WRITE_SIZE counter passes
+    summarized in profiles/ (None when this workload has not been profiled)."""
+    path = ROOT / "profiles" / "traffic.json"
+    if not path.exists():
+        return None
+    entry = json.loads(path.read_text()).get(workload)
+    if not entry or entry.get("kernel") != kernel:
+        return None
+    return entry["traffic_bytes_per_launch"]
+
+
+def scan_kernel_name(w):
+    if w["kind"] == "i8i8":
+        return f"mfmaScanKernel<{w['dim'] // 32}, false>"
+    return "valuScanKernel"
 
 
 def cpu_baseline(capi, w, corpus, keep, queries, gpu_idx, gpu_val, budget_s):
@@ -145,7 +170,7 @@ def cpu_baseline(capi, w, corpus, keep, queries, gpu_idx, gpu_val, budget_s):
     t0 = time.perf_counter()
     run([0])
     one = time.perf_counter() - t0
-    sample = int(max(1, min(batch, 64, budget_s / max(one, 1e-6))))
+    sample = int(max(1, min(batch, budget_s / max(one, 1e-6))))
     rows = list(range(sample))
     t0 = time.perf_counter()
     ref_idx, ref_val = run(rows)
@@ -174,6 +199,9 @@ def main(argv=None) -> int:
     parser.add_argument("--workload", choices=sorted(WORKLOADS), default="int8-10m")
     parser.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
     parser.add_argument("--cpu-budget", type=float, default=12.0, help="seconds of CPU sample work")
+    parser.add_argument("--copy-probe", type=int, default=0, metavar="MIB",
+                        help="before the workload, copy MIB MiB device to device once (a transfer of "
+                             "known size for calibrating rocprofv3 FETCH_SIZE/WRITE_SIZE readings)")
     args = parser.parse_args(argv)
     if args.gpus != 1:
         print(f"bench.py: this build runs on one GPU; --gpus {args.gpus} is not supported "
@@ -190,6 +218,15 @@ def main(argv=None) -> int:
     w = WORKLOADS[args.workload]
     log(f"device {info.name.decode()} {info.arch.decode()} CUs={info.compute_units}; workload {w['name']}")
 
+    if args.copy_probe > 0:
+        nbytes = args.copy_probe << 20
+        src, dst = capi.DeviceArray(nbytes, np.uint8), capi.DeviceArray(nbytes, np.uint8)
+        capi.call("zcgvs_memset", src.ptr, 1, nbytes, None)
+        capi.call("zcgvs_memcpy_d2d", dst.ptr, src.ptr, nbytes, None)
+        capi.synchronize()
+        src.free()
+        dst.free()
+        log(f"copy probe: {args.copy_probe} MiB device-to-device")
     desc, corpus, queries, keep = build_inputs(capi, w)
     size = capi.search_workspace_bytes(desc)
     workspace = capi.DeviceArray(size, np.uint8)
@@ -220,8 +257,9 @@ def main(argv=None) -> int:
 
     step_ms = [starts[i].elapsed_ms(ends[i]) for i in range(args.steps)]
     used = min(phases, max_phases)
-    scan_ms = [sum(scan_events[i][2 * p].elapsed_ms(scan_events[i][2 * p + 1]) for p in range(used))
-               for i in range(args.steps)]
+    phase_ms = [[scan_events[i][2 * p].elapsed_ms(scan_events[i][2 * p + 1]) for p in range(used)]
+                for i in range(args.steps)]
+    phase_rows = capi.search_phase_rows(desc, max_phases)[:used]
     flags = np.empty(w["batch"], dtype=np.uint32)
     capi.call("zcgvs_memcpy_d2h", flags.ctypes.data, capi.search_overflow_flags(desc, workspace),
               flags.nbytes, None)
@@ -232,9 +270,16 @@ def main(argv=None) -> int:
 
     batch = w["batch"]
     value = batch * args.steps / wall
-    mean_scan = statistics.mean(scan_ms) if used else float("nan")
-    bytes_step = algorithmic_bytes(w)
-    achieved = bytes_step / (mean_scan * 1e-3) / 1e9 if used else None
+    # Dominant kernel: the scan launches of the threshold phases (the MFMA path compiles the dense
+    # first phase as a separate kernel; the VALU path runs every phase with one kernel).
+    first = 1 if w["kind"] == "i8i8" and used > 1 else 0
+    launches = list(range(first, used))
+    mean_ms = statistics.mean(statistics.mean(phase_ms[i][p] for p in launches) for i in range(args.steps))
+    bytes_launch = statistics.mean(phase_rows[p] * row_bytes(w) + query_bytes(w) for p in launches)
+    achieved = bytes_launch / (mean_ms * 1e-3) / 1e9
+    scan_ms = statistics.mean(sum(phase_ms[i]) for i in range(args.steps))
+    log("phase ms: " + " ".join(f"{statistics.mean(phase_ms[i][p] for i in range(args.steps)):.3f}"
+                                 for p in range(used)) + f"; rows {phase_rows}")
     result = {
         "metric": "queries/sec + p50 latency (N=10M d=768 int8, k=100); scan HBM GB/s",
         "value": round(value, 2),
@@ -253,18 +298,21 @@ def main(argv=None) -> int:
                    "scan_phases": phases},
         "roofline": {
             "bound": "hbm",
-            "achieved": round(achieved, 1) if achieved else None,
+            "achieved": round(achieved, 1),
             "peak": HBM_PEAK_GBS,
             "unit": "GB/s",
-            "frac": round(achieved / HBM_PEAK_GBS, 4) if achieved else None,
-            "traffic": None,
-            "kernel": "scan (all phase launches of one step)",
-            "kernel_ms": round(mean_scan, 4) if used else None,
+            "frac": round(achieved / HBM_PEAK_GBS, 4),
+            "traffic": measured_traffic(args.workload, scan_kernel_name(w)),
+            "kernel": scan_kernel_name(w),
+            "launches_per_step": len(launches),
+            "kernel_ms": round(mean_ms, 4),
+            "algorithmic_bytes_per_launch": int(bytes_launch),
+            "all_scan_launches_ms": round(scan_ms, 4),
         },
     }
     if w["kind"] == "i8i8":
-        ops = 2.0 * w["n"] * w["dim"] * batch
-        tops = ops / (mean_scan * 1e-3) / 1e12
+        ops = statistics.mean(2.0 * phase_rows[p] * w["dim"] * batch for p in launches)
+        tops = ops / (mean_ms * 1e-3) / 1e12
         result["mfma"] = {"achieved": round(tops, 1), "peak": INT8_MFMA_PEAK_TOPS, "unit": "TOP/s",
                           "frac": round(tops / INT8_MFMA_PEAK_TOPS, 4)}
     if flags.any():

@@ -283,6 +283,12 @@ int zcgvs_search_topk_profiled(const zcgvs_search_desc* desc, void* d_workspace,
                                zcgvs_stream_t stream, zcgvs_event_t* events, int max_phases,
                                int* phases);
 
+/* Corpus rows each scan phase of the fused pipeline visits for `desc` (rows[p] for p <
+ * max_phases; the phase count in *phases; 0 phases when the pipeline materializes the score
+ * matrix instead). Host only; used to price the scan launches. No reference counterpart. */
+int zcgvs_search_phase_rows(const zcgvs_search_desc* desc, long long* rows, int max_phases,
+                            int* phases);
+
 /* Device address of the [batch] uint32 overflow flags inside a workspace laid out for `desc`
  * (non-zero: that query's result is incomplete and must be recomputed exactly, e.g. with
  * zcgvs_launch_similarity + zcgvs_launch_topk). */

@@ -105,6 +105,8 @@ _SIGNATURES = {
     "zcgvs_search_overflow_flags": (_i32, [ctypes.POINTER(SearchDesc), _vp, ctypes.POINTER(_vp)]),
     "zcgvs_search_topk_profiled": (_i32, [ctypes.POINTER(SearchDesc), _vp, _sz, _vp, _vp, _vp,
                                           ctypes.POINTER(_vp), _i32, ctypes.POINTER(_i32)]),
+    "zcgvs_search_phase_rows": (_i32, [ctypes.POINTER(SearchDesc), ctypes.POINTER(_i64), _i32,
+                                       ctypes.POINTER(_i32)]),
     "zcgvs_generate_normalized": (_i32, [_vp, _i64, _i32, _u64, _i64, _vp]),
 }
 
@@ -400,6 +402,14 @@ def search_topk_profiled(desc: SearchDesc, workspace, workspace_bytes, out_idx, 
     call("zcgvs_search_topk_profiled", ctypes.byref(desc), ptr(workspace), workspace_bytes, ptr(out_idx),
          ptr(out_val), getattr(stream, "handle", stream), handles, max_phases, ctypes.byref(phases))
     return phases.value
+
+
+def search_phase_rows(desc: SearchDesc, max_phases: int = 16) -> list[int]:
+    """Corpus rows each scan phase visits (empty when the pipeline materializes scores)."""
+    rows = (_i64 * max_phases)()
+    phases = _i32(0)
+    call("zcgvs_search_phase_rows", ctypes.byref(desc), rows, max_phases, ctypes.byref(phases))
+    return [int(rows[p]) for p in range(min(phases.value, max_phases))]
 
 
 def search_overflow_flags(desc: SearchDesc, workspace) -> int:

@@ -633,4 +633,30 @@ int zcgvs_search_topk_profiled(const zcgvs_search_desc* desc, void* d_workspace,
                       events, max_phases, phases);
 }
 
+int zcgvs_search_phase_rows(const zcgvs_search_desc* desc, long long* rows, int max_phases,
+                            int* phases) {
+    if (desc == nullptr || phases == nullptr || (rows == nullptr && max_phases > 0)) {
+        return setError(ZCGVS_ERR_INVALID_ARGUMENT, "zcgvs: descriptor and outputs must not be null");
+    }
+    const Plan plan = makePlan(*desc);
+    if (plan.status != ZCGVS_OK) {
+        return setError(plan.status, plan.error);
+    }
+    *phases = static_cast<int>(plan.phases.size());
+    const long long n = desc->corpus.doc_count;
+    const long long last_block = (n + plan.block_rows - 1) / plan.block_rows - 1;
+    for (std::size_t p = 0; p < plan.phases.size() && static_cast<int>(p) < max_phases; ++p) {
+        const PhaseArgs& phase = plan.phases[p];
+        long long r = phase.items * phase.block_rows;
+        // the partial last block belongs to the phase whose stride divides it and skip does not
+        const bool holds_last = last_block % phase.stride == 0 &&
+                                (phase.skip == 0 || last_block % (phase.stride * phase.skip) != 0);
+        if (holds_last) {
+            r -= (last_block + 1) * plan.block_rows - n;
+        }
+        rows[p] = r;
+    }
+    return clearError();
+}
+
 }  // extern "C"
