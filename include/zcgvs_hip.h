@@ -260,7 +260,14 @@ typedef struct zcgvs_search_desc {
     const int* query_terms;    /* [batch, lexical_stride] device term ids, -1 padded           */
     int lexical_stride;
     float dense_weight;
+    int flags;                 /* zcgvs_search_flags bits; 0 for the default pipeline           */
 } zcgvs_search_desc;
+
+/* zcgvs_search_desc.flags. ZCGVS_SEARCH_MATERIALIZE runs the reference-order pipeline (a
+ * [batch, doc_count] score matrix in the workspace, then zcgvs_launch_topk) instead of the fused
+ * scan; its workspace is correspondingly larger. It never overflows, so it is the exact
+ * recompute for queries zcgvs_search_overflow_flags reports. */
+enum zcgvs_search_flags { ZCGVS_SEARCH_MATERIALIZE = 1 };
 
 /* Bytes of device workspace zcgvs_search_topk needs for this descriptor (0 on error). */
 size_t zcgvs_search_workspace_bytes(const zcgvs_search_desc* desc);

@@ -20,6 +20,7 @@ OK, ERR_INVALID_ARGUMENT, ERR_RUNTIME, ERR_HIP, ERR_UNSUPPORTED = 0, 1, 2, 3, 4
 COSINE, DOT, L2 = 0, 1, 2
 F32, F16, I8, BINARY = 0, 1, 2, 3
 INT8_REFERENCE, INT8_PER_VECTOR = 0, 1
+SEARCH_MATERIALIZE = 1
 
 _vp = ctypes.c_void_p
 _i32 = ctypes.c_int
@@ -46,7 +47,7 @@ class SearchDesc(ctypes.Structure):
                 ("k", _i32), ("metric", _i32), ("int8_mode", _i32), ("mask", _vp),
                 ("rescore_candidates", _i32), ("lex_offsets", _vp), ("lex_docs", _vp),
                 ("lex_weights", _vp), ("lex_doc_count", _i64), ("lex_vocab_size", _i32), ("query_terms", _vp),
-                ("lexical_stride", _i32), ("dense_weight", _f32)]
+                ("lexical_stride", _i32), ("dense_weight", _f32), ("flags", _i32)]
 
 
 # name -> (restype, argtypes)
@@ -367,11 +368,11 @@ def store_desc(data=None, doc_count=0, dim=0, dtype=F32, scale=1.0, row_scales=N
 def search_desc(corpus: StoreDesc, queries, batch, k, metric=COSINE, *, int8_mode=INT8_REFERENCE,
                 mask=None, rescore: StoreDesc | None = None, rescore_candidates=0, lex_offsets=None,
                 lex_docs=None, lex_weights=None, lex_doc_count=0, lex_vocab_size=0, query_terms=None,
-                lexical_stride=0, dense_weight=1.0) -> SearchDesc:
+                lexical_stride=0, dense_weight=1.0, flags=0) -> SearchDesc:
     desc = SearchDesc(corpus, rescore if rescore is not None else StoreDesc(), ptr(queries), batch, k,
                       metric, int8_mode, ptr(mask), rescore_candidates, ptr(lex_offsets), ptr(lex_docs),
                       ptr(lex_weights), lex_doc_count, lex_vocab_size, ptr(query_terms), lexical_stride,
-                      dense_weight)
+                      dense_weight, flags)
     # the nested StoreDesc fields are copied by value: carry their owners over as well
     return _keep_alive(desc, *getattr(corpus, "_owners", []),
                        *(getattr(rescore, "_owners", []) if rescore is not None else []),

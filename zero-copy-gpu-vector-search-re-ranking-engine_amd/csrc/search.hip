@@ -231,8 +231,9 @@ Plan makePlan(const zcgvs_search_desc& d) {
     if (plan.hybrid) {
         probe.lexical = reinterpret_cast<const float*>(static_cast<std::uintptr_t>(kAlign));
     }
-    plan.use_mfma = mfmaSupported(probe);
-    plan.materialized = !plan.use_mfma && !valuSupported(probe);
+    const bool forced = (d.flags & ZCGVS_SEARCH_MATERIALIZE) != 0;
+    plan.use_mfma = !forced && mfmaSupported(probe);
+    plan.materialized = forced || (!plan.use_mfma && !valuSupported(probe));
     if (plan.per_vector && plan.materialized && dim % 16 != 0) {
         return fail(ZCGVS_ERR_INVALID_ARGUMENT,
                     "zcgvs: per-vector int8 mode needs dim % 16 == 0 and a 16-byte aligned corpus");
