@@ -15,6 +15,12 @@
 // pass; that pass runs right after the next barrier, before that step's tile copies are issued,
 // so candidate stores never sit behind later tile copies in the vmcnt order.
 //
+// Candidate staging. A key the exact pass accepts gets its segment slot from the per-query LDS
+// counter and is parked in a per-wavefront LDS buffer; the buffers are written to the segments
+// after the scan loop. A global store inside the loop would enter the same in-order vmcnt queue
+// as the tile copies, and the next tile wait would have to wait for the store's completion too;
+// only a wavefront whose buffer is full stores directly.
+//
 // Corpus streaming. Tiles of 64 rows go from HBM straight into a ring of LDS buffers with
 // global_load_lds_dwordx4 (no staging registers), kDepth - 1 tiles ahead of the one being
 // multiplied. Before a tile is used every wavefront waits for its own copies of that tile
@@ -65,6 +71,7 @@ constexpr int kWaves = kThreads / kWave;
 constexpr int kQueriesPerLaunch = kWaves * 32;
 constexpr float kFilterMargin = 9.5367431640625e-07f;  // 2^-20
 constexpr std::size_t kRingBudget = 150 * 1024;
+constexpr int kStaged = 64;  // candidates parked per wavefront before they reach the segments
 
 // LDS byte address of a __shared__ location.
 __device__ __forceinline__ std::uint32_t ldsAddress(const void* p) {
@@ -137,6 +144,9 @@ void mfmaScanKernel(ScanArgs scan, PhaseArgs phase, EmitArgs emit, int q_offset,
     __shared__ __attribute__((aligned(16))) float scale_ring[kScaleDepth][kRows];
     __shared__ std::uint32_t lds_count[kQueriesPerLaunch];
     __shared__ std::uint32_t lds_simd[4];
+    __shared__ std::uint64_t stage_key[kDense ? 1 : kWaves][kStaged];
+    __shared__ std::uint32_t stage_slot[kDense ? 1 : kWaves][kStaged];  // (segment slot << 8) | local query
+    __shared__ std::uint32_t stage_count[kWaves];
 
     const int tid = threadIdx.x;
     const int lane = tid & (kWave - 1);
@@ -177,6 +187,9 @@ void mfmaScanKernel(ScanArgs scan, PhaseArgs phase, EmitArgs emit, int q_offset,
     }
     if (tid < 4) {
         lds_simd[tid] = 0u;
+    }
+    if (tid < kWaves) {
+        stage_count[tid] = 0u;
     }
 
     // ---- per-lane copy plan: LDS slot P of the tile holds global slot (P % spr) ^ swizzle(row).
@@ -379,7 +392,30 @@ void mfmaScanKernel(ScanArgs scan, PhaseArgs phase, EmitArgs emit, int q_offset,
             }
             return q_valid && best * qscale >= tau_floor;
         };
+        const std::uint32_t seg_capacity = 1u << emit.seg_log2;
+        const std::size_t seg_base = static_cast<std::size_t>(blockIdx.x) * batch;
+        auto stageCandidate = [&](std::uint64_t key) {
+            const int qlocal_ = q - q_offset;
+            const std::uint32_t slot = atomicAdd(&lds_count[qlocal_], 1u);
+            if (slot >= seg_capacity) {
+                return;  // counted; the merge reports the overflow
+            }
+            const std::uint32_t parked = atomicAdd(&stage_count[wave], 1u);
+            if (parked < static_cast<std::uint32_t>(kStaged)) {
+                stage_key[wave][parked] = key;
+                stage_slot[wave][parked] = (slot << 8) | static_cast<std::uint32_t>(qlocal_);
+            } else {
+                emit.seg[((seg_base + q) << emit.seg_log2) + slot] = key;
+            }
+        };
         // Exact scores and keys of the tile in (acc0, acc1); keys above the threshold are appended.
+        // First pass: every value's exact score against the threshold, folded into a wave-uniform
+        // 32-bit set of value slots that some lane passes (4 VALU per value, no branches). Second
+        // pass: the key work for those slots only. Masked and padding rows (NaN scale) score NaN
+        // here and never pass; they qualify only against a -FLT_MAX threshold, where the whole
+        // tile takes the general path.
+        const float tau_pass = q_valid ? tau_floor : INFINITY;
+        const bool masked_ok = q_valid && kMaskedScore >= tau_floor;
         auto exact = [&](const v16i& acc0, const v16i& acc1, const float* scales, long long row0) {
             // Tile-relative rows in 32 bits; the empty asm keeps the compiler from hoisting the
             // 32 per-row constants out of the scan loop into registers.
@@ -387,26 +423,42 @@ void mfmaScanKernel(ScanArgs scan, PhaseArgs phase, EmitArgs emit, int q_offset,
             asm volatile("" : "+v"(hb));
             const int valid_rows = static_cast<int>(min(static_cast<long long>(kRows), doc_count - row0));
             const std::uint32_t row_base = static_cast<std::uint32_t>(row0);
-#pragma unroll
-            for (int mb = 0; mb < 2; ++mb) {
-#pragma unroll
-                for (int g = 0; g < 4; ++g) {
-                    const int rl0 = mb * 32 + 8 * g + hb;
-                    const float4 rs = *reinterpret_cast<const float4*>(scales + rl0);
-                    const float rsv[4] = {rs.x, rs.y, rs.z, rs.w};
-#pragma unroll
-                    for (int j = 0; j < 4; ++j) {
-                        const int rl = rl0 + j;
-                        const int dot = mb == 0 ? acc0[4 * g + j] : acc1[4 * g + j];
-                        const float combined = qscale * rsv[j];
-                        const float score = rsv[j] == rsv[j] ? static_cast<float>(dot) * combined : kMaskedScore;
-                        if (q_valid && rl < valid_rows && score >= tau_floor) {
-                            const std::uint64_t key = makeKey(score, row_base + static_cast<std::uint32_t>(rl));
-                            if (key > tau) {
-                                appendCandidate(emit, lds_count, q, q_offset, batch, key);
-                            }
-                        }
+            auto value = [&](int slot) { return slot < 16 ? acc0[slot] : acc1[slot - 16]; };
+            auto rowOf = [&](int slot) { return (slot / 16) * 32 + 8 * ((slot % 16) / 4) + hb + slot % 4; };
+            auto emitSlot = [&](int slot, float rs) {
+                const int rl = rowOf(slot);
+                const float combined = qscale * rs;
+                const float score = rs == rs ? static_cast<float>(value(slot)) * combined : kMaskedScore;
+                if (q_valid && rl < valid_rows && score >= tau_floor) {
+                    const std::uint64_t key = makeKey(score, row_base + static_cast<std::uint32_t>(rl));
+                    if (key > tau) {
+                        stageCandidate(key);
                     }
+                }
+            };
+            if (__any(masked_ok)) {
+#pragma unroll
+                for (int slot = 0; slot < 32; ++slot) {
+                    emitSlot(slot, scales[rowOf(slot)]);
+                }
+                return;
+            }
+            std::uint32_t passing = 0;  // wave-uniform
+#pragma unroll
+            for (int slot = 0; slot < 32; slot += 4) {
+                const float4 rs = *reinterpret_cast<const float4*>(scales + rowOf(slot));
+                const float rsv[4] = {rs.x, rs.y, rs.z, rs.w};
+#pragma unroll
+                for (int j = 0; j < 4; ++j) {
+                    const float score = static_cast<float>(value(slot + j)) * (qscale * rsv[j]);
+                    const bool pass = score >= tau_pass;
+                    passing |= (__builtin_amdgcn_ballot_w64(pass) != 0 ? 1u : 0u) << (slot + j);
+                }
+            }
+#pragma unroll
+            for (int slot = 0; slot < 32; ++slot) {
+                if (passing & (1u << slot)) {
+                    emitSlot(slot, scales[rowOf(slot)]);
                 }
             }
         };
@@ -445,6 +497,15 @@ void mfmaScanKernel(ScanArgs scan, PhaseArgs phase, EmitArgs emit, int q_offset,
             exact(acc0, acc1, scale_ring[acc_sslot], acc_row0);
         }
 
+        // write the parked candidates of this wavefront
+        {
+            const std::uint32_t parked = min(stage_count[wave], static_cast<std::uint32_t>(kStaged));
+            for (std::uint32_t i = static_cast<std::uint32_t>(lane); i < parked; i += kWave) {
+                const std::uint32_t packed = stage_slot[wave][i];
+                const std::size_t qg = static_cast<std::size_t>(q_offset) + (packed & 0xFFu);
+                emit.seg[((seg_base + qg) << emit.seg_log2) + (packed >> 8)] = stage_key[wave][i];
+            }
+        }
         __syncthreads();
         for (int i = tid; i < q_count; i += kThreads) {
             emit.seg_count[static_cast<std::size_t>(blockIdx.x) * batch + q_offset + i] = lds_count[i];

@@ -325,7 +325,8 @@ Plan makePlan(const zcgvs_search_desc& d) {
     plan.dense_stride = first.items * plan.block_rows;
     // Segment capacity: 4x the expected candidates per (workgroup, query) of the widest phase.
     const long long expected = (static_cast<long long>(plan.width) * growth) / plan.workgroups;
-    plan.seg_log2 = std::max(5, ceilLog2(4 * expected + 16));
+    // (at most 2^24 slots: the MFMA scan packs a slot and an 8-bit query into 32 bits)
+    plan.seg_log2 = std::min(24, std::max(5, ceilLog2(4 * expected + 16)));
 
     if (plan.hybrid) {
         plan.lex = layout.add(static_cast<std::size_t>(batch) * n * 4);
