@@ -374,9 +374,24 @@ void mfmaScanKernel(ScanArgs scan, PhaseArgs phase, EmitArgs emit, int q_offset,
             lead = __builtin_amdgcn_readfirstlane(rank) == 0u;
         }
 
-        // Filter: does any row of the tile in (acc0, acc1) reach this lane's threshold?
-        auto filter = [&](const v16i& acc0, const v16i& acc1, const float* scales) {
-            float best = -INFINITY;
+        // relaxed per-lane threshold of the filter; lanes past the launch's queries never pass
+        float relaxed_floor = INFINITY;
+        if (q_valid) {
+            const float t = tau_floor / qscale;
+            relaxed_floor = t - fabsf(t) * kFilterMargin - 1e-30f;
+        }
+        const bool examine_all = __any(q_valid && kMaskedScore >= tau_floor);
+        // Filter: the wave-uniform set of value slots (slot = 16 * block + result index) in which
+        // some lane's relaxed score (float)dot * s_r reaches the lane's relaxed threshold
+        // (tau_floor / s_q, lowered by 2^-20 relative: far more than the few-ulp gap between
+        // this product order and the exact score's, so every exact candidate's slot is set).
+        // A masked or padding row (NaN scale) never passes here; such rows can qualify only
+        // against a -FLT_MAX threshold, and then every slot is examined.
+        auto filter = [&](const v16i& acc0, const v16i& acc1, const float* scales) -> std::uint32_t {
+            if (examine_all) {
+                return 0xFFFFFFFFu;
+            }
+            std::uint32_t passing = 0u;
 #pragma unroll
             for (int mb = 0; mb < 2; ++mb) {
 #pragma unroll
@@ -386,11 +401,12 @@ void mfmaScanKernel(ScanArgs scan, PhaseArgs phase, EmitArgs emit, int q_offset,
 #pragma unroll
                     for (int j = 0; j < 4; ++j) {
                         const int dot = mb == 0 ? acc0[4 * g + j] : acc1[4 * g + j];
-                        best = fmaxf(best, static_cast<float>(dot) * rsv[j]);  // NaN (masked) ignored
+                        const bool pass = static_cast<float>(dot) * rsv[j] >= relaxed_floor;
+                        passing |= (__builtin_amdgcn_ballot_w64(pass) != 0 ? 1u : 0u) << (16 * mb + 4 * g + j);
                     }
                 }
             }
-            return q_valid && best * qscale >= tau_floor;
+            return passing;
         };
         const std::uint32_t seg_capacity = 1u << emit.seg_log2;
         const std::size_t seg_base = static_cast<std::size_t>(blockIdx.x) * batch;
@@ -408,57 +424,30 @@ void mfmaScanKernel(ScanArgs scan, PhaseArgs phase, EmitArgs emit, int q_offset,
                 emit.seg[((seg_base + q) << emit.seg_log2) + slot] = key;
             }
         };
-        // Exact scores and keys of the tile in (acc0, acc1); keys above the threshold are appended.
-        // First pass: every value's exact score against the threshold, folded into a wave-uniform
-        // 32-bit set of value slots that some lane passes (4 VALU per value, no branches). Second
-        // pass: the key work for those slots only. Masked and padding rows (NaN scale) score NaN
-        // here and never pass; they qualify only against a -FLT_MAX threshold, where the whole
-        // tile takes the general path.
-        const float tau_pass = q_valid ? tau_floor : INFINITY;
-        const bool masked_ok = q_valid && kMaskedScore >= tau_floor;
-        auto exact = [&](const v16i& acc0, const v16i& acc1, const float* scales, long long row0) {
+        // Exact scores and keys of the value slots `passing` marks; keys above the threshold are
+        // appended.
+        auto exact = [&](const v16i& acc0, const v16i& acc1, const float* scales, long long row0,
+                         std::uint32_t passing) {
             // Tile-relative rows in 32 bits; the empty asm keeps the compiler from hoisting the
             // 32 per-row constants out of the scan loop into registers.
             int hb = 4 * half;
             asm volatile("" : "+v"(hb));
             const int valid_rows = static_cast<int>(min(static_cast<long long>(kRows), doc_count - row0));
             const std::uint32_t row_base = static_cast<std::uint32_t>(row0);
-            auto value = [&](int slot) { return slot < 16 ? acc0[slot] : acc1[slot - 16]; };
-            auto rowOf = [&](int slot) { return (slot / 16) * 32 + 8 * ((slot % 16) / 4) + hb + slot % 4; };
-            auto emitSlot = [&](int slot, float rs) {
-                const int rl = rowOf(slot);
-                const float combined = qscale * rs;
-                const float score = rs == rs ? static_cast<float>(value(slot)) * combined : kMaskedScore;
-                if (q_valid && rl < valid_rows && score >= tau_floor) {
-                    const std::uint64_t key = makeKey(score, row_base + static_cast<std::uint32_t>(rl));
-                    if (key > tau) {
-                        stageCandidate(key);
-                    }
-                }
-            };
-            if (__any(masked_ok)) {
-#pragma unroll
-                for (int slot = 0; slot < 32; ++slot) {
-                    emitSlot(slot, scales[rowOf(slot)]);
-                }
-                return;
-            }
-            std::uint32_t passing = 0;  // wave-uniform
-#pragma unroll
-            for (int slot = 0; slot < 32; slot += 4) {
-                const float4 rs = *reinterpret_cast<const float4*>(scales + rowOf(slot));
-                const float rsv[4] = {rs.x, rs.y, rs.z, rs.w};
-#pragma unroll
-                for (int j = 0; j < 4; ++j) {
-                    const float score = static_cast<float>(value(slot + j)) * (qscale * rsv[j]);
-                    const bool pass = score >= tau_pass;
-                    passing |= (__builtin_amdgcn_ballot_w64(pass) != 0 ? 1u : 0u) << (slot + j);
-                }
-            }
 #pragma unroll
             for (int slot = 0; slot < 32; ++slot) {
                 if (passing & (1u << slot)) {
-                    emitSlot(slot, scales[rowOf(slot)]);
+                    const int rl = (slot / 16) * 32 + 8 * ((slot % 16) / 4) + hb + slot % 4;
+                    const float rs = scales[rl];
+                    const int dot = slot < 16 ? acc0[slot] : acc1[slot - 16];
+                    const float combined = qscale * rs;
+                    const float score = rs == rs ? static_cast<float>(dot) * combined : kMaskedScore;
+                    if (q_valid && rl < valid_rows && score >= tau_floor) {
+                        const std::uint64_t key = makeKey(score, row_base + static_cast<std::uint32_t>(rl));
+                        if (key > tau) {
+                            stageCandidate(key);
+                        }
+                    }
                 }
             }
         };
@@ -467,16 +456,16 @@ void mfmaScanKernel(ScanArgs scan, PhaseArgs phase, EmitArgs emit, int q_offset,
         v16i acc1 = {};
         long long acc_row0 = -1;  // first row of the tile in (acc0, acc1); -1 = none yet
         int acc_sslot = 0;
-        bool owed = false;        // the tile in (acc0, acc1) passed its filter: exact pass owed
+        std::uint32_t owed = 0u;  // slots of the tile in (acc0, acc1) that owe an exact pass
         for (; item < phase.items; item += stride_items) {
             arrive(item);
             if (wave_active && !lead && acc_row0 >= 0) {
                 owed = filter(acc0, acc1, scale_ring[acc_sslot]);
             }
-            if (__any(owed)) {
-                exact(acc0, acc1, scale_ring[acc_sslot], acc_row0);
+            if (owed != 0u) {
+                exact(acc0, acc1, scale_ring[acc_sslot], acc_row0, owed);
             }
-            owed = false;
+            owed = 0u;
             refill(item, slot, sslot);
             if (wave_active) {
                 multiply(ring[slot], acc0, acc1);
@@ -493,8 +482,8 @@ void mfmaScanKernel(ScanArgs scan, PhaseArgs phase, EmitArgs emit, int q_offset,
         if (wave_active && !lead && acc_row0 >= 0) {
             owed = filter(acc0, acc1, scale_ring[acc_sslot]);
         }
-        if (__any(owed)) {
-            exact(acc0, acc1, scale_ring[acc_sslot], acc_row0);
+        if (owed != 0u) {
+            exact(acc0, acc1, scale_ring[acc_sslot], acc_row0, owed);
         }
 
         // write the parked candidates of this wavefront
