@@ -292,17 +292,23 @@ __global__ __launch_bounds__(kSelectThreads) void selectMergeKernel(
             }
         }
         if (in.seg != nullptr) {
+            // Candidate i of the compacted list lives in the last segment whose offset is <= i
+            // (empty segments share their successor's offset), at position i - offset there.
             const std::uint32_t base = k_prev + n_dense;
-            const long long total = static_cast<long long>(in.n_seg) << in.seg_log2;
-            const long long slot_mask = (1LL << in.seg_log2) - 1;
 #pragma unroll 4
-            for (long long i = t; i < total; i += blockDim.x) {
-                const int s = static_cast<int>(i >> in.seg_log2);
-                const std::uint32_t j = static_cast<std::uint32_t>(i & slot_mask);
-                if (j < lds_seg[s]) {
-                    lds_cand[base + lds_offset[s] + j] =
-                        in.seg[((static_cast<std::size_t>(s) * batch + q) << in.seg_log2) + j];
+            for (std::uint32_t i = t; i < seg_total; i += blockDim.x) {
+                int lo = 0;
+                int hi = in.n_seg - 1;
+                while (lo < hi) {
+                    const int mid = (lo + hi + 1) >> 1;
+                    if (lds_offset[mid] <= i) {
+                        lo = mid;
+                    } else {
+                        hi = mid - 1;
+                    }
                 }
+                const std::uint32_t j = i - lds_offset[lo];
+                lds_cand[base + i] = in.seg[((static_cast<std::size_t>(lo) * batch + q) << in.seg_log2) + j];
             }
         }
     }
