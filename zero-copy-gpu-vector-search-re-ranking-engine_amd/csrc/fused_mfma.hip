@@ -92,6 +92,22 @@ __device__ __forceinline__ void copyToLds(const void* src, std::uint32_t lds_bas
                  : "memory");
 }
 
+// The same copy from a wave-uniform base address (SGPR pair) plus a per-lane 32-bit byte
+// offset, so no 64-bit address arithmetic runs per lane.
+__device__ __forceinline__ void copyToLds(const void* uniform_base, std::uint32_t lane_offset,
+                                          std::uint32_t lds_base) {
+    // readfirstlane returns int: each half goes through uint32_t so the low word is not
+    // sign-extended into the high one.
+    const auto address = reinterpret_cast<std::uintptr_t>(uniform_base);
+    const auto hi = static_cast<std::uint32_t>(__builtin_amdgcn_readfirstlane(static_cast<std::uint32_t>(address >> 32)));
+    const auto lo = static_cast<std::uint32_t>(__builtin_amdgcn_readfirstlane(static_cast<std::uint32_t>(address)));
+    const std::uint64_t sbase = (static_cast<std::uint64_t>(hi) << 32) | lo;
+    asm volatile("s_nop 0\n\tglobal_load_lds_dwordx4 %0, %1"
+                 :
+                 : "v"(lane_offset), "s"(sbase), "{m0}"(lds_base)
+                 : "memory");
+}
+
 // s_waitcnt that waits until at most n vector-memory operations of this wavefront are pending
 // (expcnt and lgkmcnt fields at their "no wait" maxima).
 __device__ constexpr int vmcntOnly(int n) {
@@ -192,21 +208,15 @@ void mfmaScanKernel(ScanArgs scan, PhaseArgs phase, EmitArgs emit, int q_offset,
         stage_count[tid] = 0u;
     }
 
-    // ---- per-lane copy plan: LDS slot P of the tile holds global slot (P % spr) ^ swizzle(row).
-    //      The tile-relative source offsets (< 64 KiB) are kept two to a register. ----
-    static_assert(kTileBytes <= 65536, "copy offsets fit 16 bits");
-    constexpr int kPacked = (kCopies + 1) / 2;
-    std::uint32_t copy_pk[kPacked];
-#pragma unroll
-    for (int i = 0; i < kPacked; ++i) {
-        copy_pk[i] = 0u;
-    }
+    // ---- per-lane copy plan: LDS slot P of the tile holds global slot (P % spr) ^ swizzle(row);
+    //      copy_off[i] is the tile-relative source byte offset of this lane's i-th copy. ----
+    std::uint32_t copy_off[kCopies];
 #pragma unroll
     for (int i = 0; i < kCopies; ++i) {
         const int p = (wave * kCopies + i) * kWave + lane;
         const int row = p / kSlotsPerRow;
         const int ls = p - row * kSlotsPerRow;
-        copy_pk[i / 2] |= static_cast<std::uint32_t>(row * kDim + (ls ^ swizzle(row)) * 16) << (16 * (i % 2));
+        copy_off[i] = static_cast<std::uint32_t>(row * kDim + (ls ^ swizzle(row)) * 16);
     }
     auto issue = [&](long long item, int slot, int sslot) {
         const long long row0 = phaseBlock(item, phase.stride, phase.skip) * kRows;
@@ -215,8 +225,7 @@ void mfmaScanKernel(ScanArgs scan, PhaseArgs phase, EmitArgs emit, int q_offset,
         if (row0 + kRows <= doc_count) {
 #pragma unroll
             for (int i = 0; i < kCopies; ++i) {
-                const int off = static_cast<int>((copy_pk[i / 2] >> (16 * (i % 2))) & 0xFFFFu);
-                copyToLds(base + off,
+                copyToLds(base, copy_off[i],
                           __builtin_amdgcn_readfirstlane(slot_base + (wave * kCopies + i) * kWave * 16));
             }
         } else {
@@ -224,15 +233,14 @@ void mfmaScanKernel(ScanArgs scan, PhaseArgs phase, EmitArgs emit, int q_offset,
             const int last = static_cast<int>(doc_count - row0) - 1;
 #pragma unroll
             for (int i = 0; i < kCopies; ++i) {
-                const int off = static_cast<int>((copy_pk[i / 2] >> (16 * (i % 2))) & 0xFFFFu);
-                const int row = off / kDim;
-                copyToLds(base + off - (row - min(row, last)) * kDim,
-                          __builtin_amdgcn_readfirstlane(slot_base + (wave * kCopies + i) * kWave * 16));
+                const int row = static_cast<int>(copy_off[i]) / kDim;
+                const std::uint32_t off = copy_off[i] - static_cast<std::uint32_t>((row - min(row, last)) * kDim);
+                copyToLds(base, off, __builtin_amdgcn_readfirstlane(slot_base + (wave * kCopies + i) * kWave * 16));
             }
         }
         if (wave == 0 && lane < kRows / 4) {
             // the padded scale copy makes rows row0 .. row0 + 63 readable for every tile
-            copyToLds(scan.row_scales + row0 + 4 * lane,
+            copyToLds(scan.row_scales + row0, static_cast<std::uint32_t>(16 * lane),
                       __builtin_amdgcn_readfirstlane(ldsAddress(&scale_ring[sslot][0])));
         }
     };
