@@ -86,6 +86,10 @@ struct ScanArgs {
     int dtype = 0;               // zcgvs_dtype; I8 with row_scales != nullptr = per-vector mode
     float scale = 1.0f;
     const float* row_scales = nullptr;
+    // MFMA scan: when set, the last (partial) tile reads its 64 scales here (valid rows, then NaN)
+    // and every full tile reads row_scales directly; when null, row_scales is padded to whole
+    // tiles.
+    const float* tail_scales = nullptr;
     const void* queries = nullptr;  // f32 [batch, dim] | packed words [batch, W] | int8 [batch, dim]
     const float* query_scales = nullptr;
     int batch = 0;

@@ -43,8 +43,9 @@
 // 64 consecutive LDS slots, so each lane computes which global 16 bytes belong to its LDS slot.
 //
 // Row scales travel in a ring of their own, one deeper than the tile ring, so the scales of tile
-// t - 1 stay readable through step t. They come from a workspace copy of the scales padded to
-// whole tiles, in which masked and padding rows hold NaN; such a row scores -FLT_MAX.
+// t - 1 stay readable through step t. Full tiles read the caller's scales; with an allow-mask,
+// or for the partial last tile, they come from a workspace copy in which masked and padding
+// rows hold NaN; such a row scores -FLT_MAX.
 //
 // Filter of a threshold phase: per lane the largest (float)dot * s_r of the tile is compared with
 // the query's threshold score minus a relative margin of 2^-20 (far above the few-ulp difference
@@ -239,8 +240,10 @@ void mfmaScanKernel(ScanArgs scan, PhaseArgs phase, EmitArgs emit, int q_offset,
             }
         }
         if (wave == 0 && lane < kRows / 4) {
-            // the padded scale copy makes rows row0 .. row0 + 63 readable for every tile
-            copyToLds(scan.row_scales + row0, static_cast<std::uint32_t>(16 * lane),
+            // a full tile's 64 scales, or the padded copy of the partial last tile's
+            const float* scales = scan.tail_scales != nullptr && row0 + kRows > doc_count ? scan.tail_scales
+                                                                                          : scan.row_scales + row0;
+            copyToLds(scales, static_cast<std::uint32_t>(16 * lane),
                       __builtin_amdgcn_readfirstlane(ldsAddress(&scale_ring[sslot][0])));
         }
     };

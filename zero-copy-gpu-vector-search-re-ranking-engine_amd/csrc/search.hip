@@ -61,6 +61,7 @@ struct Plan {
     bool rescore = false;
     bool materialized = false;
     bool use_mfma = false;
+    bool direct_scales = false;  // MFMA path without a mask: only the tail tile's scales are copied
     int width = 0;  // keys selected by the scan stage
     int block_rows = 64;
     int workgroups = 1;
@@ -192,7 +193,12 @@ ScanArgs scanArgsOf(const zcgvs_search_desc& d, const Plan& plan, std::uint8_t* 
     if (plan.per_vector) {
         scan.row_scales = d.corpus.row_scales;
         if (plan.use_mfma) {
-            scan.row_scales = ws != nullptr ? reinterpret_cast<const float*>(ws + plan.mscales) : nullptr;
+            const float* staged = ws != nullptr ? reinterpret_cast<const float*>(ws + plan.mscales) : nullptr;
+            if (plan.direct_scales) {
+                scan.tail_scales = staged;
+            } else {
+                scan.row_scales = staged;
+            }
             scan.mask = nullptr;
         }
         scan.queries = ws != nullptr ? ws + plan.qi8 : nullptr;
@@ -247,8 +253,11 @@ Plan makePlan(const zcgvs_search_desc& d) {
         plan.qi8 = layout.add(static_cast<std::size_t>(batch) * dim);
         plan.qscale = layout.add(static_cast<std::size_t>(batch) * 4);
         if (plan.use_mfma) {
+            // Without a mask the scan reads the caller's scales and needs a padded copy of the
+            // last tile's only; with one, masked rows get NaN in a padded copy of all scales.
+            plan.direct_scales = d.mask == nullptr && aligned16(d.corpus.row_scales);
             const long long tiles = (n + kMfmaBlockRows - 1) / kMfmaBlockRows;
-            plan.mscales = layout.add(static_cast<std::size_t>(tiles) * kMfmaBlockRows * 4);
+            plan.mscales = layout.add(static_cast<std::size_t>(plan.direct_scales ? 1 : tiles) * kMfmaBlockRows * 4);
         }
     }
     plan.overflow = layout.add(static_cast<std::size_t>(batch) * 4);
@@ -421,14 +430,16 @@ int runMaterialized(const zcgvs_search_desc& d, const Plan& plan, std::uint8_t* 
 
 // The MFMA scan's row scales: the corpus scales padded to `padded` rows, with NaN (its
 // masked-row marker) for rows the allow-mask excludes and for the padding.
+// out[i] = scales[first + i] for allowed rows below n, NaN otherwise, for i < count.
 __global__ void mergeMaskedScalesKernel(const float* __restrict__ scales,
                                         const std::uint8_t* __restrict__ mask, long long n,
-                                        long long padded, float* __restrict__ out) {
+                                        long long first, long long count, float* __restrict__ out) {
     const long long stride = static_cast<long long>(gridDim.x) * blockDim.x;
-    for (long long i = static_cast<long long>(blockIdx.x) * blockDim.x + threadIdx.x; i < padded;
+    for (long long i = static_cast<long long>(blockIdx.x) * blockDim.x + threadIdx.x; i < count;
          i += stride) {
-        const bool allowed = i < n && (mask == nullptr || mask[i] != 0);
-        out[i] = allowed ? scales[i] : __uint_as_float(0x7FC00000u);
+        const long long row = first + i;
+        const bool allowed = row < n && (mask == nullptr || mask[row] != 0);
+        out[i] = allowed ? scales[row] : __uint_as_float(0x7FC00000u);
     }
 }
 
@@ -538,8 +549,14 @@ int searchTopk(const zcgvs_search_desc* desc, void* d_workspace, std::size_t wor
     if (plan.use_mfma) {
         const long long n = d.corpus.doc_count;
         const long long padded = (n + kMfmaBlockRows - 1) / kMfmaBlockRows * kMfmaBlockRows;
-        mergeMaskedScalesKernel<<<static_cast<unsigned>(std::min<long long>(8192, (padded + 255) / 256)), 256, 0, s>>>(
-            d.corpus.row_scales, d.mask, n, padded, at<float>(ws, plan.mscales));
+        if (plan.direct_scales) {
+            mergeMaskedScalesKernel<<<1, kMfmaBlockRows, 0, s>>>(d.corpus.row_scales, nullptr, n,
+                                                                 padded - kMfmaBlockRows, kMfmaBlockRows,
+                                                                 at<float>(ws, plan.mscales));
+        } else {
+            mergeMaskedScalesKernel<<<static_cast<unsigned>(std::min<long long>(8192, (padded + 255) / 256)), 256, 0, s>>>(
+                d.corpus.row_scales, d.mask, n, 0, padded, at<float>(ws, plan.mscales));
+        }
         ZCGVS_LAUNCH_CHECK("merge mask");
     }
     const ScanArgs scan = scanArgsOf(d, plan, ws);
