@@ -1,0 +1,100 @@
+"""Parity at the benchmark configurations' full sizes: 1M x 384 float32/float16 (batch 1 and 64),
+10M x 768 per-vector int8 (batch 256, k=100) and 50M x 1024 binary with a float16 rescore of 1000
+candidates (batch 32, k=10). Inputs are generated on the device at their real shapes by the seeded
+generator the benchmark uses. The CPU oracle checks sampled queries against the whole corpus
+(copied to the host); every query is checked for the properties that hold at any size (ids unique
+and in range, scores sorted, each returned score equal to the oracle's score of that id)."""
+
+from __future__ import annotations
+
+import numpy as np
+import pytest
+
+import bench
+import oracle
+from helpers import assert_topk_equivalent, float_tolerance
+
+pytestmark = pytest.mark.gpu
+
+
+def _search(capi, w):
+    desc, corpus, queries, keep = bench.build_inputs(capi, w)
+    idx, val, flags = capi.search(desc)
+    assert not flags.any(), "candidate overflow on a random corpus"
+    return idx, val, corpus, queries, keep
+
+
+def _ranked(idx, val, n):
+    for b in range(idx.shape[0]):
+        assert len(set(idx[b].tolist())) == idx.shape[1], f"query {b}: repeated id"
+        assert ((idx[b] >= 0) & (idx[b] < n)).all(), f"query {b}: id out of range"
+        assert np.all(np.diff(val[b].astype(np.float64)) <= 0), f"query {b}: scores not descending"
+
+
+@pytest.mark.parametrize("workload", ["f32-1m-b1", "f16-1m-b1", "f32-1m-b64", "f16-1m-b64"])
+def test_one_million_by_384_float(gpu, workload):
+    w = bench.WORKLOADS[workload]
+    idx, val, corpus, queries, _ = _search(gpu, w)
+    _ranked(idx, val, w["n"])
+    decoded = corpus.to_host().astype(np.float32)
+    host_q = queries.to_host()
+    tol = float_tolerance(host_q, decoded, oracle.COSINE)
+    assert_topk_equivalent(idx, val, oracle.scores_f32(decoded, host_q, oracle.COSINE), w["k"], tol)
+
+
+def test_ten_million_by_768_per_vector_int8(gpu):
+    w = bench.WORKLOADS["int8-10m"]
+    idx, val, corpus, queries, keep = _search(gpu, w)
+    _ranked(idx, val, w["n"])
+    codes = corpus.to_host()
+    scales = keep["scales"].to_host()
+    qcodes, qscales = oracle.quantize_rows_i8(queries.to_host())
+    # every query: the reported score of each returned id is the oracle's score, bit for bit
+    for b in range(w["batch"]):
+        rows = idx[b]
+        exact = oracle.scores_i8i8(codes[rows], scales[rows], qcodes[b:b + 1], qscales[b:b + 1])[0]
+        assert np.array_equal(val[b], exact), f"query {b}: scores differ from the oracle's"
+    # sampled queries: the whole top-100 against a scan of all 10M rows
+    sample = [0, 1, 77, 128, 255]
+    ref = oracle.scores_i8i8(codes, scales, qcodes[sample], qscales[sample])
+    assert_topk_equivalent(idx[sample], val[sample], ref, w["k"])
+
+
+def test_fifty_million_binary_with_fp16_rescore(gpu):
+    capi = gpu
+    w = bench.WORKLOADS["binary-50m"]
+    idx, val, corpus, queries, keep = _search(capi, w)
+    _ranked(idx, val, w["n"])
+    dim, c, k = w["dim"], w["candidates"], w["k"]
+    words = corpus.to_host()
+    host_q = queries.to_host()
+    half = keep["rescore"]
+
+    def rows_of(ids):
+        out = np.empty((len(ids), dim), dtype=np.float16)
+        for i, r in enumerate(ids):
+            capi.call("zcgvs_memcpy_d2h", out[i].ctypes.data, half.ptr + int(r) * dim * 2, dim * 2, None)
+        capi.synchronize()
+        return out.astype(np.float32)
+
+    # every query: each returned score is the float16 rescore of that id
+    for b in range(w["batch"]):
+        got = rows_of(idx[b])
+        exact = oracle.rescore(got, host_q[b:b + 1], np.arange(k, dtype=np.int32)[None, :])[0]
+        tol = float_tolerance(host_q[b:b + 1], got, oracle.COSINE)[0]
+        assert np.all(np.abs(val[b].astype(np.float64) - exact) <= tol), f"query {b}: rescore differs"
+    # sampled queries: Hamming top-1000 over all 50M rows, then the float16 rescore and top-10
+    qwords = oracle.pack_binary(host_q)
+    for b in (0, 31):
+        cand, _ = oracle.topk(oracle.scores_hamming(words, qwords[b:b + 1], dim), c)
+        rows = rows_of(cand[0])
+        rescored = oracle.rescore(rows, host_q[b:b + 1], np.arange(c, dtype=np.int32)[None, :])
+        tol = float_tolerance(host_q[b:b + 1], rows, oracle.COSINE)
+        ref_local, ref_val = oracle.topk(rescored, k)
+        position = {int(g): i for i, g in enumerate(cand[0])}
+        for r in range(k):
+            g, e = int(idx[b, r]), int(cand[0][ref_local[0, r]])
+            assert g in position, f"query {b} rank {r}: id {g} is not a Hamming top-{c} candidate"
+            if g != e:
+                assert abs(float(rescored[0, position[g]]) - float(ref_val[0, r])) <= (
+                    tol[0, position[g]] + tol[0, ref_local[0, r]]), f"query {b} rank {r}: not a near-tie"
