@@ -138,6 +138,8 @@ def measured_traffic(workload, kernel):
 def scan_kernel_name(w):
     if w["kind"] == "i8i8":
         return f"mfmaScanKernel<{w['dim'] // 32}, false>"
+    if w["kind"] in ("f32", "f16") and w["batch"] >= 4 and w["dim"] in (128, 256, 384, 512):
+        return f"mfmaFloatScanKernel<{0 if w['kind'] == 'f32' else 1}, {w['dim']}, false>"
     return "valuScanKernel"
 
 
@@ -270,9 +272,9 @@ def main(argv=None) -> int:
 
     batch = w["batch"]
     value = batch * args.steps / wall
-    # Dominant kernel: the scan launches of the threshold phases (the MFMA path compiles the dense
+    # Dominant kernel: the scan launches of the threshold phases (the MFMA paths compile the dense
     # first phase as a separate kernel; the VALU path runs every phase with one kernel).
-    first = 1 if w["kind"] == "i8i8" and used > 1 else 0
+    first = 1 if scan_kernel_name(w).startswith("mfma") and used > 1 else 0
     launches = list(range(first, used))
     mean_ms = statistics.mean(statistics.mean(phase_ms[i][p] for p in launches) for i in range(args.steps))
     bytes_launch = statistics.mean(phase_rows[p] * row_bytes(w) + query_bytes(w) for p in launches)

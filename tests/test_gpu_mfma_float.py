@@ -1,0 +1,82 @@
+"""Batched float32 / float16 searches (the matrix-core scan) against the CPU oracle.
+
+Batches of 4 or more queries over float32 or float16 rows of 128, 256, 384 or 512 dims take the
+MFMA scan; these cases cover every such row size, partial query groups (17), a batch over two
+launches (130), a partial last tile (n not a multiple of the tile rows), k = 1 and k = 100, both
+metrics, and query magnitudes far from 1 (the float16 path rescales each query by a power of two
+before splitting it). Ids must match the oracle's except at near-ties within the float32
+tolerance, and every score must be within it."""
+
+import numpy as np
+import pytest
+
+import oracle
+from helpers import assert_topk_equivalent, float_tolerance, normalized
+
+pytestmark = pytest.mark.gpu
+
+
+def search(capi, rows, dtype, queries, k, metric):
+    n, dim = rows.shape
+    store = capi.store_desc(capi.DeviceArray.from_host(rows), n, dim, dtype)
+    desc = capi.search_desc(store, capi.DeviceArray.from_host(queries), queries.shape[0], k, metric)
+    idx, val, flags = capi.search(desc)
+    assert not flags.any(), "candidate overflow on a random corpus"
+    return idx, val
+
+
+CASES = [
+    # kind, n, dim, batch, k, metric, query scale
+    ("f32", 60_013, 128, 17, 10, 0, 1.0),
+    ("f32", 60_013, 256, 17, 10, 1, 1.0),
+    ("f32", 100_003, 384, 4, 10, 0, 1.0),
+    ("f32", 100_003, 384, 64, 100, 1, 1.0),
+    ("f32", 100_003, 384, 130, 10, 0, 1.0),
+    ("f32", 60_013, 512, 33, 1, 0, 1.0),
+    ("f16", 60_013, 128, 17, 10, 0, 1.0),
+    ("f16", 60_013, 256, 17, 10, 1, 1.0),
+    ("f16", 100_003, 384, 4, 10, 0, 1.0),
+    ("f16", 100_003, 384, 64, 100, 1, 1.0),
+    ("f16", 100_003, 384, 130, 10, 0, 1.0),
+    ("f16", 60_013, 512, 33, 1, 0, 1.0),
+    ("f16", 100_003, 384, 16, 10, 1, 1000.0),
+    ("f16", 100_003, 384, 16, 10, 1, 1e-3),
+]
+
+
+@pytest.mark.parametrize("kind,n,dim,batch,k,metric,qscale", CASES)
+def test_batched_float_scan(gpu, kind, n, dim, batch, k, metric, qscale):
+    capi = gpu
+    corpus = normalized(n, dim, 100 + dim)
+    queries = (normalized(batch, dim, 200 + batch) * np.float32(qscale)).astype(np.float32)
+    if kind == "f32":
+        rows, dtype, decoded = corpus, capi.F32, corpus
+    else:
+        rows = oracle.f32_to_f16(corpus)
+        dtype, decoded = capi.F16, rows.astype(np.float32)
+    idx, val = search(capi, rows, dtype, queries, k, metric)
+    ref = oracle.scores_f32(decoded, queries, metric)
+    assert_topk_equivalent(idx, val, ref, k, float_tolerance(queries, decoded, metric))
+
+
+def test_batched_float_scan_ties(gpu):
+    # Row i repeats row i % 1000, so each class of 40 identical rows ties exactly on any path:
+    # within a class the result must hold its lowest ids, in ascending order.
+    capi = gpu
+    n, dim, batch, k = 40_000, 384, 8, 50
+    base = normalized(1000, dim, 5)
+    corpus = base[np.arange(n) % 1000]
+    queries = normalized(batch, dim, 6)
+    for kind in ("f32", "f16"):
+        rows = corpus if kind == "f32" else oracle.f32_to_f16(corpus)
+        dtype = capi.F32 if kind == "f32" else capi.F16
+        decoded = rows.astype(np.float32)
+        idx, val = search(capi, rows, dtype, queries, k, 0)
+        assert_topk_equivalent(idx, val, oracle.scores_f32(decoded, queries, 0), k,
+                               float_tolerance(queries, decoded, 0))
+        for b in range(batch):
+            classes = idx[b] % 1000
+            for c in np.unique(classes):
+                members = idx[b][classes == c]
+                lowest = c + 1000 * np.arange(len(members))
+                assert np.array_equal(members, lowest), f"{kind} query {b}: class {c} ids {members}"

@@ -61,6 +61,7 @@ struct Plan {
     bool rescore = false;
     bool materialized = false;
     bool use_mfma = false;
+    bool use_mfma_float = false;
     bool direct_scales = false;  // MFMA path without a mask: only the tail tile's scales are copied
     int width = 0;  // keys selected by the scan stage
     int block_rows = 64;
@@ -239,7 +240,8 @@ Plan makePlan(const zcgvs_search_desc& d) {
     }
     const bool forced = (d.flags & ZCGVS_SEARCH_MATERIALIZE) != 0;
     plan.use_mfma = !forced && mfmaSupported(probe);
-    plan.materialized = forced || (!plan.use_mfma && !valuSupported(probe));
+    plan.use_mfma_float = !forced && !plan.use_mfma && mfmaFloatSupported(probe);
+    plan.materialized = forced || (!plan.use_mfma && !plan.use_mfma_float && !valuSupported(probe));
     if (plan.per_vector && plan.materialized && dim % 16 != 0) {
         return fail(ZCGVS_ERR_INVALID_ARGUMENT,
                     "zcgvs: per-vector int8 mode needs dim % 16 == 0 and a 16-byte aligned corpus");
@@ -295,6 +297,9 @@ Plan makePlan(const zcgvs_search_desc& d) {
 
     if (plan.use_mfma) {
         plan.block_rows = kMfmaBlockRows;
+        plan.workgroups = mfmaWorkgroups();
+    } else if (plan.use_mfma_float) {
+        plan.block_rows = mfmaFloatBlockRows(probe);
         plan.workgroups = mfmaWorkgroups();
     } else {
         const ValuShape shape = valuShape(probe);
@@ -560,7 +565,7 @@ int searchTopk(const zcgvs_search_desc* desc, void* d_workspace, std::size_t wor
         ZCGVS_LAUNCH_CHECK("merge mask");
     }
     const ScanArgs scan = scanArgsOf(d, plan, ws);
-    if (plan.use_mfma && !mfmaSupported(scan)) {
+    if ((plan.use_mfma && !mfmaSupported(scan)) || (plan.use_mfma_float && !mfmaFloatSupported(scan))) {
         return setError(ZCGVS_ERR_INVALID_ARGUMENT, "zcgvs: corpus or queries are not 16-byte aligned");
     }
     EmitArgs emit;
@@ -583,8 +588,13 @@ int searchTopk(const zcgvs_search_desc* desc, void* d_workspace, std::size_t wor
         if (timed) {
             ZCGVS_HIP_RETURN(hipEventRecord(reinterpret_cast<hipEvent_t>(events[2 * p]), s));
         }
-        status = plan.use_mfma ? launchMfmaScan(scan, phase, emit, plan.workgroups, s)
-                               : launchValuScan(scan, phase, emit, plan.workgroups, s);
+        if (plan.use_mfma) {
+            status = launchMfmaScan(scan, phase, emit, plan.workgroups, s);
+        } else if (plan.use_mfma_float) {
+            status = launchMfmaFloatScan(scan, phase, emit, plan.workgroups, s);
+        } else {
+            status = launchValuScan(scan, phase, emit, plan.workgroups, s);
+        }
         if (status != ZCGVS_OK) {
             return status;
         }
