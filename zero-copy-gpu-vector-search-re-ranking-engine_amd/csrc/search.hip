@@ -30,7 +30,12 @@ bool valuSupported(const ScanArgs& scan);
 namespace {
 
 constexpr std::size_t kAlign = 256;
+// Each threshold phase visits up to `growth` times as many rows as all phases before it, so it
+// yields about width * growth candidates per query on a corpus in random order. The growth is 8,
+// or larger while batch * width * growth stays within kCandidateBudget keys (small batches and k
+// then need only a dense sample and one threshold phase).
 constexpr long long kPhaseGrowth = 8;
+constexpr long long kCandidateBudget = 1LL << 18;
 
 std::size_t alignUp(std::size_t value) { return (value + kAlign - 1) / kAlign * kAlign; }
 
@@ -308,7 +313,11 @@ Plan makePlan(const zcgvs_search_desc& d) {
     }
 
     // Phase schedule: phase 0 samples ~max(16 * width, 4096) rows densely; each later phase
-    // visits up to kPhaseGrowth times as many blocks as all phases before it.
+    // visits up to growth_cap times as many blocks as all phases before it.
+    long long growth_cap = kPhaseGrowth;
+    while (growth_cap * 2 * batch * plan.width <= kCandidateBudget) {
+        growth_cap *= 2;
+    }
     const long long blocks = (n + plan.block_rows - 1) / plan.block_rows;
     const long long target_rows = std::max<long long>(16LL * plan.width, 4096);
     const long long blocks0 = (target_rows + plan.block_rows - 1) / plan.block_rows;
@@ -325,7 +334,7 @@ Plan makePlan(const zcgvs_search_desc& d) {
     plan.phases.push_back(first);
     long long growth = 1;
     while (stride > 1) {
-        const long long next = std::max<long long>(1, stride / kPhaseGrowth);
+        const long long next = std::max<long long>(1, stride / growth_cap);
         PhaseArgs phase;
         phase.stride = next;
         phase.skip = stride / next;
@@ -518,9 +527,6 @@ int searchTopk(const zcgvs_search_desc* desc, void* d_workspace, std::size_t wor
     const int dim = d.corpus.dim;
     int status = ZCGVS_OK;
 
-    zeroWordsKernel<<<1, 256, 0, s>>>(at<std::uint32_t>(ws, plan.overflow), static_cast<std::size_t>(batch));
-    ZCGVS_LAUNCH_CHECK("zero flags");
-
     // 1. queries
     if (plan.binary) {
         status = zcgvs_launch_pack_binary(d.queries, ws + plan.qbits, batch, dim, stream);
@@ -536,6 +542,9 @@ int searchTopk(const zcgvs_search_desc* desc, void* d_workspace, std::size_t wor
         if (phases_out != nullptr) {
             *phases_out = 0;
         }
+        // the materialized pipeline never overflows; its flags are simply cleared
+        zeroWordsKernel<<<1, 256, 0, s>>>(at<std::uint32_t>(ws, plan.overflow), static_cast<std::size_t>(batch));
+        ZCGVS_LAUNCH_CHECK("zero flags");
         status = runMaterialized(d, plan, ws, d_out_indices, d_out_values, s);
         return status == ZCGVS_OK ? clearError() : status;
     }
@@ -606,6 +615,7 @@ int searchTopk(const zcgvs_search_desc* desc, void* d_workspace, std::size_t wor
             in.dense = emit.dense;
             in.n_dense = phase.items * phase.block_rows;
             in.dense_stride = plan.dense_stride;
+            in.reset_overflow = true;
         } else {
             in.prev = keys;
             in.k_prev = plan.width;

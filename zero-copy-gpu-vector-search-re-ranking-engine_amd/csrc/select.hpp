@@ -39,10 +39,42 @@ __device__ __forceinline__ std::uint64_t selectThreshold(const SelectState& s) {
     return s.bits >= 64 ? s.prefix : (s.prefix << (64 - s.bits));
 }
 
+// Inclusive sum of `value` over the block's threads in thread order (threads 0..t), for a block
+// of kSelectThreads threads: a shuffle scan inside each wavefront, then the wavefront totals
+// through LDS (`wave_sums`, kSelectThreads / kWave words). `total` receives the block's sum.
+// Two barriers; every thread must call it.
+__device__ inline std::uint32_t blockInclusiveSum(std::uint32_t value, std::uint32_t* wave_sums,
+                                                  std::uint32_t* total) {
+    const int lane = threadIdx.x & (kWave - 1);
+    const int wave = threadIdx.x / kWave;
+#pragma unroll
+    for (int offset = 1; offset < kWave; offset <<= 1) {
+        const std::uint32_t other = __shfl_up(value, offset, kWave);
+        if (lane >= offset) {
+            value += other;
+        }
+    }
+    if (lane == kWave - 1) {
+        wave_sums[wave] = value;
+    }
+    __syncthreads();
+    std::uint32_t before = 0u;
+    std::uint32_t sum = 0u;
+#pragma unroll
+    for (int w = 0; w < kSelectThreads / kWave; ++w) {
+        const std::uint32_t v = wave_sums[w];
+        before += w < wave ? v : 0u;
+        sum += v;
+    }
+    __syncthreads();  // wave_sums is free again
+    *total = sum;
+    return value + before;
+}
+
 // Given a full histogram of the current digit, pick the bucket holding the need-th best key and
 // update the state. Runs on one block of kSelectThreads threads; `scratch` is LDS of
-// kSelectThreads u32. The histogram may be in LDS or global memory (read with plain loads; the
-// caller makes it visible first).
+// kSelectThreads / kWave u32. The histogram may be in LDS or global memory (read with plain
+// loads; the caller makes it visible first).
 __device__ inline void selectPickBucket(const std::uint32_t* hist, int width, SelectState* state,
                                         std::uint32_t* scratch) {
     const int bins = 1 << width;
@@ -54,19 +86,10 @@ __device__ inline void selectPickBucket(const std::uint32_t* hist, int width, Se
     for (int b = top - 1; b >= top - per_thread; --b) {
         local += hist[b];
     }
-    scratch[t] = local;
-    __syncthreads();
-    // Inclusive scan over threads (from the top bins down), Hillis-Steele.
-    for (int offset = 1; offset < kSelectThreads; offset <<= 1) {
-        const std::uint32_t add = t >= offset ? scratch[t - offset] : 0u;
-        __syncthreads();
-        scratch[t] += add;
-        __syncthreads();
-    }
     const std::uint32_t need = state->need;
-    const std::uint32_t before = t == 0 ? 0u : scratch[t - 1];
-    const std::uint32_t through = scratch[t];
-    __syncthreads();
+    std::uint32_t total = 0u;
+    const std::uint32_t through = blockInclusiveSum(local, scratch, &total);
+    const std::uint32_t before = through - local;
     if (before < need && need <= through) {
         std::uint32_t above = before;
         for (int b = top - 1; b >= top - per_thread; --b) {
@@ -123,11 +146,15 @@ struct MergeInputs {
     const std::uint32_t* seg_count = nullptr;
     int n_seg = 0;
     int seg_log2 = 0;
+    // true for the first merge of a search: it writes every query's overflow flag (0 or 1)
+    // instead of only raising flags, so no separate clearing pass is needed
+    bool reset_overflow = false;
 };
 
 // Selects the best k keys of each query's candidate set; writes them sorted descending to
 // out_keys[q][0..k), sets threshold[q] to the k-th best key (0 if fewer than k keys exist) and
-// sets overflow[q] when a segment count exceeded its capacity. When out_index/out_score are
+// sets overflow[q] when a segment count exceeded its capacity (and clears it otherwise when
+// in.reset_overflow is set). When out_index/out_score are
 // non-null the selection is also written as (index, score) pairs [batch, k].
 int launchSelectMerge(const MergeInputs& in, int k, int batch, std::uint64_t* out_keys,
                       std::uint64_t* threshold, std::uint32_t* overflow, int* out_index,

@@ -183,6 +183,7 @@ __device__ __forceinline__ void forEachCandidate(const MergeInputs& in, int q, i
     }
     if (in.dense != nullptr) {
         const std::uint64_t* dense = in.dense + static_cast<std::size_t>(q) * in.dense_stride;
+#pragma unroll 8
         for (long long i = threadIdx.x; i < in.n_dense; i += blockDim.x) {
             const std::uint64_t key = dense[i];
             if (key != 0ull) {
@@ -193,6 +194,7 @@ __device__ __forceinline__ void forEachCandidate(const MergeInputs& in, int q, i
     if (in.seg != nullptr) {
         const long long total = static_cast<long long>(in.n_seg) << in.seg_log2;
         const long long mask = (1LL << in.seg_log2) - 1;
+#pragma unroll 8
         for (long long i = threadIdx.x; i < total; i += blockDim.x) {
             const int s = static_cast<int>(i >> in.seg_log2);
             const long long j = i & mask;
@@ -255,15 +257,8 @@ __global__ __launch_bounds__(kSelectThreads) void selectMergeKernel(
         const int s = t * per_thread + i;
         run += s < in.n_seg ? lds_seg[s] : 0u;
     }
-    lds_scan[t] = run;
-    __syncthreads();
-    for (int offset = 1; offset < kSelectThreads; offset <<= 1) {
-        const std::uint32_t add = t >= offset ? lds_scan[t - offset] : 0u;
-        __syncthreads();
-        lds_scan[t] += add;
-        __syncthreads();
-    }
-    std::uint32_t acc = t == 0 ? 0u : lds_scan[t - 1];
+    std::uint32_t seg_total = 0u;
+    std::uint32_t acc = blockInclusiveSum(run, lds_scan, &seg_total) - run;
     for (int i = 0; i < per_thread; ++i) {
         const int s = t * per_thread + i;
         if (s < in.n_seg) {
@@ -271,7 +266,6 @@ __global__ __launch_bounds__(kSelectThreads) void selectMergeKernel(
             acc += lds_seg[s];
         }
     }
-    const std::uint32_t seg_total = lds_scan[kSelectThreads - 1];
     const std::uint32_t k_prev = in.prev != nullptr ? static_cast<std::uint32_t>(in.k_prev) : 0u;
     const std::uint32_t n_dense = in.dense != nullptr ? static_cast<std::uint32_t>(in.n_dense) : 0u;
     const std::uint64_t gathered = static_cast<std::uint64_t>(k_prev) + n_dense + seg_total;
@@ -287,6 +281,7 @@ __global__ __launch_bounds__(kSelectThreads) void selectMergeKernel(
         }
         if (n_dense > 0u) {
             const std::uint64_t* dense = in.dense + static_cast<std::size_t>(q) * in.dense_stride;
+#pragma unroll 8
             for (std::uint32_t i = t; i < n_dense; i += blockDim.x) {
                 lds_cand[k_prev + i] = dense[i];
             }
@@ -390,8 +385,8 @@ __global__ __launch_bounds__(kSelectThreads) void selectMergeKernel(
         if (threshold != nullptr) {
             threshold[q] = taken >= static_cast<std::uint32_t>(k) ? lds_keys[k - 1] : 0ull;
         }
-        if (lds_overflow != 0u && overflow != nullptr) {
-            overflow[q] = 1u;
+        if (overflow != nullptr && (lds_overflow != 0u || in.reset_overflow)) {
+            overflow[q] = lds_overflow != 0u ? 1u : 0u;
         }
     }
 }
