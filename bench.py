@@ -140,6 +140,8 @@ def scan_kernel_name(w):
         return f"mfmaScanKernel<{w['dim'] // 32}, false>"
     if w["kind"] in ("f32", "f16") and w["batch"] >= 4 and w["dim"] in (128, 256, 384, 512):
         return f"mfmaFloatScanKernel<{0 if w['kind'] == 'f32' else 1}, {w['dim']}, false>"
+    if w["kind"] == "binary" and w["batch"] >= 4 and w["dim"] in (512, 1024):
+        return f"mfmaBinaryScanKernel<{w['dim'] // 32}, false>"
     return "valuScanKernel"
 
 

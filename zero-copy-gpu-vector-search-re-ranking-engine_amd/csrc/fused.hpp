@@ -125,4 +125,11 @@ int mfmaFloatBlockRows(const ScanArgs& scan);
 int launchMfmaFloatScan(const ScanArgs& scan, const PhaseArgs& phase, const EmitArgs& emit,
                         int workgroups, hipStream_t stream);
 
+// The binary (Hamming) MFMA scan (batches of at least 4 queries, no mask or lexical scores,
+// dim 512 or 1024).
+bool mfmaBinarySupported(const ScanArgs& scan);
+int mfmaBinaryBlockRows(const ScanArgs& scan);
+int launchMfmaBinaryScan(const ScanArgs& scan, const PhaseArgs& phase, const EmitArgs& emit,
+                         int workgroups, hipStream_t stream);
+
 }  // namespace zcgvs_hip

@@ -1,0 +1,408 @@
+// Binary (1-bit) MFMA fused scan: Hamming distances of sign-packed corpus rows to a batch of
+// sign-packed queries on the int8 matrix cores, with the threshold emission of fused.hpp. The
+// reference computes popc(c ^ q) word by word on the VALU (src/cuda/similarity.cu:169-238,
+// hammingScanKernel) and scores (d - 2h) / d (include/zcgvs/cuda/decode.cuh:45-47).
+//
+// Arithmetic. With r the row's bits and q the query's bits as 0/1 values,
+//   sum_k r_k (1 - 2 q_k) = popc(r) - 2 r.q,  so  h = popc(r) + popc(q) - 2 r.q = acc + popc(q)
+// where acc is the int8 MFMA product of the row as 0/1 bytes (A) with the query as +-1 bytes (B).
+// Integer arithmetic throughout, so h is exact; the score is the reference's IEEE division
+// (d - 2h) / d. A threshold phase compares h itself with the integer threshold equivalent to the
+// query's key threshold (scores are strictly decreasing in h), so the division runs only for
+// keys that pass.
+//
+// Expansion. Each lane turns 16 bits of its row into 16 bytes per k-step: four nibbles, each
+// spread to the low bits of four bytes by (n * 0x204081) & 0x01010101 (the partial products
+// n << 0, 7, 14, 21 do not overlap). That VALU work is shared by the two query groups of 16 a
+// wavefront serves.
+//
+// Work split. 8 wavefronts; a wavefront serves a set of up to 32 queries (two groups of 16, B
+// operands in registers for the whole launch) and a share of each tile's 16-row blocks; with
+// more than one set per launch (up to 4, 128 queries) the wavefronts of a set split the blocks.
+//
+// MFMA layout (v_mfma_i32_16x16x64_i8). Lane l supplies row (A) / query (B) l % 16 and 16 dims
+// of lane group h = l / 16 per step: 16-byte chunk h + 4j of the row covers steps 8j .. 8j + 7,
+// two 16-bit halves of each of its words in turn; A and B use the same assignment, so every
+// dim is counted once. D: lane l holds query l % 16 and rows 4h + i, i < 4.
+//
+// Corpus streaming as in the other MFMA scans (lds_copy.hpp): ~32 KB tiles HBM -> LDS by
+// global_load_lds_dwordx4 in a 4-deep ring. LDS slot s of row r holds chunk s ^ swz(r) with
+// swz(r) = (r / (256 / row bytes)) & (chunks - 1), so the 16 rows of one ds_read_b128
+// quarter-wave hit 16 distinct 16-byte bank groups.
+#include <hip/hip_runtime.h>
+
+#include <algorithm>
+
+#include "common.hpp"
+#include "fused.hpp"
+#include "lds_copy.hpp"
+
+namespace zcgvs_hip {
+
+namespace {
+
+typedef int v4i __attribute__((ext_vector_type(4)));
+typedef unsigned int u32x4 __attribute__((ext_vector_type(4)));
+
+constexpr int kThreads = 512;
+constexpr int kWaves = kThreads / kWave;
+constexpr int kSetQueries = 32;  // two MFMA query groups of 16 per wavefront
+constexpr int kQueriesPerLaunch = 4 * kSetQueries;
+constexpr int kTileBytesTarget = 32 * 1024;
+constexpr int kMinBatch = 4;  // below this the VALU popcount scan does less work per row
+
+template <int kWords>
+struct BinaryTile {
+    static constexpr int kRowBytes = kWords * 4;
+    static constexpr int kChunks = kRowBytes / 16;
+    static constexpr int kLaneChunks = kChunks / 4;  // chunks per lane group
+    static constexpr int kSteps = kLaneChunks * 8;   // 64 dims per step
+    static constexpr int kRows = kTileBytesTarget / kRowBytes;
+    static constexpr int kRowBlocks = kRows / 16;
+    static constexpr int kTileBytes = kRows * kRowBytes;
+    static constexpr int kDepth = 4;
+    static constexpr int kCopies = kTileBytes / 16 / kThreads;
+    static constexpr int kRowsPerBankPeriod = 256 / kRowBytes;
+    static_assert(kChunks % 4 == 0 && kChunks <= 8, "rows of 64 or 128 bytes (queries in registers)");
+    static_assert(kTileBytes % (16 * kThreads) == 0, "tile must split over the lanes");
+    static_assert(3 * kCopies < 63, "copies in flight fit the vmcnt counter");
+    __host__ __device__ static constexpr int swizzle(int row) {
+        return (row / kRowsPerBankPeriod) & (kChunks - 1);
+    }
+};
+
+// 16 bits -> 16 bytes of 0/1 (byte e of dword j = bit 4j + e).
+__device__ __forceinline__ v4i spreadBits(std::uint32_t bits16) {
+    v4i out;
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+        const std::uint32_t nibble = __builtin_amdgcn_ubfe(bits16, 4 * j, 4);
+        out[j] = static_cast<int>(__umul24(nibble, 0x204081u) & 0x01010101u);
+    }
+    return out;
+}
+
+// 16 bits -> 16 bytes of +1 (bit clear) / -1 (bit set).
+__device__ __forceinline__ v4i signBytes(std::uint32_t bits16) {
+    v4i out;
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+        std::uint32_t word = 0u;
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+            const std::uint32_t bit = (bits16 >> (4 * j + e)) & 1u;
+            word |= (bit ? 0xFFu : 0x01u) << (8 * e);
+        }
+        out[j] = static_cast<int>(word);
+    }
+    return out;
+}
+
+// 16 bits of step t (lane group h) from the lane's chunk words: chunk jc = t / 8, word (t % 8) / 2,
+// half t % 2.
+template <int kLaneChunks>
+__device__ __forceinline__ std::uint32_t stepBits(const u32x4 (&chunk)[kLaneChunks], int t) {
+    const std::uint32_t word = chunk[t / 8][(t % 8) / 2];
+    return (t % 2) ? (word >> 16) : (word & 0xFFFFu);
+}
+
+template <int kWords, bool kDense>
+__global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(2, 2)))
+void mfmaBinaryScanKernel(ScanArgs scan, PhaseArgs phase, EmitArgs emit, int q_offset, int q_count) {
+    using Tile = BinaryTile<kWords>;
+    constexpr int kRows = Tile::kRows;
+    constexpr int kRowBytes = Tile::kRowBytes;
+    constexpr int kChunks = Tile::kChunks;
+    constexpr int kLaneChunks = Tile::kLaneChunks;
+    constexpr int kSteps = Tile::kSteps;
+    constexpr int kDepth = Tile::kDepth;
+    constexpr int kCopies = Tile::kCopies;
+    constexpr int kRowBlocks = Tile::kRowBlocks;
+    constexpr int kDim = kWords * 32;
+
+    __shared__ __attribute__((aligned(16))) std::uint8_t ring[kDepth][Tile::kTileBytes];
+    __shared__ std::uint32_t lds_count[kQueriesPerLaunch];
+
+    const int tid = threadIdx.x;
+    const int lane = tid & (kWave - 1);
+    const int wave = tid / kWave;
+    const int r16 = lane & 15;
+    const int h = lane >> 4;
+    const int sets = (q_count + kSetQueries - 1) / kSetQueries;
+    const int waves_per_set = kWaves / sets;
+    const bool wave_active = wave < sets * waves_per_set;
+    const int set = wave % sets;
+    const int first_block = wave / sets;
+    const bool two_groups = set * kSetQueries + 16 < q_count;  // wave-uniform
+    const long long doc_count = scan.doc_count;
+    const std::uint8_t* corpus = static_cast<const std::uint8_t*>(scan.corpus);
+    const std::uint32_t* qwords = static_cast<const std::uint32_t*>(scan.queries);
+
+    // ---- per query group g of the set: B operands, popc(q), integer threshold ----
+    v4i qb[2][kSteps];
+    int popq[2];
+    int q_of[2];
+    bool valid_of[2];
+    int h_limit[2];          // keys pass when h < h_limit, or h == h_limit and row < row_limit
+    std::uint32_t row_limit[2];
+#pragma unroll
+    for (int g = 0; g < 2; ++g) {
+        const int qlocal = set * kSetQueries + g * 16 + r16;
+        valid_of[g] = wave_active && qlocal < q_count;
+        const int q = q_offset + min(qlocal, q_count - 1);
+        q_of[g] = q;
+        const std::uint32_t* qrow = qwords + static_cast<std::size_t>(q) * kWords;
+        u32x4 chunk[kLaneChunks];
+#pragma unroll
+        for (int jc = 0; jc < kLaneChunks; ++jc) {
+            chunk[jc] = *reinterpret_cast<const u32x4*>(qrow + 4 * (h + 4 * jc));
+        }
+        int pop = 0;
+#pragma unroll
+        for (int jc = 0; jc < kLaneChunks; ++jc) {
+#pragma unroll
+            for (int w = 0; w < 4; ++w) {
+                pop += __popc(chunk[jc][w]);
+            }
+        }
+        // the four lane groups hold disjoint chunks of the query
+        pop += waveXor(pop, 16);
+        pop += waveXor(pop, 32);
+        popq[g] = pop;
+#pragma unroll
+        for (int t = 0; t < kSteps; ++t) {
+            qb[g][t] = valid_of[g] ? signBytes(stepBits<kLaneChunks>(chunk, t)) : v4i{0, 0, 0, 0};
+        }
+        h_limit[g] = kDim + 1;  // no threshold: every h passes
+        row_limit[g] = 0xFFFFFFFFu;
+        if constexpr (!kDense) {
+            const std::uint64_t tau = emit.tau[q];
+            if (tau != 0ull) {
+                const float t_score = keyScore(tau);
+                // the h whose score (d - 2h) / d is exactly the threshold's score
+                const float estimate = (static_cast<float>(kDim) - t_score * static_cast<float>(kDim)) * 0.5f;
+                int ht = estimate >= 0.0f && estimate <= static_cast<float>(kDim) ? static_cast<int>(rintf(estimate)) : 0;
+                for (int c = max(0, ht - 2); c <= min(kDim, ht + 2); ++c) {
+                    if (static_cast<float>(kDim - 2 * c) / static_cast<float>(kDim) == t_score) {
+                        ht = c;
+                    }
+                }
+                h_limit[g] = ht;
+                row_limit[g] = 0xFFFFFFFFu - static_cast<std::uint32_t>(tau);
+            }
+        }
+    }
+    // acc threshold of the fast reject (invalid queries never pass)
+    int acc_limit[2];
+#pragma unroll
+    for (int g = 0; g < 2; ++g) {
+        acc_limit[g] = valid_of[g] ? h_limit[g] - popq[g] : -(kDim + 1);
+    }
+    for (int i = tid; i < kQueriesPerLaunch; i += kThreads) {
+        lds_count[i] = 0u;
+    }
+
+    // ---- copy plan ----
+    std::uint32_t copy_off[kCopies];
+#pragma unroll
+    for (int i = 0; i < kCopies; ++i) {
+        const int p = (wave * kCopies + i) * kWave + lane;
+        const int row = p / kChunks;
+        const int slot = p - row * kChunks;
+        copy_off[i] = static_cast<std::uint32_t>(row * kRowBytes + (slot ^ Tile::swizzle(row)) * 16);
+    }
+    auto issue = [&](long long item, int slot) {
+        const long long row0 = phaseBlock(item, phase.stride, phase.skip) * kRows;
+        const std::uint8_t* base = corpus + static_cast<std::size_t>(row0) * kRowBytes;
+        const std::uint32_t slot_base = ldsAddress(&ring[slot][0]);
+        if (row0 + kRows <= doc_count) {
+#pragma unroll
+            for (int i = 0; i < kCopies; ++i) {
+                copyToLds(base, copy_off[i],
+                          __builtin_amdgcn_readfirstlane(slot_base + (wave * kCopies + i) * kWave * 16));
+            }
+        } else {
+            const int last = static_cast<int>(doc_count - row0) - 1;
+#pragma unroll
+            for (int i = 0; i < kCopies; ++i) {
+                const int row = static_cast<int>(copy_off[i]) / kRowBytes;
+                const std::uint32_t off = copy_off[i] - static_cast<std::uint32_t>((row - min(row, last)) * kRowBytes);
+                copyToLds(base, off, __builtin_amdgcn_readfirstlane(slot_base + (wave * kCopies + i) * kWave * 16));
+            }
+        }
+    };
+
+    const long long stride_items = gridDim.x;
+    long long item = blockIdx.x;
+#pragma unroll
+    for (int d = 0; d < kDepth - 1; ++d) {
+        if (item + d * stride_items < phase.items) {
+            issue(item + d * stride_items, d);
+        }
+    }
+    __syncthreads();  // lds_count initialization visible
+
+    auto arrive = [&](long long it) {
+        int later = 0;
+#pragma unroll
+        for (int d = 1; d <= kDepth - 2; ++d) {
+            later += it + d * stride_items < phase.items ? 1 : 0;
+        }
+        waitTiles<kCopies, kDepth - 2>(later);
+        __builtin_amdgcn_s_barrier();
+        asm volatile("" ::: "memory");  // no LDS access moves above the barrier
+    };
+
+    // chunk h + 4 jc of row r16 of a block
+    std::uint32_t a_off[kLaneChunks];
+#pragma unroll
+    for (int jc = 0; jc < kLaneChunks; ++jc) {
+        a_off[jc] = static_cast<std::uint32_t>(r16 * kRowBytes + ((h + 4 * jc) ^ Tile::swizzle(r16)) * 16);
+    }
+
+    auto emitKeys = [&](const v4i& acc, int g, long long row0, int block, long long item_) {
+        if (!valid_of[g]) {
+            return;
+        }
+        const int q = q_of[g];
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+            const int local = block * 16 + 4 * h + i;
+            const long long row = row0 + local;
+            const int hd = acc[i] + popq[g];
+            if constexpr (kDense) {
+                std::uint64_t key = 0ull;
+                if (row < doc_count) {
+                    const float score = static_cast<float>(kDim - 2 * hd) / static_cast<float>(kDim);
+                    key = makeKey(score, static_cast<std::uint32_t>(row));
+                }
+                emit.dense[static_cast<std::size_t>(q) * emit.dense_stride + item_ * kRows + local] = key;
+            } else {
+                const std::uint32_t r32 = static_cast<std::uint32_t>(row);
+                const bool pass = hd < h_limit[g] || (hd == h_limit[g] && r32 < row_limit[g]);
+                if (pass && row < doc_count) {
+                    const float score = static_cast<float>(kDim - 2 * hd) / static_cast<float>(kDim);
+                    appendCandidate(emit, lds_count, q, q_offset, scan.batch, makeKey(score, r32));
+                }
+            }
+        }
+    };
+
+    int slot = 0;
+    for (; item < phase.items; item += stride_items) {
+        arrive(item);
+        {
+            const long long ahead = item + (kDepth - 1) * stride_items;
+            if (ahead < phase.items) {
+                issue(ahead, slot == 0 ? kDepth - 1 : slot - 1);
+            }
+        }
+        if (wave_active) {
+            const long long row0 = phaseBlock(item, phase.stride, phase.skip) * kRows;
+            for (int block = first_block; block < kRowBlocks; block += waves_per_set) {
+                const std::uint8_t* rows = ring[slot] + block * 16 * kRowBytes;
+                u32x4 chunk[kLaneChunks];
+#pragma unroll
+                for (int jc = 0; jc < kLaneChunks; ++jc) {
+                    chunk[jc] = *reinterpret_cast<const u32x4*>(rows + a_off[jc]);
+                }
+                v4i acc0 = {0, 0, 0, 0};
+                v4i acc1 = {0, 0, 0, 0};
+                // One path for one or two query groups (the second group's B operands are zero
+                // when it has no queries), so the compiler has no two copies of the expansion
+                // to hoist. The A operand is double-buffered: step t's MFMAs are issued first,
+                // then step t + 1's expansion into the other buffer, which the matrix core is
+                // not reading, so the VALU work runs under the MFMAs instead of waiting for them
+                // to read their operands; a sched_barrier per step pins that order.
+                v4i a[2];
+                a[0] = spreadBits(stepBits<kLaneChunks>(chunk, 0));
+#pragma unroll
+                for (int t = 0; t < kSteps; ++t) {
+                    acc0 = __builtin_amdgcn_mfma_i32_16x16x64_i8(a[t % 2], qb[0][t], acc0, 0, 0, 0);
+                    acc1 = __builtin_amdgcn_mfma_i32_16x16x64_i8(a[t % 2], qb[1][t], acc1, 0, 0, 0);
+                    if (t + 1 < kSteps) {
+                        a[(t + 1) % 2] = spreadBits(stepBits<kLaneChunks>(chunk, t + 1));
+                        // keeps step t's operand allocated until the expansion is written, so
+                        // the two buffers never share registers
+                        asm volatile("" ::"v"(a[t % 2]));
+                    }
+                    __builtin_amdgcn_sched_barrier(0);
+                }
+                if constexpr (kDense) {
+                    emitKeys(acc0, 0, row0, block, item);
+                    if (two_groups) {
+                        emitKeys(acc1, 1, row0, block, item);
+                    }
+                } else {
+                    // Fast reject: a key can pass only if acc <= h_limit - popc(q) (h = acc +
+                    // popc(q)); one ballot over the wavefront's 8 products usually ends here.
+                    const int m0 = min(min(acc0[0], acc0[1]), min(acc0[2], acc0[3]));
+                    const int m1 = min(min(acc1[0], acc1[1]), min(acc1[2], acc1[3]));
+                    const bool maybe = m0 <= acc_limit[0] || m1 <= acc_limit[1];
+                    if (__builtin_amdgcn_ballot_w64(maybe) != 0) {
+                        emitKeys(acc0, 0, row0, block, item);
+                        if (two_groups) {
+                            emitKeys(acc1, 1, row0, block, item);
+                        }
+                    }
+                }
+            }
+        }
+        slot = slot + 1 == kDepth ? 0 : slot + 1;
+    }
+    if constexpr (!kDense) {
+        __syncthreads();
+        for (int i = tid; i < q_count; i += kThreads) {
+            emit.seg_count[static_cast<std::size_t>(blockIdx.x) * scan.batch + q_offset + i] = lds_count[i];
+        }
+    }
+}
+
+template <int kWords>
+int launchShape(const ScanArgs& scan, const PhaseArgs& phase, const EmitArgs& emit, int workgroups,
+                hipStream_t stream) {
+    const long long wanted = phase.dense ? std::min<long long>(phase.items, workgroups) : workgroups;
+    const dim3 grid(static_cast<unsigned>(std::max(1LL, wanted)));
+    for (int q0 = 0; q0 < scan.batch; q0 += kQueriesPerLaunch) {
+        const int count = std::min(kQueriesPerLaunch, scan.batch - q0);
+        if (phase.dense) {
+            mfmaBinaryScanKernel<kWords, true><<<grid, kThreads, 0, stream>>>(scan, phase, emit, q0, count);
+        } else {
+            mfmaBinaryScanKernel<kWords, false><<<grid, kThreads, 0, stream>>>(scan, phase, emit, q0, count);
+        }
+        ZCGVS_LAUNCH_CHECK("binary mfma scan");
+    }
+    return ZCGVS_OK;
+}
+
+}  // namespace
+
+bool mfmaBinarySupported(const ScanArgs& scan) {
+    if (scan.dtype != ZCGVS_DTYPE_BINARY || scan.mask != nullptr || scan.lexical != nullptr ||
+        scan.batch < kMinBatch) {
+        return false;
+    }
+    if (!aligned16(scan.corpus) || !aligned16(scan.queries)) {
+        return false;
+    }
+    return scan.dim == 512 || scan.dim == 1024;
+}
+
+int mfmaBinaryBlockRows(const ScanArgs& scan) {
+    return scan.dim == 512 ? BinaryTile<16>::kRows : BinaryTile<32>::kRows;
+}
+
+int launchMfmaBinaryScan(const ScanArgs& scan, const PhaseArgs& phase, const EmitArgs& emit,
+                         int workgroups, hipStream_t stream) {
+    if (phase.items <= 0) {
+        return ZCGVS_OK;
+    }
+    switch (scan.dim) {
+        case 512: return launchShape<16>(scan, phase, emit, workgroups, stream);
+        case 1024: return launchShape<32>(scan, phase, emit, workgroups, stream);
+        default:
+            return setError(ZCGVS_ERR_INVALID_ARGUMENT, "zcgvs: binary MFMA scan does not take this shape");
+    }
+}
+
+}  // namespace zcgvs_hip

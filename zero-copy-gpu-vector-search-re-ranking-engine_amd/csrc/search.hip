@@ -67,6 +67,7 @@ struct Plan {
     bool materialized = false;
     bool use_mfma = false;
     bool use_mfma_float = false;
+    bool use_mfma_binary = false;
     bool direct_scales = false;  // MFMA path without a mask: only the tail tile's scales are copied
     int width = 0;  // keys selected by the scan stage
     int block_rows = 64;
@@ -246,7 +247,9 @@ Plan makePlan(const zcgvs_search_desc& d) {
     const bool forced = (d.flags & ZCGVS_SEARCH_MATERIALIZE) != 0;
     plan.use_mfma = !forced && mfmaSupported(probe);
     plan.use_mfma_float = !forced && !plan.use_mfma && mfmaFloatSupported(probe);
-    plan.materialized = forced || (!plan.use_mfma && !plan.use_mfma_float && !valuSupported(probe));
+    plan.use_mfma_binary = !forced && mfmaBinarySupported(probe);
+    plan.materialized = forced || (!plan.use_mfma && !plan.use_mfma_float && !plan.use_mfma_binary &&
+                                   !valuSupported(probe));
     if (plan.per_vector && plan.materialized && dim % 16 != 0) {
         return fail(ZCGVS_ERR_INVALID_ARGUMENT,
                     "zcgvs: per-vector int8 mode needs dim % 16 == 0 and a 16-byte aligned corpus");
@@ -306,20 +309,24 @@ Plan makePlan(const zcgvs_search_desc& d) {
     } else if (plan.use_mfma_float) {
         plan.block_rows = mfmaFloatBlockRows(probe);
         plan.workgroups = mfmaWorkgroups();
+    } else if (plan.use_mfma_binary) {
+        plan.block_rows = mfmaBinaryBlockRows(probe);
+        plan.workgroups = mfmaWorkgroups();
     } else {
         const ValuShape shape = valuShape(probe);
         plan.block_rows = shape.block_rows;
         plan.workgroups = shape.workgroups;
     }
 
-    // Phase schedule: phase 0 samples ~max(16 * width, 4096) rows densely; each later phase
+    // Phase schedule: phase 0 samples ~max(8 * width, 4096) rows densely (for wide selections
+    // that keeps its keys within the merge's LDS capacity); each later phase
     // visits up to growth_cap times as many blocks as all phases before it.
     long long growth_cap = kPhaseGrowth;
     while (growth_cap * 2 * batch * plan.width <= kCandidateBudget) {
         growth_cap *= 2;
     }
     const long long blocks = (n + plan.block_rows - 1) / plan.block_rows;
-    const long long target_rows = std::max<long long>(16LL * plan.width, 4096);
+    const long long target_rows = std::max<long long>(8LL * plan.width, 4096);
     const long long blocks0 = (target_rows + plan.block_rows - 1) / plan.block_rows;
     long long stride = 1;
     while ((blocks + 2 * stride - 1) / (2 * stride) >= blocks0) {
@@ -574,7 +581,8 @@ int searchTopk(const zcgvs_search_desc* desc, void* d_workspace, std::size_t wor
         ZCGVS_LAUNCH_CHECK("merge mask");
     }
     const ScanArgs scan = scanArgsOf(d, plan, ws);
-    if ((plan.use_mfma && !mfmaSupported(scan)) || (plan.use_mfma_float && !mfmaFloatSupported(scan))) {
+    if ((plan.use_mfma && !mfmaSupported(scan)) || (plan.use_mfma_float && !mfmaFloatSupported(scan)) ||
+        (plan.use_mfma_binary && !mfmaBinarySupported(scan))) {
         return setError(ZCGVS_ERR_INVALID_ARGUMENT, "zcgvs: corpus or queries are not 16-byte aligned");
     }
     EmitArgs emit;
@@ -601,6 +609,8 @@ int searchTopk(const zcgvs_search_desc* desc, void* d_workspace, std::size_t wor
             status = launchMfmaScan(scan, phase, emit, plan.workgroups, s);
         } else if (plan.use_mfma_float) {
             status = launchMfmaFloatScan(scan, phase, emit, plan.workgroups, s);
+        } else if (plan.use_mfma_binary) {
+            status = launchMfmaBinaryScan(scan, phase, emit, plan.workgroups, s);
         } else {
             status = launchValuScan(scan, phase, emit, plan.workgroups, s);
         }

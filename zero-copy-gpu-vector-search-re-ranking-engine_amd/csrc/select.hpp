@@ -14,6 +14,7 @@ namespace zcgvs_hip {
 constexpr int kSelectBins = 2048;
 constexpr int kSelectPasses = 6;
 constexpr int kSelectThreads = 256;
+constexpr int kMergeThreads = 1024;  // block size of the fused search's per-query merge
 constexpr int kMaxK = 1024;
 
 __host__ __device__ constexpr int selectDigitWidth(int pass) {
@@ -40,9 +41,10 @@ __device__ __forceinline__ std::uint64_t selectThreshold(const SelectState& s) {
 }
 
 // Inclusive sum of `value` over the block's threads in thread order (threads 0..t), for a block
-// of kSelectThreads threads: a shuffle scan inside each wavefront, then the wavefront totals
-// through LDS (`wave_sums`, kSelectThreads / kWave words). `total` receives the block's sum.
-// Two barriers; every thread must call it.
+// of kThreads threads: a shuffle scan inside each wavefront, then the wavefront totals through
+// LDS (`wave_sums`, kThreads / kWave words). `total` receives the block's sum. Two barriers;
+// every thread must call it.
+template <int kThreads = kSelectThreads>
 __device__ inline std::uint32_t blockInclusiveSum(std::uint32_t value, std::uint32_t* wave_sums,
                                                   std::uint32_t* total) {
     const int lane = threadIdx.x & (kWave - 1);
@@ -61,7 +63,7 @@ __device__ inline std::uint32_t blockInclusiveSum(std::uint32_t value, std::uint
     std::uint32_t before = 0u;
     std::uint32_t sum = 0u;
 #pragma unroll
-    for (int w = 0; w < kSelectThreads / kWave; ++w) {
+    for (int w = 0; w < kThreads / kWave; ++w) {
         const std::uint32_t v = wave_sums[w];
         before += w < wave ? v : 0u;
         sum += v;
@@ -72,13 +74,14 @@ __device__ inline std::uint32_t blockInclusiveSum(std::uint32_t value, std::uint
 }
 
 // Given a full histogram of the current digit, pick the bucket holding the need-th best key and
-// update the state. Runs on one block of kSelectThreads threads; `scratch` is LDS of
-// kSelectThreads / kWave u32. The histogram may be in LDS or global memory (read with plain
-// loads; the caller makes it visible first).
+// update the state. Runs on one block of kThreads threads (at most 1024); `scratch` is LDS of
+// kThreads / kWave u32. The histogram may be in LDS or global memory (read with plain loads; the
+// caller makes it visible first).
+template <int kThreads = kSelectThreads>
 __device__ inline void selectPickBucket(const std::uint32_t* hist, int width, SelectState* state,
                                         std::uint32_t* scratch) {
     const int bins = 1 << width;
-    const int per_thread = bins / kSelectThreads;  // 8 or 4
+    const int per_thread = bins / kThreads;  // 8 or 4 bins at 256 threads, 2 or 1 at 1024
     const int t = threadIdx.x;
     // Thread t owns the t-th group of bins counted from the top.
     const int top = bins - per_thread * t;  // exclusive upper bin
@@ -88,7 +91,7 @@ __device__ inline void selectPickBucket(const std::uint32_t* hist, int width, Se
     }
     const std::uint32_t need = state->need;
     std::uint32_t total = 0u;
-    const std::uint32_t through = blockInclusiveSum(local, scratch, &total);
+    const std::uint32_t through = blockInclusiveSum<kThreads>(local, scratch, &total);
     const std::uint32_t before = through - local;
     if (before < need && need <= through) {
         std::uint32_t above = before;

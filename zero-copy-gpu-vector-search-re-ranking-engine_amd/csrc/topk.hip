@@ -216,12 +216,12 @@ __device__ __forceinline__ void forEachCandidate(const MergeInputs& in, int q, i
 // segment s goes to offset[s] + j, from the exclusive scan of the segment counts.
 constexpr std::uint32_t kSelectLdsKeys = 12288;
 
-__global__ __launch_bounds__(kSelectThreads) void selectMergeKernel(
+__global__ __launch_bounds__(kMergeThreads) void selectMergeKernel(
     MergeInputs in, int k, int batch, std::uint64_t* __restrict__ out_keys,
     std::uint64_t* __restrict__ threshold, std::uint32_t* __restrict__ overflow,
     int* __restrict__ out_index, float* __restrict__ out_score) {
     __shared__ std::uint32_t lds_hist[kSelectBins];
-    __shared__ std::uint32_t lds_scan[kSelectThreads];
+    __shared__ std::uint32_t lds_scan[kMergeThreads / kWave];
     __shared__ std::uint64_t lds_keys[kMaxK];
     __shared__ std::uint32_t lds_seg[kMaxSegments];     // valid count per segment
     __shared__ std::uint32_t lds_offset[kMaxSegments];  // exclusive scan of lds_seg
@@ -251,14 +251,14 @@ __global__ __launch_bounds__(kSelectThreads) void selectMergeKernel(
     }
     __syncthreads();
     // Exclusive scan of the segment counts: thread t owns a contiguous run of segments.
-    const int per_thread = (in.n_seg + kSelectThreads - 1) / kSelectThreads;
+    const int per_thread = (in.n_seg + kMergeThreads - 1) / kMergeThreads;
     std::uint32_t run = 0u;
     for (int i = 0; i < per_thread; ++i) {
         const int s = t * per_thread + i;
         run += s < in.n_seg ? lds_seg[s] : 0u;
     }
     std::uint32_t seg_total = 0u;
-    std::uint32_t acc = blockInclusiveSum(run, lds_scan, &seg_total) - run;
+    std::uint32_t acc = blockInclusiveSum<kMergeThreads>(run, lds_scan, &seg_total) - run;
     for (int i = 0; i < per_thread; ++i) {
         const int s = t * per_thread + i;
         if (s < in.n_seg) {
@@ -349,7 +349,7 @@ __global__ __launch_bounds__(kSelectThreads) void selectMergeKernel(
             }
         });
         __syncthreads();
-        selectPickBucket(lds_hist, width, &lds_state, lds_scan);
+        selectPickBucket<kMergeThreads>(lds_hist, width, &lds_state, lds_scan);
     }
 
     const std::uint64_t cut = n_valid <= static_cast<std::uint32_t>(k) ? 1ull : selectThreshold(lds_state);
@@ -408,7 +408,7 @@ int launchSelectMerge(const MergeInputs& in, int k, int batch, std::uint64_t* ou
     if (in.n_seg > kMaxSegments) {
         return setError(ZCGVS_ERR_RUNTIME, "zcgvs select: too many candidate segments");
     }
-    selectMergeKernel<<<batch, kSelectThreads, 0, stream>>>(in, k, batch, out_keys, threshold,
+    selectMergeKernel<<<batch, kMergeThreads, 0, stream>>>(in, k, batch, out_keys, threshold,
                                                             overflow, out_index, out_score);
     ZCGVS_LAUNCH_CHECK("select merge");
     return ZCGVS_OK;
