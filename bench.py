@@ -52,9 +52,14 @@ WORKLOADS = {
                        name="float16 1M x 384, batch 64, k=10"),
     "binary-50m": dict(kind="binary", n=50_000_000, dim=1024, batch=32, k=10, candidates=1000,
                        name="binary 50M x 1024 + float16 rescore of 1000, batch 32, k=10"),
+    "hybrid-1m": dict(kind="hybrid", n=1_000_000, dim=384, batch=16, k=10, vocab=30_000, terms=8,
+                      dense_weight=0.5,
+                      name="hybrid BM25 (V=30,000, 8-term queries) + float16 1M x 384 cosine, batch 16, k=10"),
     "cpu-ref": dict(kind="f32", n=5183, dim=384, batch=1, k=10,
                     name="float32 5,183 x 384, batch 1, k=10"),
 }
+LEXICAL_SEED = 7
+TERMS_SEED = 11
 
 
 def log(*args):
@@ -74,7 +79,7 @@ def build_inputs(capi, w):
         keep["scales"] = scales
     elif kind == "f32":
         corpus = capi.DeviceArray((n, dim), np.float32)
-    elif kind == "f16":
+    elif kind in ("f16", "hybrid"):
         corpus = capi.DeviceArray((n, dim), np.float16)
     else:
         corpus = capi.DeviceArray((n, (dim + 31) // 32), np.uint32)
@@ -87,7 +92,7 @@ def build_inputs(capi, w):
             capi.launch_quantize_rows_i8(stage, rows, dim, corpus.ptr + start * dim, scales.ptr + start * 4)
         elif kind == "f32":
             capi.call("zcgvs_memcpy_d2d", corpus.ptr + start * dim * 4, stage.ptr, rows * dim * 4, None)
-        elif kind == "f16":
+        elif kind in ("f16", "hybrid"):
             capi.launch_convert_f32_to_f16(stage, corpus.ptr + start * dim * 2, rows * dim)
         else:
             words = (dim + 31) // 32
@@ -98,7 +103,7 @@ def build_inputs(capi, w):
     queries = capi.DeviceArray((batch, dim), np.float32)
     capi.generate_normalized(queries, batch, dim, QUERY_SEED, 0)
     capi.synchronize()
-    dtype = {"i8i8": capi.I8, "f32": capi.F32, "f16": capi.F16, "binary": capi.BINARY}[kind]
+    dtype = {"i8i8": capi.I8, "f32": capi.F32, "f16": capi.F16, "hybrid": capi.F16, "binary": capi.BINARY}[kind]
     store = capi.store_desc(corpus, n, dim, dtype, 1.0, keep.get("scales"))
     extra = {}
     if kind == "i8i8":
@@ -106,6 +111,19 @@ def build_inputs(capi, w):
     if kind == "binary":
         extra["rescore"] = capi.store_desc(keep["rescore"], n, dim, capi.F16)
         extra["rescore_candidates"] = w["candidates"]
+    if kind == "hybrid":
+        from zcgvs_amd.zcgvs_tools import lexical
+        log(f"building the synthetic BM25 index ({n:,} documents, vocabulary {w['vocab']:,})")
+        index = lexical.synthetic_index(n, w["vocab"], seed=LEXICAL_SEED)
+        terms = lexical.synthetic_queries(batch, w["terms"], w["vocab"], seed=TERMS_SEED)
+        keep["lexical"] = {name: capi.DeviceArray.from_host(index[name])
+                           for name in ("offsets", "posting_docs", "posting_weights")}
+        keep["terms"] = capi.DeviceArray.from_host(terms)
+        keep["postings"] = int(index["offsets"][-1])
+        extra.update(lex_offsets=keep["lexical"]["offsets"], lex_docs=keep["lexical"]["posting_docs"],
+                     lex_weights=keep["lexical"]["posting_weights"], lex_doc_count=n,
+                     lex_vocab_size=w["vocab"], query_terms=keep["terms"], lexical_stride=w["terms"],
+                     dense_weight=w["dense_weight"])
     desc = capi.search_desc(store, queries, batch, w["k"], capi.COSINE, **extra)
     return desc, corpus, queries, keep
 
@@ -113,6 +131,8 @@ def build_inputs(capi, w):
 def row_bytes(w):
     """Algorithmic HBM bytes per corpus row a scan reads (row + its per-row scale)."""
     dim = w["dim"]
+    if w["kind"] == "hybrid":
+        return dim * 2 + 4 * w["batch"]  # the row and its fused lexical score per query
     return {"i8i8": dim + 4, "f32": dim * 4, "f16": dim * 2, "binary": (dim + 31) // 32 * 4}[w["kind"]]
 
 
@@ -120,7 +140,7 @@ def query_bytes(w):
     """Bytes of the (device-prepared) queries one scan launch reads."""
     dim, batch = w["dim"], w["batch"]
     return {"i8i8": batch * (dim + 4), "f32": batch * dim * 4, "f16": batch * dim * 4,
-            "binary": batch * (dim + 31) // 32 * 4}[w["kind"]]
+            "hybrid": batch * dim * 4, "binary": batch * (dim + 31) // 32 * 4}[w["kind"]]
 
 
 def measured_traffic(workload, kernel):
@@ -296,7 +316,7 @@ def main(argv=None) -> int:
         "higher_is_better": True,
         "scaling": "weak",
         "vs_baseline": None,
-        "dtype": {"i8i8": "int8", "f32": "f32", "f16": "f16", "binary": "u32"}[w["kind"]],
+        "dtype": {"i8i8": "int8", "f32": "f32", "f16": "f16", "hybrid": "f16", "binary": "u32"}[w["kind"]],
         "data": "synthetic (seeded N(0,1) rows, L2-normalized, generated on the device)",
         "config": {"workload": w["name"], "N": w["n"], "dim": w["dim"], "batch": batch, "k": w["k"],
                    "scan_phases": phases},

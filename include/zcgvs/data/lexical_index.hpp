@@ -35,6 +35,8 @@ public:
     float k1() const { return k1_; }
     float b() const { return b_; }
     float averageDocLength() const { return average_doc_length_; }
+    // Every term's postings strictly ascending by document (checked at load).
+    bool postingsSorted() const { return sorted_postings_; }
     std::size_t deviceBytes() const {
         return offsets_.bytes() + posting_docs_.bytes() + posting_weights_.bytes();
     }
@@ -49,6 +51,7 @@ private:
     float k1_ = 1.2f;
     float b_ = 0.75f;
     float average_doc_length_ = 0.0f;
+    bool sorted_postings_ = true;
 };
 
 }  // namespace zcgvs

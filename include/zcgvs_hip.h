@@ -266,8 +266,13 @@ typedef struct zcgvs_search_desc {
 /* zcgvs_search_desc.flags. ZCGVS_SEARCH_MATERIALIZE runs the reference-order pipeline (a
  * [batch, doc_count] score matrix in the workspace, then zcgvs_launch_topk) instead of the fused
  * scan; its workspace is correspondingly larger. It never overflows, so it is the exact
- * recompute for queries zcgvs_search_overflow_flags reports. */
-enum zcgvs_search_flags { ZCGVS_SEARCH_MATERIALIZE = 1 };
+ * recompute for queries zcgvs_search_overflow_flags reports.
+ * By default the BM25 stage reads each query term's postings in document-range slices, which
+ * needs every term's postings in ascending document order, one per document (as the reference's
+ * index builder writes them, python/zcgvs_tools/build_lexical.py:147-163).
+ * ZCGVS_SEARCH_UNSORTED_POSTINGS lifts that requirement: the postings are then scattered term
+ * slot by term slot, in any order. */
+enum zcgvs_search_flags { ZCGVS_SEARCH_MATERIALIZE = 1, ZCGVS_SEARCH_UNSORTED_POSTINGS = 2 };
 
 /* Bytes of device workspace zcgvs_search_topk needs for this descriptor (0 on error). */
 size_t zcgvs_search_workspace_bytes(const zcgvs_search_desc* desc);

@@ -227,6 +227,49 @@ def test_hybrid_bm25_fused(gpu):
     assert_topk_equivalent(idx, val, fused, k, tol)
 
 
+def test_hybrid_sweep_matches_unsorted_scatter(gpu):
+    # The default BM25 stage reads document-range slices of sorted postings; with
+    # SEARCH_UNSORTED_POSTINGS the postings are scattered slot by slot in any order. Both add a
+    # document's weights in slot order, so a shuffled copy of the index gives bit-identical
+    # results. Term lists padded with -1 and an out-of-vocabulary id are skipped by both.
+    capi = gpu
+    n, vocab, dim, batch, k, w = 70_001, 30_000, 384, 12, 10, 0.25
+    offsets, docs, weights, p = zipf_lexical_index(n, vocab, 21)
+    rng = np.random.default_rng(22)
+    terms = np.stack([rng.choice(vocab, size=8, replace=False, p=p) for _ in range(batch)]).astype(np.int32)
+    terms[0, 5:] = -1
+    terms[1, 7] = vocab + 3
+    shuffled_docs, shuffled_weights = docs.copy(), weights.copy()
+    for t in range(0, vocab, 7):
+        lo, hi = offsets[t], offsets[t + 1]
+        order = rng.permutation(hi - lo)
+        shuffled_docs[lo:hi] = docs[lo:hi][order]
+        shuffled_weights[lo:hi] = weights[lo:hi][order]
+    half = oracle.f32_to_f16(normalized(n, dim, 23))
+    queries = normalized(batch, dim, 24)
+    d_half = capi.DeviceArray.from_host(half)
+    results = []
+    for doc_array, weight_array, flags in ((docs, weights, 0),
+                                           (shuffled_docs, shuffled_weights, capi.SEARCH_UNSORTED_POSTINGS)):
+        results.append(run_search(capi, d_half, n, dim, capi.F16, queries, k,
+                                  lex_offsets=capi.DeviceArray.from_host(offsets),
+                                  lex_docs=capi.DeviceArray.from_host(doc_array),
+                                  lex_weights=capi.DeviceArray.from_host(weight_array), lex_doc_count=n,
+                                  lex_vocab_size=vocab, query_terms=capi.DeviceArray.from_host(terms),
+                                  lexical_stride=8, dense_weight=w, flags=flags))
+    assert np.array_equal(results[0][0], results[1][0])
+    assert np.array_equal(results[0][1], results[1][1])
+    decoded = half.astype(np.float32)
+    dense = oracle.scores_f32(decoded, queries, 0)
+    fused = np.empty_like(dense)
+    known = np.where(terms < vocab, terms, -1)  # the search skips ids past the vocabulary
+    for b in range(batch):
+        lex = oracle.bm25(offsets, docs, weights, known[b], n)
+        fused[b] = oracle.fuse(dense[b], lex, oracle.max_positive(lex), w)
+    tol = np.float32(w) * float_tolerance(queries, decoded, 0) + 1e-6
+    assert_topk_equivalent(results[0][0], results[0][1], fused, k, tol)
+
+
 @pytest.mark.parametrize("bad,match", [
     (dict(k=0), "k must be positive"),
     (dict(k=2000), "exceeds kernel capacity"),

@@ -21,6 +21,7 @@ COSINE, DOT, L2 = 0, 1, 2
 F32, F16, I8, BINARY = 0, 1, 2, 3
 INT8_REFERENCE, INT8_PER_VECTOR = 0, 1
 SEARCH_MATERIALIZE = 1
+SEARCH_UNSORTED_POSTINGS = 2
 
 _vp = ctypes.c_void_p
 _i32 = ctypes.c_int

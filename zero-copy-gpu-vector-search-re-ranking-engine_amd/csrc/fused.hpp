@@ -118,8 +118,8 @@ int mfmaWorkgroups();
 int launchMfmaScan(const ScanArgs& scan, const PhaseArgs& phase, const EmitArgs& emit,
                    int workgroups, hipStream_t stream);
 
-// The float32 / float16 MFMA scan (batches of at least 4 queries, cosine or dot, no mask or
-// lexical scores, dim in {128, 256, 384, 512}); block rows depend on the row size.
+// The float32 / float16 MFMA scan (batches of at least 4 queries, cosine or dot, no mask, dim in
+// {128, 256, 384, 512}; lexical scores are fused); block rows depend on the row size.
 bool mfmaFloatSupported(const ScanArgs& scan);
 int mfmaFloatBlockRows(const ScanArgs& scan);
 int launchMfmaFloatScan(const ScanArgs& scan, const PhaseArgs& phase, const EmitArgs& emit,

@@ -28,6 +28,11 @@
 // MFMA) or 4 floats (four f32 MFMAs, component c of every lane group forming the c-th).
 // D: lane l holds query l % 16 and rows 4 * (l / 16) + i, i < 4.
 //
+// Hybrid searches (lexical scores fused into the dense score, fuseHybrid of fused.hpp) take up
+// to 16 queries per launch; each tile's [16, rows] block of lexical scores travels HBM -> LDS
+// with global_load_lds_dword in a ring beside the tile ring, so the epilogue reads LDS only (a
+// plain global load there would make the compiler wait for every copy in flight).
+//
 // Corpus streaming is the one of the int8 MFMA scan (lds_copy.hpp): tiles of whole rows go HBM ->
 // LDS through global_load_lds_dwordx4 into a ring kDepth - 1 tiles ahead; every wavefront waits
 // for its own copies of a tile and meets the others at a bare s_barrier. Tile rows are sized so
@@ -56,6 +61,7 @@ constexpr int kQueriesPerLaunch = kWaves * kGroupQueries;
 constexpr int kTileTarget = 48 * 1024;
 constexpr int kRingBudget = 150 * 1024;
 constexpr int kMinBatch = 4;  // below this the VALU scan is already bound by HBM
+constexpr int kLexQueries = 16;  // queries per launch of a hybrid search
 
 constexpr int pow2Floor(int value) {
     int p = 1;
@@ -79,9 +85,16 @@ struct FloatTile {
     static_assert(kRowBytes % 256 == 0, "rows must be whole multiples of 256 bytes");
     static_assert(kRows * kChunks % kThreads == 0, "tile must split over the lanes");
     static_assert(2 * kCopies < 63, "copies in flight fit the vmcnt counter");
+    // lexical ring of hybrid launches: [kDepth][kLexQueries][kLexStride] floats; each wave
+    // copies the rows of queries w and w + 8, 64 rows per dword copy
+    static constexpr int kLexStride = kRows < kWave ? kWave : kRows;
+    static constexpr int kLexPieces = (kRows + kWave - 1) / kWave;
+    static constexpr int kLexCopies = 2 * kLexPieces;
+    static_assert(kDepth * (kTileBytes + kLexQueries * kLexStride * 4) + 4 * kQueriesPerLaunch <= 160 * 1024,
+                  "tile and lexical rings fit the LDS");
 };
 
-template <int kKind, int kDim, bool kDense>
+template <int kKind, int kDim, bool kDense, bool kLex>
 __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(2, 2)))
 void mfmaFloatScanKernel(ScanArgs scan, PhaseArgs phase, EmitArgs emit, int q_offset, int q_count) {
     using Tile = FloatTile<kKind, kDim>;
@@ -93,9 +106,13 @@ void mfmaFloatScanKernel(ScanArgs scan, PhaseArgs phase, EmitArgs emit, int q_of
     constexpr int kDepth = Tile::kDepth;
     constexpr int kCopies = Tile::kCopies;
     constexpr int kRowBlocks = kRows / 16;
+    constexpr int kLexStride = Tile::kLexStride;
+    constexpr int kLexPieces = Tile::kLexPieces;
+    constexpr int kPerTile = kCopies + (kLex ? Tile::kLexCopies : 0);  // copies per wave per tile
 
     __shared__ __attribute__((aligned(16))) std::uint8_t ring[kDepth][Tile::kTileBytes];
     __shared__ std::uint32_t lds_count[kQueriesPerLaunch];
+    __shared__ float lex_ring[kLex ? kDepth : 1][kLex ? kLexQueries : 1][kLex ? kLexStride : 1];
 
     const int tid = threadIdx.x;
     const int lane = tid & (kWave - 1);
@@ -166,6 +183,11 @@ void mfmaFloatScanKernel(ScanArgs scan, PhaseArgs phase, EmitArgs emit, int q_of
     if constexpr (!kDense) {
         tau = emit.tau[q];
     }
+    float inverse = 0.0f;  // 1 / (the query's largest lexical score), 0 when none is positive
+    if constexpr (kLex) {
+        const float peak = scan.lexical_max[q];
+        inverse = peak > 0.0f ? 1.0f / peak : 0.0f;
+    }
     for (int i = tid; i < kQueriesPerLaunch; i += kThreads) {
         lds_count[i] = 0u;
     }
@@ -199,6 +221,21 @@ void mfmaFloatScanKernel(ScanArgs scan, PhaseArgs phase, EmitArgs emit, int q_of
                 copyToLds(base, off, __builtin_amdgcn_readfirstlane(slot_base + (wave * kCopies + i) * kWave * 16));
             }
         }
+        if constexpr (kLex) {
+            // rows row0 + 64 p + lane of queries wave and wave + 8 (rows past the corpus re-read
+            // its last row; a missing query re-reads query 0's scores; neither is ever used)
+#pragma unroll
+            for (int j = 0; j < 2; ++j) {
+                const int ql = wave + 8 * j;
+                const long long qg = q_offset + (ql < q_count ? ql : 0);
+#pragma unroll
+                for (int p = 0; p < kLexPieces; ++p) {
+                    const long long row = min(row0 + kWave * p + lane, doc_count - 1);
+                    copyDwordToLds(scan.lexical + qg * doc_count + row,
+                                   __builtin_amdgcn_readfirstlane(ldsAddress(&lex_ring[slot][ql][kWave * p])));
+                }
+            }
+        }
     };
 
     const long long stride_items = gridDim.x;
@@ -217,7 +254,7 @@ void mfmaFloatScanKernel(ScanArgs scan, PhaseArgs phase, EmitArgs emit, int q_of
         for (int d = 1; d <= kDepth - 2; ++d) {
             later += it + d * stride_items < phase.items ? 1 : 0;
         }
-        waitTiles<kCopies, kDepth - 2>(later);
+        waitTiles<kPerTile, kDepth - 2>(later);
         __builtin_amdgcn_s_barrier();
         asm volatile("" ::: "memory");  // no LDS access moves above the barrier
     };
@@ -297,8 +334,12 @@ void mfmaFloatScanKernel(ScanArgs scan, PhaseArgs phase, EmitArgs emit, int q_of
                     for (int i = 0; i < 4; ++i) {
                         const int local = block * 16 + 4 * h + i;
                         const long long row = row0 + local;
+                        float value = score[i];
+                        if constexpr (kLex) {
+                            value = fuseHybrid(value, lex_ring[slot][qlocal][local], scan.dense_weight, inverse);
+                        }
                         const std::uint64_t key =
-                            row < doc_count ? makeKey(score[i], static_cast<std::uint32_t>(row)) : 0ull;
+                            row < doc_count ? makeKey(value, static_cast<std::uint32_t>(row)) : 0ull;
                         if constexpr (kDense) {
                             emit.dense[static_cast<std::size_t>(q) * emit.dense_stride + item * kRows + local] = key;
                         } else if (key > tau) {
@@ -318,21 +359,29 @@ void mfmaFloatScanKernel(ScanArgs scan, PhaseArgs phase, EmitArgs emit, int q_of
     }
 }
 
+template <int kKind, int kDim, bool kLex>
+int launchQueries(const ScanArgs& scan, const PhaseArgs& phase, const EmitArgs& emit, dim3 grid,
+                  hipStream_t stream) {
+    const int per_launch = kLex ? kLexQueries : kQueriesPerLaunch;
+    for (int q0 = 0; q0 < scan.batch; q0 += per_launch) {
+        const int count = std::min(per_launch, scan.batch - q0);
+        if (phase.dense) {
+            mfmaFloatScanKernel<kKind, kDim, true, kLex><<<grid, kThreads, 0, stream>>>(scan, phase, emit, q0, count);
+        } else {
+            mfmaFloatScanKernel<kKind, kDim, false, kLex><<<grid, kThreads, 0, stream>>>(scan, phase, emit, q0, count);
+        }
+        ZCGVS_LAUNCH_CHECK("float mfma scan");
+    }
+    return ZCGVS_OK;
+}
+
 template <int kKind, int kDim>
 int launchShape(const ScanArgs& scan, const PhaseArgs& phase, const EmitArgs& emit, int workgroups,
                 hipStream_t stream) {
     const long long wanted = phase.dense ? std::min<long long>(phase.items, workgroups) : workgroups;
     const dim3 grid(static_cast<unsigned>(std::max(1LL, wanted)));
-    for (int q0 = 0; q0 < scan.batch; q0 += kQueriesPerLaunch) {
-        const int count = std::min(kQueriesPerLaunch, scan.batch - q0);
-        if (phase.dense) {
-            mfmaFloatScanKernel<kKind, kDim, true><<<grid, kThreads, 0, stream>>>(scan, phase, emit, q0, count);
-        } else {
-            mfmaFloatScanKernel<kKind, kDim, false><<<grid, kThreads, 0, stream>>>(scan, phase, emit, q0, count);
-        }
-        ZCGVS_LAUNCH_CHECK("float mfma scan");
-    }
-    return ZCGVS_OK;
+    return scan.lexical != nullptr ? launchQueries<kKind, kDim, true>(scan, phase, emit, grid, stream)
+                                   : launchQueries<kKind, kDim, false>(scan, phase, emit, grid, stream);
 }
 
 // Calls f(FloatTile<kind, dim>-shaped tag) for the supported (kind, dim) pairs; false otherwise.
@@ -378,7 +427,7 @@ bool mfmaFloatSupported(const ScanArgs& scan) {
     if (scan.metric != ZCGVS_METRIC_COSINE && scan.metric != ZCGVS_METRIC_DOT) {
         return false;
     }
-    if (scan.mask != nullptr || scan.lexical != nullptr || scan.batch < kMinBatch) {
+    if (scan.mask != nullptr || scan.batch < kMinBatch) {
         return false;
     }
     if (!aligned16(scan.corpus) || !aligned16(scan.queries)) {

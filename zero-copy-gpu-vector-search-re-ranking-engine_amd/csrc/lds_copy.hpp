@@ -43,6 +43,15 @@ __device__ __forceinline__ void copyToLds(const void* uniform_base, std::uint32_
                  : "memory");
 }
 
+// One global_load_lds_dword: every active lane copies 4 bytes from `src` to LDS at
+// lds_base + 4 * lane (same ordering rules as copyToLds).
+__device__ __forceinline__ void copyDwordToLds(const void* src, std::uint32_t lds_base) {
+    asm volatile("s_nop 0\n\tglobal_load_lds_dword %0, off"
+                 :
+                 : "v"(src), "{m0}"(lds_base)
+                 : "memory");
+}
+
 // s_waitcnt that waits until at most n vector-memory operations of this wavefront are pending
 // (expcnt and lgkmcnt fields at their "no wait" maxima).
 __device__ constexpr int vmcntOnly(int n) {

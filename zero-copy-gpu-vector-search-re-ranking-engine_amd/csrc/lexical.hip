@@ -8,6 +8,14 @@
 // postings of one term touch distinct documents (the index builder emits one posting per
 // (term, document)), so every document's sum is ((w_0 + w_1) + w_2) ... in slot order, the order
 // of the CPU loop in tests/cpp/test_lexical.cu:71-80, on every run.
+//
+// The fused search's default needs no atomics in global memory and no separate clearing or
+// maximum pass. With every term's postings ascending by document, bm25BoundsKernel finds where
+// each query term's postings cross every 1024-document boundary (one binary search per thread,
+// all at once), and bm25SweepKernel, one workgroup per (query, slice), loads its slice of every
+// term's postings, adds them into an LDS accumulator slot by slot in slot order (the same
+// per-document order), then writes the slice, zeros included, and folds its maximum into the
+// query's.
 #include <hip/hip_runtime.h>
 
 #include <algorithm>
@@ -21,6 +29,10 @@ namespace {
 
 constexpr int kPostingThreads = 256;
 constexpr int kReduceThreads = 256;
+constexpr int kSweepThreads = 256;
+constexpr int kSweepDocs = 1024;              // documents per sweep workgroup
+constexpr int kSweepPerThread = kSweepDocs / kSweepThreads;  // postings per thread per slot
+constexpr int kSweepSlotGroup = 8;            // slots whose postings are loaded together
 
 // Postings of term slot `slot` for each query (blockIdx.y) of the batch.
 __global__ __launch_bounds__(kPostingThreads) void bm25SlotKernel(
@@ -41,6 +53,156 @@ __global__ __launch_bounds__(kPostingThreads) void bm25SlotKernel(
         if (doc >= 0 && doc < doc_count) {
             atomicAdd(&row[doc], weights[p]);
         }
+    }
+}
+
+// Raises *target (a non-negative float, ordered as its bits) to at least `value`. Thousands of
+// workgroups fold into one address per query, and atomics on one address serialize, so the
+// current value is read first and the atomic is issued only when it would raise it (a stale
+// read only costs an unneeded atomic).
+__device__ __forceinline__ void raiseMax(float* target, float value) {
+    unsigned int* bits = reinterpret_cast<unsigned int*>(target);
+    const unsigned int mine = __float_as_uint(value);
+    if (__atomic_load_n(bits, __ATOMIC_RELAXED) < mine) {
+        atomicMax(bits, mine);
+    }
+}
+
+// First position in docs[lo, hi) whose document is >= target (hi if none).
+__device__ __forceinline__ std::int64_t lowerBound(const int* __restrict__ docs, std::int64_t lo,
+                                                   std::int64_t hi, int target) {
+    while (lo < hi) {
+        const std::int64_t mid = lo + ((hi - lo) >> 1);
+        if (docs[mid] < target) {
+            lo = mid + 1;
+        } else {
+            hi = mid;
+        }
+    }
+    return lo;
+}
+
+// bounds[(q * term_stride + slot) * (slices + 1) + c] = first posting of the term in slot `slot`
+// of query q whose document is >= c * kSweepDocs (c = slices: >= doc_count); an unknown term
+// gets 0 everywhere (an empty range). One thread per entry, so all searches run at once.
+__global__ void bm25BoundsKernel(const std::int64_t* __restrict__ offsets, const int* __restrict__ docs,
+                                 const int* __restrict__ query_terms, int term_stride, int batch,
+                                 int doc_count, int vocab_size, int slices,
+                                 std::int64_t* __restrict__ bounds) {
+    const long long total = static_cast<long long>(batch) * term_stride * (slices + 1);
+    const long long i = static_cast<long long>(blockIdx.x) * blockDim.x + threadIdx.x;
+    if (i >= total) {
+        return;
+    }
+    const int c = static_cast<int>(i % (slices + 1));
+    const long long qs = i / (slices + 1);  // q * term_stride + slot
+    const int term = query_terms[qs];
+    std::int64_t position = 0;
+    if (term >= 0 && term < vocab_size) {
+        position = lowerBound(docs, offsets[term], offsets[term + 1],
+                              c == slices ? doc_count : c * kSweepDocs);
+    }
+    bounds[i] = position;
+}
+
+// BM25 scores of documents [blockIdx.x * kSweepDocs, + kSweepDocs) for query blockIdx.y from the
+// postings between the slice bounds; writes every score of the slice and raises lexical_max[q]
+// (zeroed beforehand) to the slice's max(0, max score). A slot's postings inside one slice are
+// distinct documents, so there are at most kSweepDocs of them: each thread loads up to
+// kSweepPerThread per slot, for kSweepSlotGroup slots at a time, before any is added, and the
+// additions of one slot touch distinct accumulator entries.
+__global__ __launch_bounds__(kSweepThreads) void bm25SweepKernel(
+    const int* __restrict__ docs, const float* __restrict__ weights, const std::int64_t* __restrict__ bounds,
+    int term_stride, int doc_count, int slices, float* __restrict__ scores, float* __restrict__ lexical_max) {
+    __shared__ float acc[kSweepDocs];
+    __shared__ float partial[kSweepThreads / kWave];
+    const int q = blockIdx.y;
+    const int c = blockIdx.x;
+    const int t = threadIdx.x;
+    const int d0 = c * kSweepDocs;
+    const int d1 = min(d0 + kSweepDocs, doc_count);
+    for (int i = t; i < kSweepDocs; i += kSweepThreads) {
+        acc[i] = 0.0f;
+    }
+    __syncthreads();
+    const std::int64_t* qb = bounds + static_cast<std::size_t>(q) * term_stride * (slices + 1);
+    for (int g0 = 0; g0 < term_stride; g0 += kSweepSlotGroup) {
+        int doc[kSweepSlotGroup][kSweepPerThread];
+        float weight[kSweepSlotGroup][kSweepPerThread];
+        std::int64_t begin[kSweepSlotGroup];
+        std::int64_t end[kSweepSlotGroup];
+        // Every load of the group is issued before any loaded value is used: positions past a
+        // slot's range read its last posting (the range is uniform; an empty one loads nothing)
+        // and validity is decided later from the positions alone.
+#pragma unroll
+        for (int g = 0; g < kSweepSlotGroup; ++g) {  // all bounds first: one wait for all of them
+            const int slot = g0 + g;
+            begin[g] = 0;
+            end[g] = 0;
+            if (slot < term_stride) {
+                begin[g] = qb[static_cast<std::size_t>(slot) * (slices + 1) + c];
+                end[g] = qb[static_cast<std::size_t>(slot) * (slices + 1) + c + 1];
+            }
+        }
+#pragma unroll
+        for (int g = 0; g < kSweepSlotGroup; ++g) {
+            if (end[g] > begin[g]) {
+#pragma unroll
+                for (int j = 0; j < kSweepPerThread; ++j) {
+                    const std::int64_t p = begin[g] + t + j * kSweepThreads;
+                    const std::int64_t safe = p < end[g] ? p : end[g] - 1;
+                    doc[g][j] = docs[safe];
+                    weight[g][j] = weights[safe];
+                }
+            }
+        }
+#pragma unroll
+        for (int g = 0; g < kSweepSlotGroup; ++g) {
+            if (g0 + g < term_stride) {
+                if (end[g] > begin[g]) {
+#pragma unroll
+                    for (int j = 0; j < kSweepPerThread; ++j) {
+                        const std::int64_t p = begin[g] + t + j * kSweepThreads;
+                        // distinct documents within a slot: plain adds do not race (and an
+                        // LDS float atomic is several times slower here)
+                        if (p < end[g] && doc[g][j] >= d0 && doc[g][j] < d1) {
+                            acc[doc[g][j] - d0] += weight[g][j];
+                        }
+                    }
+                    // More than kSweepDocs postings in one slice can only come from repeated
+                    // documents (outside the sorted-index contract); they are still all added.
+                    for (std::int64_t p = begin[g] + kSweepDocs + t; p < end[g]; p += kSweepThreads) {
+                        const int extra = docs[p];
+                        if (extra >= d0 && extra < d1) {
+                            atomicAdd(&acc[extra - d0], weights[p]);
+                        }
+                    }
+                }
+                __syncthreads();  // slot g's additions land before slot g + 1's
+            }
+        }
+    }
+    float best = 0.0f;
+    float* row = scores + static_cast<std::size_t>(q) * doc_count + d0;
+    for (int i = t; i < d1 - d0; i += kSweepThreads) {
+        const float value = acc[i];
+        row[i] = value;
+        best = fmaxf(best, value);
+    }
+#pragma unroll
+    for (int offset = kWave / 2; offset > 0; offset >>= 1) {
+        best = fmaxf(best, waveXor(best, offset));
+    }
+    if ((t & (kWave - 1)) == 0) {
+        partial[t / kWave] = best;
+    }
+    __syncthreads();
+    if (t == 0) {
+        float block_best = 0.0f;
+        for (int w = 0; w < kSweepThreads / kWave; ++w) {
+            block_best = fmaxf(block_best, partial[w]);
+        }
+        raiseMax(lexical_max + q, block_best);
     }
 }
 
@@ -68,7 +230,7 @@ __global__ __launch_bounds__(kReduceThreads) void maxPositiveKernel(
         for (int w = 0; w < kReduceThreads / kWave; ++w) {
             block_best = fmaxf(block_best, partial[w]);
         }
-        atomicMax(reinterpret_cast<unsigned int*>(out_max + q), __float_as_uint(block_best));
+        raiseMax(out_max + q, block_best);
     }
 }
 
@@ -106,12 +268,31 @@ unsigned postingBlocks() { return static_cast<unsigned>(std::max(1, deviceComput
 
 }  // namespace
 
+std::size_t lexicalBoundsBytes(int batch, int term_stride, int doc_count) {
+    const long long slices = (static_cast<long long>(doc_count) + kSweepDocs - 1) / kSweepDocs;
+    return static_cast<std::size_t>(batch) * static_cast<std::size_t>(term_stride) *
+           static_cast<std::size_t>(slices + 1) * sizeof(std::int64_t);
+}
+
 int launchLexicalScores(const std::int64_t* offsets, const int* docs, const float* weights,
                         int vocab_size, const int* query_terms, int term_stride, int batch,
-                        int doc_count, float* lexical, float* lexical_max, hipStream_t stream) {
+                        int doc_count, float* lexical, float* lexical_max, std::int64_t* bounds,
+                        hipStream_t stream) {
+    zeroKernel<<<1, 256, 0, stream>>>(lexical_max, static_cast<std::size_t>(batch));
+    ZCGVS_LAUNCH_CHECK("lexical zero");
+    if (bounds != nullptr) {
+        const int slices = (doc_count + kSweepDocs - 1) / kSweepDocs;
+        const long long entries = static_cast<long long>(batch) * term_stride * (slices + 1);
+        bm25BoundsKernel<<<static_cast<unsigned>((entries + 255) / 256), 256, 0, stream>>>(
+            offsets, docs, query_terms, term_stride, batch, doc_count, vocab_size, slices, bounds);
+        ZCGVS_LAUNCH_CHECK("bm25 bounds");
+        bm25SweepKernel<<<dim3(static_cast<unsigned>(slices), static_cast<unsigned>(batch)), kSweepThreads, 0,
+                          stream>>>(docs, weights, bounds, term_stride, doc_count, slices, lexical, lexical_max);
+        ZCGVS_LAUNCH_CHECK("bm25 sweep");
+        return ZCGVS_OK;
+    }
     const std::size_t elements = static_cast<std::size_t>(batch) * doc_count;
     zeroKernel<<<std::min<std::size_t>(8192, (elements + 255) / 256), 256, 0, stream>>>(lexical, elements);
-    zeroKernel<<<1, 256, 0, stream>>>(lexical_max, static_cast<std::size_t>(batch));
     ZCGVS_LAUNCH_CHECK("lexical zero");
     const dim3 grid(postingBlocks(), static_cast<unsigned>(batch));
     for (int slot = 0; slot < term_stride; ++slot) {

@@ -14,10 +14,15 @@ int launchRescoreKeys(const void* corpus, int dtype, float scale, int doc_count,
                       hipStream_t stream);
 
 // BM25 over the CSR index for [batch, term_stride] term slots into lexical [batch, doc_count]
-// (zeroed first by this call), then the per-query maximum into lexical_max [batch].
+// (every entry written), and the per-query maximum max(0, max_i lexical) into lexical_max
+// [batch]. With `bounds` (lexicalBoundsBytes of scratch; each term's postings ascending by
+// document, one per document) the postings are read in document-range slices; with null they
+// are scattered slot by slot, in any order.
+std::size_t lexicalBoundsBytes(int batch, int term_stride, int doc_count);
 int launchLexicalScores(const std::int64_t* offsets, const int* docs, const float* weights,
                         int vocab_size, const int* query_terms, int term_stride, int batch,
-                        int doc_count, float* lexical, float* lexical_max, hipStream_t stream);
+                        int doc_count, float* lexical, float* lexical_max, std::int64_t* bounds,
+                        hipStream_t stream);
 
 // Per-row int8 quantization used for the queries of the per-vector int8 mode.
 int launchQuantizeRows(const float* src, int rows, int dim, std::int8_t* dst, float* scales,

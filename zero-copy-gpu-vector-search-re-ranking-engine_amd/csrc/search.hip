@@ -69,6 +69,7 @@ struct Plan {
     bool use_mfma_float = false;
     bool use_mfma_binary = false;
     bool direct_scales = false;  // MFMA path without a mask: only the tail tile's scales are copied
+    bool lex_sorted = false;     // hybrid with postings ascending by document: sliced BM25 stage
     int width = 0;  // keys selected by the scan stage
     int block_rows = 64;
     int workgroups = 1;
@@ -81,7 +82,7 @@ struct Plan {
     std::size_t qbits = 0, qi8 = 0, qscale = 0, lex = 0, lexmax = 0, dense = 0, seg = 0,
                 segcnt = 0, keys = 0, tau = 0, overflow = 0, rescored = 0, scores = 0, lexmat = 0,
                 topk_a = 0, topk_b = 0, topk_c = 0, topk_d = 0, cand_idx = 0, cand_val = 0,
-                local_idx = 0, rescore_val = 0, lexmax_m = 0;
+                local_idx = 0, rescore_val = 0, lexmax_m = 0, lexbounds = 0;
     std::size_t total = 0;
 };
 
@@ -271,6 +272,10 @@ Plan makePlan(const zcgvs_search_desc& d) {
         }
     }
     plan.overflow = layout.add(static_cast<std::size_t>(batch) * 4);
+    if (plan.hybrid && (d.flags & ZCGVS_SEARCH_UNSORTED_POSTINGS) == 0) {
+        plan.lex_sorted = true;
+        plan.lexbounds = layout.add(lexicalBoundsBytes(batch, d.lexical_stride, static_cast<int>(n)));
+    }
 
     if (plan.materialized) {
         // Reference-order pipeline over a workspace score matrix.
@@ -407,7 +412,9 @@ int runMaterialized(const zcgvs_search_desc& d, const Plan& plan, std::uint8_t* 
         float* lexical = at<float>(ws, plan.lexmat);
         float* lexmax = at<float>(ws, plan.lexmax_m);
         status = launchLexicalScores(d.lex_offsets, d.lex_docs, d.lex_weights, d.lex_vocab_size, d.query_terms,
-                                     d.lexical_stride, batch, n, lexical, lexmax, stream);
+                                     d.lexical_stride, batch, n, lexical, lexmax,
+                                     plan.lex_sorted ? at<std::int64_t>(ws, plan.lexbounds) : nullptr,
+                                     stream);
         if (status != ZCGVS_OK) {
             return status;
         }
@@ -560,7 +567,8 @@ int searchTopk(const zcgvs_search_desc* desc, void* d_workspace, std::size_t wor
     if (plan.hybrid) {
         status = launchLexicalScores(d.lex_offsets, d.lex_docs, d.lex_weights, d.lex_vocab_size, d.query_terms,
                                      d.lexical_stride, batch, static_cast<int>(d.corpus.doc_count),
-                                     at<float>(ws, plan.lex), at<float>(ws, plan.lexmax), s);
+                                     at<float>(ws, plan.lex), at<float>(ws, plan.lexmax),
+                                     plan.lex_sorted ? at<std::int64_t>(ws, plan.lexbounds) : nullptr, s);
         if (status != ZCGVS_OK) {
             return status;
         }

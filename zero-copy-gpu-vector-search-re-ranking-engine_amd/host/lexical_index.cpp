@@ -13,7 +13,9 @@ namespace zcgvs {
 namespace {
 
 // Offsets start at 0, never decrease and end at nnz; every posting names a document in range.
-void validateCsr(const std::int64_t* offsets, const int* docs, int vocab_size, std::int64_t nnz,
+// Returns whether every term's postings are strictly ascending by document (the layout the
+// reference's builder writes, which the device BM25 stage reads in document-range slices).
+bool validateCsr(const std::int64_t* offsets, const int* docs, int vocab_size, std::int64_t nnz,
                  std::int64_t doc_count) {
     if (offsets[0] != 0 || offsets[vocab_size] != nnz) {
         throw std::runtime_error("zcgvs: lexical index CSR offsets are inconsistent with nnz");
@@ -28,6 +30,16 @@ void validateCsr(const std::int64_t* offsets, const int* docs, int vocab_size, s
             throw std::runtime_error("zcgvs: lexical index posting names a document out of range");
         }
     }
+    bool sorted = true;
+    for (int t = 0; t < vocab_size && sorted; ++t) {
+        for (std::int64_t i = offsets[t] + 1; i < offsets[t + 1]; ++i) {
+            if (docs[i] <= docs[i - 1]) {
+                sorted = false;
+                break;
+            }
+        }
+    }
+    return sorted;
 }
 
 void upload(const void* host, void* device, std::size_t bytes) {
@@ -48,8 +60,9 @@ LexicalIndex LexicalIndex::fromHostCsr(const std::int64_t* offsets, const int* d
     if (nnz < 0 || (nnz > 0 && (docs == nullptr || weights == nullptr))) {
         throw std::invalid_argument("zcgvs: lexical index postings are missing");
     }
-    validateCsr(offsets, docs, vocab_size, nnz, doc_count);
+    const bool sorted = validateCsr(offsets, docs, vocab_size, nnz, doc_count);
     LexicalIndex index;
+    index.sorted_postings_ = sorted;
     index.doc_count_ = doc_count;
     index.vocab_size_ = vocab_size;
     index.posting_count_ = nnz;

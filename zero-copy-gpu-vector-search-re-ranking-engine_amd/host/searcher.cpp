@@ -162,6 +162,9 @@ zcgvs_search_desc Searcher::describe(const float* queries, int batch, const Sear
         desc.lex_weights = lexical_index_->devicePostingWeights();
         desc.lex_doc_count = lexical_index_->docCount();
         desc.lex_vocab_size = lexical_index_->vocabSize();
+        if (!lexical_index_->postingsSorted()) {
+            desc.flags |= ZCGVS_SEARCH_UNSORTED_POSTINGS;
+        }
         desc.query_terms = d_query_terms_.data();
         desc.lexical_stride = params.lexical_stride;
         desc.dense_weight = params.dense_weight;
@@ -290,7 +293,7 @@ void Searcher::recomputeExact(int query, const HipStream& stream) {
     if (desc.query_terms != nullptr) {
         desc.query_terms += static_cast<std::size_t>(query) * static_cast<std::size_t>(desc.lexical_stride);
     }
-    desc.flags = ZCGVS_SEARCH_MATERIALIZE;
+    desc.flags |= ZCGVS_SEARCH_MATERIALIZE;
     grow(d_exact_workspace_, workspaceBytes(desc));
     const std::size_t row = static_cast<std::size_t>(query) * static_cast<std::size_t>(current_k_);
     check(zcgvs_search_topk(&desc, d_exact_workspace_.data(), d_exact_workspace_.size(), d_out_indices_.data() + row,
