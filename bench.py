@@ -158,8 +158,10 @@ def measured_traffic(workload, kernel):
 def scan_kernel_name(w):
     if w["kind"] == "i8i8":
         return f"mfmaScanKernel<{w['dim'] // 32}, false>"
-    if w["kind"] in ("f32", "f16") and w["batch"] >= 4 and w["dim"] in (128, 256, 384, 512):
-        return f"mfmaFloatScanKernel<{0 if w['kind'] == 'f32' else 1}, {w['dim']}, false>"
+    if w["kind"] in ("f32", "f16", "hybrid") and w["batch"] >= 4 and w["dim"] in (128, 256, 384, 512):
+        kind = 0 if w["kind"] == "f32" else 1
+        lexical = "true" if w["kind"] == "hybrid" else "false"
+        return f"mfmaFloatScanKernel<{kind}, {w['dim']}, false, {lexical}>"
     if w["kind"] == "binary" and w["batch"] >= 4 and w["dim"] in (512, 1024):
         return f"mfmaBinaryScanKernel<{w['dim'] // 32}, false>"
     return "valuScanKernel"
