@@ -115,6 +115,8 @@ int launchValuScan(const ScanArgs& scan, const PhaseArgs& phase, const EmitArgs&
 bool mfmaSupported(const ScanArgs& scan);
 constexpr int kMfmaBlockRows = 64;
 int mfmaWorkgroups();
+// Candidate segments per workgroup of the int8 MFMA scan (one per row half of a query's lanes).
+int mfmaSegmentsPerWorkgroup();
 int launchMfmaScan(const ScanArgs& scan, const PhaseArgs& phase, const EmitArgs& emit,
                    int workgroups, hipStream_t stream);
 

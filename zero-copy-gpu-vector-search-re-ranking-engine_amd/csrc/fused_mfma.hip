@@ -12,14 +12,18 @@
 // and one lags: after the tile barrier the leader multiplies tile t and then filters it, while
 // the lagger first filters tile t - 1 and then multiplies tile t. So each wavefront's VALU filter
 // work runs while the other keeps the SIMD's matrix core busy. A filter that passes owes an exact
-// pass; that pass runs right after the next barrier, before that step's tile copies are issued,
-// so candidate stores never sit behind later tile copies in the vmcnt order.
+// pass; that pass runs right after the next barrier, before that step's tile copies are issued
+// (its keys go to an LDS staging buffer, so in the loop global stores, which would queue behind
+// the copies in the vmcnt order, happen only when that buffer is full).
 //
-// Candidate staging. A key the exact pass accepts gets its segment slot from the per-query LDS
-// counter and is parked in a per-wavefront LDS buffer; the buffers are written to the segments
-// after the scan loop. A global store inside the loop would enter the same in-order vmcnt queue
-// as the tile copies, and the next tile wait would have to wait for the store's completion too;
-// only a wavefront whose buffer is full stores directly.
+// Candidate staging. A query's candidates in a workgroup come from exactly two lanes (its two
+// row halves), so each lane owns a candidate segment (segment 2 * workgroup + half) and counts
+// its slots in a register: no LDS atomic, and no wait for one's return, on the emission path. A
+// key the exact pass accepts is parked in a per-wavefront LDS buffer at a position handed out by
+// a wave-wide ballot prefix count; the buffers are written to the segments after the scan loop.
+// A global store inside the loop would enter the same in-order vmcnt queue as the tile copies,
+// and the next tile wait would have to wait for the store's completion too; only a wavefront
+// whose buffer is full stores directly.
 //
 // Corpus streaming. Tiles of 64 rows go from HBM straight into a ring of LDS buffers with
 // global_load_lds_dwordx4 (no staging registers), kDepth - 1 tiles ahead of the one being
@@ -95,11 +99,10 @@ void mfmaScanKernel(ScanArgs scan, PhaseArgs phase, EmitArgs emit, int q_offset,
 
     __shared__ __attribute__((aligned(16))) std::uint8_t ring[kDepth][kTileBytes];
     __shared__ __attribute__((aligned(16))) float scale_ring[kScaleDepth][kRows];
-    __shared__ std::uint32_t lds_count[kQueriesPerLaunch];
     __shared__ std::uint32_t lds_simd[4];
     __shared__ std::uint64_t stage_key[kDense ? 1 : kWaves][kStaged];
-    __shared__ std::uint32_t stage_slot[kDense ? 1 : kWaves][kStaged];  // (segment slot << 8) | local query
-    __shared__ std::uint32_t stage_count[kWaves];
+    // (segment slot << 9) | (half << 8) | local query
+    __shared__ std::uint32_t stage_slot[kDense ? 1 : kWaves][kStaged];
 
     const int tid = threadIdx.x;
     const int lane = tid & (kWave - 1);
@@ -135,14 +138,8 @@ void mfmaScanKernel(ScanArgs scan, PhaseArgs phase, EmitArgs emit, int q_offset,
             tau_floor = t <= -3.402823466e+38f ? -INFINITY : t - fabsf(t) * kFilterMargin - 1e-30f;
         }
     }
-    for (int i = tid; i < kQueriesPerLaunch; i += kThreads) {
-        lds_count[i] = 0u;
-    }
     if (tid < 4) {
         lds_simd[tid] = 0u;
-    }
-    if (tid < kWaves) {
-        stage_count[tid] = 0u;
     }
 
     // ---- per-lane copy plan: LDS slot P of the tile holds global slot (P % spr) ^ swizzle(row);
@@ -194,7 +191,7 @@ void mfmaScanKernel(ScanArgs scan, PhaseArgs phase, EmitArgs emit, int q_offset,
             issue(ahead, d, d);
         }
     }
-    __syncthreads();  // lds_count and lds_simd initialization visible
+    __syncthreads();  // lds_simd initialization visible
 
     // Waits for this wavefront's copies of tile `item` (the ones issued after it belong to the at
     // most kDepth - 2 later tiles already in flight) and meets the other wavefronts.
@@ -356,19 +353,31 @@ void mfmaScanKernel(ScanArgs scan, PhaseArgs phase, EmitArgs emit, int q_offset,
             return passing;
         };
         const std::uint32_t seg_capacity = 1u << emit.seg_log2;
-        const std::size_t seg_base = static_cast<std::size_t>(blockIdx.x) * batch;
-        auto stageCandidate = [&](std::uint64_t key) {
-            const int qlocal_ = q - q_offset;
-            const std::uint32_t slot = atomicAdd(&lds_count[qlocal_], 1u);
-            if (slot >= seg_capacity) {
-                return;  // counted; the merge reports the overflow
+        // this lane's segment row: segment 2 * workgroup + half, query q
+        const std::size_t seg_row = (static_cast<std::size_t>(2 * blockIdx.x + half) * batch + q) << emit.seg_log2;
+        std::uint32_t seg_used = 0u;  // this lane's candidates so far (may exceed the capacity)
+        std::uint32_t parked = 0u;    // wave-uniform: entries of this wavefront's staging buffer
+        const std::uint32_t tag = (static_cast<std::uint32_t>(half) << 8) | static_cast<std::uint32_t>(q - q_offset);
+        // Appends `key` for the lanes with `take` set (called by the whole wavefront).
+        auto stageCandidates = [&](bool take, std::uint64_t key) {
+            const std::uint32_t slot = seg_used;
+            seg_used += take ? 1u : 0u;
+            const bool store = take && slot < seg_capacity;  // beyond it only counted: overflow
+            const std::uint64_t mask = __builtin_amdgcn_ballot_w64(store);
+            if (mask == 0ull) {
+                return;
             }
-            const std::uint32_t parked = atomicAdd(&stage_count[wave], 1u);
-            if (parked < static_cast<std::uint32_t>(kStaged)) {
-                stage_key[wave][parked] = key;
-                stage_slot[wave][parked] = (slot << 8) | static_cast<std::uint32_t>(qlocal_);
-            } else {
-                emit.seg[((seg_base + q) << emit.seg_log2) + slot] = key;
+            const std::uint32_t rank = __builtin_amdgcn_mbcnt_hi(static_cast<std::uint32_t>(mask >> 32),
+                                                                 __builtin_amdgcn_mbcnt_lo(static_cast<std::uint32_t>(mask), 0u));
+            const std::uint32_t at = parked + rank;
+            parked += static_cast<std::uint32_t>(__builtin_popcountll(mask));
+            if (store) {
+                if (at < static_cast<std::uint32_t>(kStaged)) {
+                    stage_key[wave][at] = key;
+                    stage_slot[wave][at] = (slot << 9) | tag;
+                } else {
+                    emit.seg[seg_row + slot] = key;
+                }
             }
         };
         // Exact scores and keys of the value slots `passing` marks; keys above the threshold are
@@ -389,12 +398,8 @@ void mfmaScanKernel(ScanArgs scan, PhaseArgs phase, EmitArgs emit, int q_offset,
                     const int dot = slot < 16 ? acc0[slot] : acc1[slot - 16];
                     const float combined = qscale * rs;
                     const float score = rs == rs ? static_cast<float>(dot) * combined : kMaskedScore;
-                    if (q_valid && rl < valid_rows && score >= tau_floor) {
-                        const std::uint64_t key = makeKey(score, row_base + static_cast<std::uint32_t>(rl));
-                        if (key > tau) {
-                            stageCandidate(key);
-                        }
-                    }
+                    const std::uint64_t key = makeKey(score, row_base + static_cast<std::uint32_t>(rl));
+                    stageCandidates(q_valid && rl < valid_rows && score >= tau_floor && key > tau, key);
                 }
             }
         };
@@ -413,6 +418,8 @@ void mfmaScanKernel(ScanArgs scan, PhaseArgs phase, EmitArgs emit, int q_offset,
                 exact(acc0, acc1, scale_ring[acc_sslot], acc_row0, owed);
             }
             owed = 0u;
+            // (issuing the refill before the pending exact pass measured slower: the pass's
+            // direct stores then queue behind the copies in the vmcnt order)
             refill(item, slot, sslot);
             if (wave_active) {
                 multiply(ring[slot], acc0, acc1);
@@ -433,18 +440,18 @@ void mfmaScanKernel(ScanArgs scan, PhaseArgs phase, EmitArgs emit, int q_offset,
             exact(acc0, acc1, scale_ring[acc_sslot], acc_row0, owed);
         }
 
-        // write the parked candidates of this wavefront
+        // write the parked candidates of this wavefront, then every lane's count
         {
-            const std::uint32_t parked = min(stage_count[wave], static_cast<std::uint32_t>(kStaged));
-            for (std::uint32_t i = static_cast<std::uint32_t>(lane); i < parked; i += kWave) {
+            const std::uint32_t held = min(parked, static_cast<std::uint32_t>(kStaged));
+            for (std::uint32_t i = static_cast<std::uint32_t>(lane); i < held; i += kWave) {
                 const std::uint32_t packed = stage_slot[wave][i];
+                const std::size_t segment = 2 * static_cast<std::size_t>(blockIdx.x) + ((packed >> 8) & 1u);
                 const std::size_t qg = static_cast<std::size_t>(q_offset) + (packed & 0xFFu);
-                emit.seg[((seg_base + qg) << emit.seg_log2) + (packed >> 8)] = stage_key[wave][i];
+                emit.seg[((segment * batch + qg) << emit.seg_log2) + (packed >> 9)] = stage_key[wave][i];
             }
         }
-        __syncthreads();
-        for (int i = tid; i < q_count; i += kThreads) {
-            emit.seg_count[static_cast<std::size_t>(blockIdx.x) * batch + q_offset + i] = lds_count[i];
+        if (q_valid) {
+            emit.seg_count[static_cast<std::size_t>(2 * blockIdx.x + half) * batch + q] = seg_used;
         }
     }
 }
@@ -493,6 +500,8 @@ bool mfmaSupported(const ScanArgs& scan) {
 }
 
 int mfmaWorkgroups() { return deviceComputeUnits(); }
+
+int mfmaSegmentsPerWorkgroup() { return 2; }
 
 int launchMfmaScan(const ScanArgs& scan, const PhaseArgs& phase, const EmitArgs& emit,
                    int workgroups, hipStream_t stream) {

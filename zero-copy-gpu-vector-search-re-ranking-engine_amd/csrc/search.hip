@@ -73,6 +73,7 @@ struct Plan {
     int width = 0;  // keys selected by the scan stage
     int block_rows = 64;
     int workgroups = 1;
+    int segments = 1;  // candidate segments per query of a threshold phase
     int seg_log2 = 5;
     long long dense_stride = 0;
     std::vector<PhaseArgs> phases;
@@ -358,10 +359,11 @@ Plan makePlan(const zcgvs_search_desc& d) {
         stride = next;
     }
     plan.dense_stride = first.items * plan.block_rows;
-    // Segment capacity: 4x the expected candidates per (workgroup, query) of the widest phase.
-    const long long expected = (static_cast<long long>(plan.width) * growth) / plan.workgroups;
-    // (at most 2^24 slots: the MFMA scan packs a slot and an 8-bit query into 32 bits)
-    plan.seg_log2 = std::min(24, std::max(5, ceilLog2(4 * expected + 16)));
+    plan.segments = plan.workgroups * (plan.use_mfma ? mfmaSegmentsPerWorkgroup() : 1);
+    // Segment capacity: 4x the expected candidates per (segment, query) of the widest phase.
+    const long long expected = (static_cast<long long>(plan.width) * growth) / plan.segments;
+    // (at most 2^23 slots: the int8 MFMA scan packs a slot, a half and an 8-bit query into 32 bits)
+    plan.seg_log2 = std::min(23, std::max(5, ceilLog2(4 * expected + 16)));
 
     if (plan.hybrid) {
         plan.lex = layout.add(static_cast<std::size_t>(batch) * n * 4);
@@ -369,8 +371,8 @@ Plan makePlan(const zcgvs_search_desc& d) {
     }
     plan.dense = layout.add(static_cast<std::size_t>(batch) * plan.dense_stride * 8);
     if (plan.phases.size() > 1) {
-        plan.seg = layout.add((static_cast<std::size_t>(plan.workgroups) * batch << plan.seg_log2) * 8);
-        plan.segcnt = layout.add(static_cast<std::size_t>(plan.workgroups) * batch * 4);
+        plan.seg = layout.add((static_cast<std::size_t>(plan.segments) * batch << plan.seg_log2) * 8);
+        plan.segcnt = layout.add(static_cast<std::size_t>(plan.segments) * batch * 4);
     }
     plan.keys = layout.add(static_cast<std::size_t>(batch) * plan.width * 8);
     plan.tau = layout.add(static_cast<std::size_t>(batch) * 8);
@@ -639,7 +641,7 @@ int searchTopk(const zcgvs_search_desc* desc, void* d_workspace, std::size_t wor
             in.k_prev = plan.width;
             in.seg = emit.seg;
             in.seg_count = emit.seg_count;
-            in.n_seg = plan.workgroups;
+            in.n_seg = plan.segments;
             in.seg_log2 = plan.seg_log2;
         }
         const bool last = p + 1 == plan.phases.size();
