@@ -335,6 +335,25 @@ void mfmaScanKernel(ScanArgs scan, PhaseArgs phase, EmitArgs emit, int q_offset,
             if (examine_all) {
                 return 0xFFFFFFFFu;
             }
+            // First the lane's largest relaxed score: the slot set is needed only when it reaches
+            // the lane's threshold somewhere in the wavefront.
+            float best = -INFINITY;
+#pragma unroll
+            for (int mb = 0; mb < 2; ++mb) {
+#pragma unroll
+                for (int g = 0; g < 4; ++g) {
+                    const float4 rs = *reinterpret_cast<const float4*>(scales + mb * 32 + 8 * g + 4 * half);
+                    const float rsv[4] = {rs.x, rs.y, rs.z, rs.w};
+#pragma unroll
+                    for (int j = 0; j < 4; ++j) {
+                        const int dot = mb == 0 ? acc0[4 * g + j] : acc1[4 * g + j];
+                        best = fmaxf(best, static_cast<float>(dot) * rsv[j]);
+                    }
+                }
+            }
+            if (!__any(best >= relaxed_floor)) {
+                return 0u;
+            }
             std::uint32_t passing = 0u;
 #pragma unroll
             for (int mb = 0; mb < 2; ++mb) {

@@ -4,7 +4,7 @@
 // successive digits (11, 11, 10 bits of the score, then 11, 11, 10 bits of the index part) narrow
 // down the bucket that holds the k-th best key. Once a bucket's population equals the number of
 // keys still needed, every key >= that bucket's lower edge is selected, which is exactly k keys
-// because keys are unique. The selected keys are then sorted descending with a bitonic network.
+// because keys are unique. Each selected key then goes to its rank in descending order.
 #pragma once
 
 #include "common.hpp"
@@ -111,23 +111,20 @@ __device__ inline void selectPickBucket(const std::uint32_t* hist, int width, Se
     __syncthreads();
 }
 
-// Sorts `n` (a power of two, <= 2 * kSelectThreads * 2) keys in LDS, descending.
-__device__ inline void bitonicSortDescending(std::uint64_t* keys, int n) {
-    for (int size = 2; size <= n; size <<= 1) {
-        for (int stride = size >> 1; stride > 0; stride >>= 1) {
-            for (int i = threadIdx.x; i < n / 2; i += blockDim.x) {
-                const int lo = 2 * i - (i & (stride - 1));
-                const int hi = lo + stride;
-                const bool descending = (lo & size) == 0;
-                const std::uint64_t a = keys[lo];
-                const std::uint64_t b = keys[hi];
-                if ((a < b) == descending) {
-                    keys[lo] = b;
-                    keys[hi] = a;
-                }
-            }
-            __syncthreads();
+// Visits the `count` keys of `keys` (in LDS, unique apart from repeated zero keys) with their
+// rank in descending order, the number of keys above them: key i belongs at position
+// #{j : keys[j] > keys[i]} of the sorted list. One pass of count comparisons per key (every lane
+// reads the same key, an LDS broadcast) and no barrier replace a sorting network.
+template <typename F>
+__device__ inline void forEachRanked(const std::uint64_t* keys, std::uint32_t count, F&& f) {
+    for (std::uint32_t i = threadIdx.x; i < count; i += blockDim.x) {
+        const std::uint64_t key = keys[i];
+        std::uint32_t rank = 0u;
+#pragma unroll 8
+        for (std::uint32_t j = 0; j < count; ++j) {
+            rank += keys[j] > key ? 1u : 0u;
         }
+        f(rank, key);
     }
 }
 

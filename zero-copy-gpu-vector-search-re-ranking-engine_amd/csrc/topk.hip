@@ -147,20 +147,20 @@ __global__ __launch_bounds__(kSelectThreads) void topkSortKernel(TopKScratch scr
                                                                  float* __restrict__ out_score) {
     __shared__ std::uint64_t lds_keys[kMaxK];
     const int q = blockIdx.x;
-    const std::uint32_t count = min(scratch.state(q)->count, static_cast<std::uint32_t>(kMaxK));
-    int padded = 1;
-    while (padded < k) {
-        padded <<= 1;
-    }
+    const std::uint32_t count = min(min(scratch.state(q)->count, static_cast<std::uint32_t>(kMaxK)),
+                                    static_cast<std::uint32_t>(k));
     const std::uint64_t* keys = in.keys(q);
-    for (int i = threadIdx.x; i < padded; i += blockDim.x) {
-        lds_keys[i] = i < static_cast<int>(count) ? keys[i] : 0ull;
+    for (std::uint32_t i = threadIdx.x; i < count; i += blockDim.x) {
+        lds_keys[i] = keys[i];
     }
     __syncthreads();
-    bitonicSortDescending(lds_keys, padded);
-    for (int i = threadIdx.x; i < k; i += blockDim.x) {
+    forEachRanked(lds_keys, count, [&](std::uint32_t rank, std::uint64_t key) {
+        const std::size_t o = static_cast<std::size_t>(q) * k + rank;
+        writeHit(key, &out_index[o], &out_score[o]);
+    });
+    for (int i = static_cast<int>(count) + threadIdx.x; i < k; i += blockDim.x) {
         const std::size_t o = static_cast<std::size_t>(q) * k + i;
-        writeHit(lds_keys[i], &out_index[o], &out_score[o]);
+        writeHit(0ull, &out_index[o], &out_score[o]);
     }
 }
 
@@ -362,28 +362,30 @@ __global__ __launch_bounds__(kMergeThreads) void selectMergeKernel(
         }
     });
     __syncthreads();
-    const std::uint32_t taken = min(lds_state.count, static_cast<std::uint32_t>(k));
-    int padded = 1;
-    while (padded < k) {
-        padded <<= 1;
-    }
-    for (int i = static_cast<int>(taken) + t; i < padded; i += blockDim.x) {
-        lds_keys[i] = 0ull;
-    }
-    __syncthreads();
-    bitonicSortDescending(lds_keys, padded);
-
+    // exactly min(n_valid, k) keys were collected (keys are unique)
+    const std::uint32_t taken = min(min(lds_state.count, static_cast<std::uint32_t>(kMaxK)),
+                                    static_cast<std::uint32_t>(k));
     std::uint64_t* dst = out_keys + static_cast<std::size_t>(q) * k;
-    for (int i = t; i < k; i += blockDim.x) {
-        dst[i] = lds_keys[i];
+    forEachRanked(lds_keys, taken, [&](std::uint32_t rank, std::uint64_t key) {
+        dst[rank] = key;
+        if (out_index != nullptr) {
+            const std::size_t o = static_cast<std::size_t>(q) * k + rank;
+            writeHit(key, &out_index[o], &out_score[o]);
+        }
+        if (threshold != nullptr && rank == static_cast<std::uint32_t>(k) - 1u) {
+            threshold[q] = key;
+        }
+    });
+    for (int i = static_cast<int>(taken) + t; i < k; i += blockDim.x) {
+        dst[i] = 0ull;
         if (out_index != nullptr) {
             const std::size_t o = static_cast<std::size_t>(q) * k + i;
-            writeHit(lds_keys[i], &out_index[o], &out_score[o]);
+            writeHit(0ull, &out_index[o], &out_score[o]);
         }
     }
     if (t == 0) {
-        if (threshold != nullptr) {
-            threshold[q] = taken >= static_cast<std::uint32_t>(k) ? lds_keys[k - 1] : 0ull;
+        if (threshold != nullptr && taken < static_cast<std::uint32_t>(k)) {
+            threshold[q] = 0ull;
         }
         if (overflow != nullptr && (lds_overflow != 0u || in.reset_overflow)) {
             overflow[q] = lds_overflow != 0u ? 1u : 0u;
