@@ -21,7 +21,7 @@ constexpr int kKindI8 = ZCGVS_DTYPE_I8;
 constexpr int kKindBinary = ZCGVS_DTYPE_BINARY;
 constexpr int kKindI8I8 = 4;
 
-constexpr int kMaxChunksPerLane = 4;
+constexpr int kMaxChunksPerLane = 8;
 constexpr std::size_t kValuQueryLds = 60 * 1024;
 
 int kindOf(const ScanArgs& scan) {
@@ -287,7 +287,7 @@ void launchKind(int lanes, dim3 grid, std::size_t shared, hipStream_t stream, co
 ValuShape valuShape(const ScanArgs& scan) {
     ValuShape shape;
     const int chunks = chunksOf(scan);
-    shape.lanes = lanesPerRow(chunks);
+    shape.lanes = lanesPerRow(chunks, kMaxChunksPerLane);
     const int rows_per_iter = (kScanThreads / kWave) * (kWave / shape.lanes);
     shape.block_rows = rows_per_iter * std::max(1, 64 / rows_per_iter);
     shape.workgroups = deviceComputeUnits() * 4;
@@ -310,7 +310,8 @@ bool valuSupported(const ScanArgs& scan) {
         return false;
     }
     const int chunks = static_cast<int>(bytes / 16);
-    return (chunks + lanesPerRow(chunks) - 1) / lanesPerRow(chunks) <= kMaxChunksPerLane;
+    const int lanes = lanesPerRow(chunks, kMaxChunksPerLane);
+    return (chunks + lanes - 1) / lanes <= kMaxChunksPerLane;
 }
 
 int launchValuScan(const ScanArgs& scan, const PhaseArgs& phase, const EmitArgs& emit,

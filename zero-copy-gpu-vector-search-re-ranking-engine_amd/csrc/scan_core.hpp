@@ -85,21 +85,77 @@ __device__ __forceinline__ uint4 loadChunkStreaming(const std::uint8_t* pointer)
     return make_uint4(raw.x, raw.y, raw.z, raw.w);
 }
 
-// Sum over the L lanes of a group (L a power of two <= 64); every lane gets the total.
+// Partner value for step `step` of groupSum: inside a row of 16 lanes the data-parallel
+// primitives pair lane i with i ^ 1, i ^ 2 (quad permutes), 7 - i within each half-row and 15 - i
+// within the row (mirrors); every pairing joins two groups that already hold their own sums, so
+// after the step each lane holds the sum of the union. Across rows a swizzle (xor 16 inside 32
+// lanes) and a permute (xor 32) follow.
+template <int kStep>
+__device__ __forceinline__ int groupPartner(int bits) {
+    if constexpr (kStep == 0) {
+        return __builtin_amdgcn_update_dpp(0, bits, 0xB1, 0xF, 0xF, false);  // quad_perm [1,0,3,2]
+    } else if constexpr (kStep == 1) {
+        return __builtin_amdgcn_update_dpp(0, bits, 0x4E, 0xF, 0xF, false);  // quad_perm [2,3,0,1]
+    } else if constexpr (kStep == 2) {
+        return __builtin_amdgcn_update_dpp(0, bits, 0x141, 0xF, 0xF, false);  // row_half_mirror
+    } else if constexpr (kStep == 3) {
+        return __builtin_amdgcn_update_dpp(0, bits, 0x140, 0xF, 0xF, false);  // row_mirror
+    } else if constexpr (kStep == 4) {
+        return __builtin_amdgcn_ds_swizzle(bits, 0x401F);  // xor 16 within 32 lanes
+    } else {
+        return __shfl_xor(bits, 32, kWave);
+    }
+}
+
+template <typename T>
+__device__ __forceinline__ int asBits(T value) {
+    if constexpr (sizeof(T) == 4 && !__is_integral(T)) {
+        return __float_as_int(value);
+    } else {
+        return static_cast<int>(value);
+    }
+}
+
+template <typename T>
+__device__ __forceinline__ T fromBits(int bits) {
+    if constexpr (sizeof(T) == 4 && !__is_integral(T)) {
+        return __int_as_float(bits);
+    } else {
+        return static_cast<T>(bits);
+    }
+}
+
+// Sum over the L lanes of a group (L a power of two <= 64, groups aligned to L); every lane of
+// the group gets the same total.
 template <int L, typename T>
 __device__ __forceinline__ T groupSum(T value) {
-#pragma unroll
-    for (int offset = L / 2; offset > 0; offset >>= 1) {
-        value += waveXor(value, offset);
+    static_assert(sizeof(T) == 4, "32-bit values");
+    if constexpr (L >= 2) {
+        value += fromBits<T>(groupPartner<0>(asBits(value)));
+    }
+    if constexpr (L >= 4) {
+        value += fromBits<T>(groupPartner<1>(asBits(value)));
+    }
+    if constexpr (L >= 8) {
+        value += fromBits<T>(groupPartner<2>(asBits(value)));
+    }
+    if constexpr (L >= 16) {
+        value += fromBits<T>(groupPartner<3>(asBits(value)));
+    }
+    if constexpr (L >= 32) {
+        value += fromBits<T>(groupPartner<4>(asBits(value)));
+    }
+    if constexpr (L >= 64) {
+        value += fromBits<T>(groupPartner<5>(asBits(value)));
     }
     return value;
 }
 
 // Lanes per row for a row of `chunks` 16-byte chunks: the smallest power of two giving each
-// lane at most four chunks, capped at a full wavefront.
-inline int lanesPerRow(int chunks) {
+// lane at most `per_lane` chunks, capped at a full wavefront.
+inline int lanesPerRow(int chunks, int per_lane = 4) {
     int lanes = 1;
-    while (lanes < kWave && (chunks + lanes - 1) / lanes > 4) {
+    while (lanes < kWave && (chunks + lanes - 1) / lanes > per_lane) {
         lanes <<= 1;
     }
     return lanes;
