@@ -117,4 +117,24 @@ __device__ __forceinline__ T waveXor(T value, int mask) {
     return __shfl_xor(value, mask, kWave);
 }
 
+// Reduction of a 64-bit value over the 64 lanes of a wavefront with an associative, commutative
+// `op`; every lane gets the result. Inside each row of 16 lanes the partners come from
+// data-parallel moves (quad permutes, half-row and row mirrors), then a swizzle joins the rows of
+// each 32-lane half and a permute joins the halves.
+template <typename Op>
+__device__ __forceinline__ std::uint64_t waveReduce64(std::uint64_t value, Op op) {
+    auto partner = [](std::uint64_t v, auto move) {
+        const int lo = move(static_cast<int>(static_cast<std::uint32_t>(v)));
+        const int hi = move(static_cast<int>(static_cast<std::uint32_t>(v >> 32)));
+        return (static_cast<std::uint64_t>(static_cast<std::uint32_t>(hi)) << 32) | static_cast<std::uint32_t>(lo);
+    };
+    value = op(value, partner(value, [](int x) { return __builtin_amdgcn_update_dpp(0, x, 0xB1, 0xF, 0xF, false); }));
+    value = op(value, partner(value, [](int x) { return __builtin_amdgcn_update_dpp(0, x, 0x4E, 0xF, 0xF, false); }));
+    value = op(value, partner(value, [](int x) { return __builtin_amdgcn_update_dpp(0, x, 0x141, 0xF, 0xF, false); }));
+    value = op(value, partner(value, [](int x) { return __builtin_amdgcn_update_dpp(0, x, 0x140, 0xF, 0xF, false); }));
+    value = op(value, partner(value, [](int x) { return __builtin_amdgcn_ds_swizzle(x, 0x401F); }));
+    value = op(value, partner(value, [](int x) { return __shfl_xor(x, 32, kWave); }));
+    return value;
+}
+
 }  // namespace zcgvs_hip

@@ -81,12 +81,13 @@ template <int kThreads = kSelectThreads>
 __device__ inline void selectPickBucket(const std::uint32_t* hist, int width, SelectState* state,
                                         std::uint32_t* scratch) {
     const int bins = 1 << width;
-    const int per_thread = bins / kThreads;  // 8 or 4 bins at 256 threads, 2 or 1 at 1024
+    const int per_thread = (bins + kThreads - 1) / kThreads;  // 8 or 4 at 256 threads, 2 or 1 at 1024
     const int t = threadIdx.x;
-    // Thread t owns the t-th group of bins counted from the top.
+    // Thread t owns the t-th group of bins counted from the top (none once they run out).
     const int top = bins - per_thread * t;  // exclusive upper bin
+    const int bottom = max(0, top - per_thread);
     std::uint32_t local = 0;
-    for (int b = top - 1; b >= top - per_thread; --b) {
+    for (int b = top - 1; b >= bottom; --b) {
         local += hist[b];
     }
     const std::uint32_t need = state->need;
@@ -95,7 +96,7 @@ __device__ inline void selectPickBucket(const std::uint32_t* hist, int width, Se
     const std::uint32_t before = through - local;
     if (before < need && need <= through) {
         std::uint32_t above = before;
-        for (int b = top - 1; b >= top - per_thread; --b) {
+        for (int b = top - 1; b >= bottom; --b) {
             const std::uint32_t h = hist[b];
             if (above + h >= need) {
                 const std::uint32_t remaining = need - above;

@@ -229,6 +229,9 @@ __global__ __launch_bounds__(kMergeThreads) void selectMergeKernel(
     __shared__ SelectState lds_state;
     __shared__ std::uint32_t lds_valid;
     __shared__ std::uint32_t lds_overflow;
+    __shared__ std::uint32_t lds_wave_count[kMergeThreads / kWave];
+    __shared__ std::uint64_t lds_wave_lo[kMergeThreads / kWave];
+    __shared__ std::uint64_t lds_wave_hi[kMergeThreads / kWave];
 
     const int q = blockIdx.x;
     const int t = threadIdx.x;
@@ -323,18 +326,52 @@ __global__ __launch_bounds__(kMergeThreads) void selectMergeKernel(
         }
     };
 
-    std::uint32_t mine = 0u;
-    forEachKey([&](std::uint64_t) { ++mine; });
-    atomicAdd(&lds_valid, mine);
-    __syncthreads();
-    const std::uint32_t n_valid = lds_valid;
-    if (t == 0) {
-        lds_state.done = n_valid <= static_cast<std::uint32_t>(k) ? 1u : 0u;
+    // Count, smallest and largest valid key: per-thread values, wavefront reductions, one LDS
+    // slot per wavefront (a block-wide atomic on one word would serialize 1024 updates).
+    {
+        std::uint32_t mine = 0u;
+        std::uint64_t lo = ~0ull;
+        std::uint64_t hi = 0ull;
+        forEachKey([&](std::uint64_t key) {
+            ++mine;
+            lo = min(lo, key);
+            hi = max(hi, key);
+        });
+        mine = static_cast<std::uint32_t>(
+            waveReduce64(mine, [](std::uint64_t a, std::uint64_t b) { return a + b; }));
+        lo = waveReduce64(lo, [](std::uint64_t a, std::uint64_t b) { return min(a, b); });
+        hi = waveReduce64(hi, [](std::uint64_t a, std::uint64_t b) { return max(a, b); });
+        if ((t & (kWave - 1)) == 0) {
+            lds_wave_count[t / kWave] = mine;
+            lds_wave_lo[t / kWave] = lo;
+            lds_wave_hi[t / kWave] = hi;
+        }
     }
     __syncthreads();
+    if (t == 0) {
+        std::uint32_t count = 0u;
+        std::uint64_t lo = ~0ull;
+        std::uint64_t hi = 0ull;
+        for (int w = 0; w < kMergeThreads / kWave; ++w) {
+            count += lds_wave_count[w];
+            lo = min(lo, lds_wave_lo[w]);
+            hi = max(hi, lds_wave_hi[w]);
+        }
+        lds_valid = count;
+        lds_state.done = count <= static_cast<std::uint32_t>(k) ? 1u : 0u;
+        if (count > static_cast<std::uint32_t>(k)) {
+            // The keys (unique, at least two) share their top `common` bits: the radix passes
+            // start below them, so the first digit already separates the keys.
+            const int common = __clzll(hi ^ lo);
+            lds_state.prefix = common == 0 ? 0ull : (hi >> (64 - common));
+            lds_state.bits = static_cast<std::uint32_t>(common);
+        }
+    }
+    __syncthreads();
+    const std::uint32_t n_valid = lds_valid;
 
     for (int pass = 0; pass < kSelectPasses && !lds_state.done; ++pass) {
-        const int width = selectDigitWidth(pass);
+        const int width = min(11, 64 - static_cast<int>(lds_state.bits));
         for (int i = t; i < (1 << width); i += blockDim.x) {
             lds_hist[i] = 0u;
         }
