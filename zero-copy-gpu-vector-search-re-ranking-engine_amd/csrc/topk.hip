@@ -390,14 +390,37 @@ __global__ __launch_bounds__(kMergeThreads) void selectMergeKernel(
     }
 
     const std::uint64_t cut = n_valid <= static_cast<std::uint32_t>(k) ? 1ull : selectThreshold(lds_state);
-    forEachKey([&](std::uint64_t key) {
-        if (key >= cut) {
-            const std::uint32_t slot = atomicAdd(&lds_state.count, 1u);
-            if (slot < static_cast<std::uint32_t>(kMaxK)) {
-                lds_keys[slot] = key;
+    if (in_lds) {
+        // one slot reservation per wavefront step (ballot, popcount, prefix count)
+        const std::uint32_t n = static_cast<std::uint32_t>(gathered);
+        for (std::uint32_t base = 0; base < n; base += blockDim.x) {
+            const std::uint32_t i = base + static_cast<std::uint32_t>(t);
+            const std::uint64_t key = i < n ? lds_cand[i] : 0ull;
+            const bool take = key != 0ull && key >= cut;
+            const std::uint64_t mask = __builtin_amdgcn_ballot_w64(take);
+            if (mask != 0ull) {
+                std::uint32_t first = 0u;
+                if ((t & (kWave - 1)) == 0) {
+                    first = atomicAdd(&lds_state.count, static_cast<std::uint32_t>(__builtin_popcountll(mask)));
+                }
+                first = __builtin_amdgcn_readfirstlane(first);
+                const std::uint32_t slot = first + __builtin_amdgcn_mbcnt_hi(static_cast<std::uint32_t>(mask >> 32),
+                                                                             __builtin_amdgcn_mbcnt_lo(static_cast<std::uint32_t>(mask), 0u));
+                if (take && slot < static_cast<std::uint32_t>(kMaxK)) {
+                    lds_keys[slot] = key;
+                }
             }
         }
-    });
+    } else {
+        forEachCandidate(in, q, batch, lds_seg, [&](std::uint64_t key) {
+            if (key >= cut) {
+                const std::uint32_t slot = atomicAdd(&lds_state.count, 1u);
+                if (slot < static_cast<std::uint32_t>(kMaxK)) {
+                    lds_keys[slot] = key;
+                }
+            }
+        });
+    }
     __syncthreads();
     // exactly min(n_valid, k) keys were collected (keys are unique)
     const std::uint32_t taken = min(min(lds_state.count, static_cast<std::uint32_t>(kMaxK)),
