@@ -42,6 +42,8 @@ QUERY_SEED = 4321
 WORKLOADS = {
     "int8-10m": dict(kind="i8i8", n=10_000_000, dim=768, batch=256, k=100,
                      name="per-vector int8 10M x 768, batch 256, k=100"),
+    "int8-10m-b1": dict(kind="i8i8", n=10_000_000, dim=768, batch=1, k=100,
+                        name="per-vector int8 10M x 768, batch 1, k=100"),
     "f32-1m-b1": dict(kind="f32", n=1_000_000, dim=384, batch=1, k=10,
                       name="float32 1M x 384, batch 1, k=10"),
     "f16-1m-b1": dict(kind="f16", n=1_000_000, dim=384, batch=1, k=10,
@@ -156,7 +158,7 @@ def measured_traffic(workload, kernel):
 
 
 def scan_kernel_name(w):
-    if w["kind"] == "i8i8":
+    if w["kind"] == "i8i8" and w["batch"] >= 8:
         return f"mfmaScanKernel<{w['dim'] // 32}, false>"
     if w["kind"] in ("f32", "f16", "hybrid") and w["batch"] >= 4 and w["dim"] in (128, 256, 384, 512):
         kind = 0 if w["kind"] == "f32" else 1
@@ -336,7 +338,7 @@ def main(argv=None) -> int:
             "all_scan_launches_ms": round(scan_ms, 4),
         },
     }
-    if w["kind"] == "i8i8":
+    if w["kind"] == "i8i8" and scan_kernel_name(w).startswith("mfma"):
         ops = statistics.mean(2.0 * phase_rows[p] * w["dim"] * batch for p in launches)
         tops = ops / (mean_ms * 1e-3) / 1e12
         result["mfma"] = {"achieved": round(tops, 1), "peak": INT8_MFMA_PEAK_TOPS, "unit": "TOP/s",

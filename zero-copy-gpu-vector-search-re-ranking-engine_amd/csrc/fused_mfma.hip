@@ -78,6 +78,7 @@ constexpr int kQueriesPerLaunch = kWaves * 32;
 constexpr float kFilterMargin = 9.5367431640625e-07f;  // 2^-20
 constexpr std::size_t kRingBudget = 150 * 1024;
 constexpr int kStaged = 64;  // candidates parked per wavefront before they reach the segments
+constexpr int kMinBatch = 8;
 
 template <int kKSteps, bool kDense>
 __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(2, 2)))
@@ -495,6 +496,11 @@ int launchShape(const ScanArgs& scan, const PhaseArgs& phase, const EmitArgs& em
 }  // namespace
 
 bool mfmaSupported(const ScanArgs& scan) {
+    // Below 8 queries the VALU scan (sdot4) is bound by HBM alone, while this kernel would keep
+    // seven of its eight wavefronts idle.
+    if (scan.batch < kMinBatch) {
+        return false;
+    }
     // The kernel reads no mask: the search merges an allow-mask into the row scales first.
     if (scan.dtype != ZCGVS_DTYPE_I8 || scan.row_scales == nullptr || scan.lexical != nullptr ||
         scan.mask != nullptr) {

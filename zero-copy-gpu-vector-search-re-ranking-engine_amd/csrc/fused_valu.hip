@@ -50,7 +50,9 @@ int chunksOf(const ScanArgs& scan) {
     return static_cast<int>(rowBytes(scan.dtype, scan.dim) / 16);
 }
 
-template <int kKind, int L>
+// kTile: queries scored per pass over a row (1 for single-query launches, which then keep one
+// accumulator per lane instead of a tile's worth).
+template <int kKind, int L, int kTile>
 __global__ __launch_bounds__(kScanThreads) void valuScanKernel(ScanArgs scan, PhaseArgs phase,
                                                                EmitArgs emit, int chunks,
                                                                int q_offset, int q_count) {
@@ -145,13 +147,13 @@ __global__ __launch_bounds__(kScanThreads) void valuScanKernel(ScanArgs scan, Ph
                 row_scale = live ? scan.row_scales[row] : 0.0f;
             }
 
-            for (int qt = 0; qt < q_count; qt += kQueryTile) {
-                const int tile = min(kQueryTile, q_count - qt);
-                float score[kQueryTile];
+            for (int qt = 0; qt < q_count; qt += kTile) {
+                const int tile = min(kTile, q_count - qt);
+                float score[kTile];
                 if constexpr (kKind == kKindBinary || kKind == kKindI8I8) {
-                    int acc[kQueryTile];
+                    int acc[kTile];
 #pragma unroll
-                    for (int q = 0; q < kQueryTile; ++q) {
+                    for (int q = 0; q < kTile; ++q) {
                         acc[q] = 0;
                     }
 #pragma unroll
@@ -159,7 +161,7 @@ __global__ __launch_bounds__(kScanThreads) void valuScanKernel(ScanArgs scan, Ph
                         const int c = group + t * L;
                         if (c < chunks) {
 #pragma unroll
-                            for (int q = 0; q < kQueryTile; ++q) {
+                            for (int q = 0; q < kTile; ++q) {
                                 if (q < tile) {
                                     const uint4 qw = *reinterpret_cast<const uint4*>(
                                         staged + static_cast<std::size_t>(qt + q) * stage_words + 4 * c);
@@ -179,7 +181,7 @@ __global__ __launch_bounds__(kScanThreads) void valuScanKernel(ScanArgs scan, Ph
                         }
                     }
 #pragma unroll
-                    for (int q = 0; q < kQueryTile; ++q) {
+                    for (int q = 0; q < kTile; ++q) {
                         if (q < tile) {
                             const int total = groupSum<L>(acc[q]);
                             if constexpr (kKind == kKindBinary) {
@@ -193,9 +195,9 @@ __global__ __launch_bounds__(kScanThreads) void valuScanKernel(ScanArgs scan, Ph
                 } else {
                     using Traits = ChunkTraits<kKind>;
                     constexpr int E = Traits::kElems;
-                    float acc[kQueryTile];
+                    float acc[kTile];
 #pragma unroll
-                    for (int q = 0; q < kQueryTile; ++q) {
+                    for (int q = 0; q < kTile; ++q) {
                         acc[q] = 0.0f;
                     }
                     const float* fstaged = reinterpret_cast<const float*>(staged);
@@ -206,7 +208,7 @@ __global__ __launch_bounds__(kScanThreads) void valuScanKernel(ScanArgs scan, Ph
                             float v[E];
                             Traits::decode(raw[t], scan.scale, v);
 #pragma unroll
-                            for (int q = 0; q < kQueryTile; ++q) {
+                            for (int q = 0; q < kTile; ++q) {
                                 if (q < tile) {
                                     const float* qv = fstaged + static_cast<std::size_t>(qt + q) * stage_words + c * E;
                                     if (l2) {
@@ -226,7 +228,7 @@ __global__ __launch_bounds__(kScanThreads) void valuScanKernel(ScanArgs scan, Ph
                         }
                     }
 #pragma unroll
-                    for (int q = 0; q < kQueryTile; ++q) {
+                    for (int q = 0; q < kTile; ++q) {
                         if (q < tile) {
                             const float total = groupSum<L>(acc[q]);
                             score[q] = l2 ? -total : total;
@@ -236,7 +238,7 @@ __global__ __launch_bounds__(kScanThreads) void valuScanKernel(ScanArgs scan, Ph
 
                 // ---- emit ----
 #pragma unroll
-                for (int q = 0; q < kQueryTile; ++q) {
+                for (int q = 0; q < kTile; ++q) {
                     if (q < tile && (q % L) == group) {
                         const int gq = q_offset + qt + q;
                         std::uint64_t key = 0ull;
@@ -267,18 +269,28 @@ __global__ __launch_bounds__(kScanThreads) void valuScanKernel(ScanArgs scan, Ph
     }
 }
 
+template <int kKind, int kTile>
+void launchLanes(int lanes, dim3 grid, std::size_t shared, hipStream_t stream, const ScanArgs& scan,
+                 const PhaseArgs& phase, const EmitArgs& emit, int chunks, int q_offset, int q_count) {
+    switch (lanes) {
+        case 1: valuScanKernel<kKind, 1, kTile><<<grid, kScanThreads, shared, stream>>>(scan, phase, emit, chunks, q_offset, q_count); break;
+        case 2: valuScanKernel<kKind, 2, kTile><<<grid, kScanThreads, shared, stream>>>(scan, phase, emit, chunks, q_offset, q_count); break;
+        case 4: valuScanKernel<kKind, 4, kTile><<<grid, kScanThreads, shared, stream>>>(scan, phase, emit, chunks, q_offset, q_count); break;
+        case 8: valuScanKernel<kKind, 8, kTile><<<grid, kScanThreads, shared, stream>>>(scan, phase, emit, chunks, q_offset, q_count); break;
+        case 16: valuScanKernel<kKind, 16, kTile><<<grid, kScanThreads, shared, stream>>>(scan, phase, emit, chunks, q_offset, q_count); break;
+        case 32: valuScanKernel<kKind, 32, kTile><<<grid, kScanThreads, shared, stream>>>(scan, phase, emit, chunks, q_offset, q_count); break;
+        default: valuScanKernel<kKind, 64, kTile><<<grid, kScanThreads, shared, stream>>>(scan, phase, emit, chunks, q_offset, q_count); break;
+    }
+}
+
 template <int kKind>
 void launchKind(int lanes, dim3 grid, std::size_t shared, hipStream_t stream, const ScanArgs& scan,
                 const PhaseArgs& phase, const EmitArgs& emit, int chunks, int q_offset,
                 int q_count) {
-    switch (lanes) {
-        case 1: valuScanKernel<kKind, 1><<<grid, kScanThreads, shared, stream>>>(scan, phase, emit, chunks, q_offset, q_count); break;
-        case 2: valuScanKernel<kKind, 2><<<grid, kScanThreads, shared, stream>>>(scan, phase, emit, chunks, q_offset, q_count); break;
-        case 4: valuScanKernel<kKind, 4><<<grid, kScanThreads, shared, stream>>>(scan, phase, emit, chunks, q_offset, q_count); break;
-        case 8: valuScanKernel<kKind, 8><<<grid, kScanThreads, shared, stream>>>(scan, phase, emit, chunks, q_offset, q_count); break;
-        case 16: valuScanKernel<kKind, 16><<<grid, kScanThreads, shared, stream>>>(scan, phase, emit, chunks, q_offset, q_count); break;
-        case 32: valuScanKernel<kKind, 32><<<grid, kScanThreads, shared, stream>>>(scan, phase, emit, chunks, q_offset, q_count); break;
-        default: valuScanKernel<kKind, 64><<<grid, kScanThreads, shared, stream>>>(scan, phase, emit, chunks, q_offset, q_count); break;
+    if (q_count == 1) {
+        launchLanes<kKind, 1>(lanes, grid, shared, stream, scan, phase, emit, chunks, q_offset, q_count);
+    } else {
+        launchLanes<kKind, kQueryTile>(lanes, grid, shared, stream, scan, phase, emit, chunks, q_offset, q_count);
     }
 }
 

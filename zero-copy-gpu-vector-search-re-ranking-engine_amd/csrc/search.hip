@@ -32,10 +32,12 @@ namespace {
 constexpr std::size_t kAlign = 256;
 // Each threshold phase visits up to `growth` times as many rows as all phases before it, so it
 // yields about width * growth candidates per query on a corpus in random order. The growth is 8,
-// or larger while batch * width * growth stays within kCandidateBudget keys (small batches and k
-// then need only a dense sample and one threshold phase).
+// or larger while batch * width * growth stays within kCandidateBudget keys and one query's
+// candidates fit the merge's LDS gather (small batches and k then need only a dense sample and
+// one threshold phase).
 constexpr long long kPhaseGrowth = 8;
 constexpr long long kCandidateBudget = 1LL << 18;
+constexpr long long kMergeLdsKeys = 12288;  // candidate keys a query's merge gathers in LDS (topk.hip)
 
 std::size_t alignUp(std::size_t value) { return (value + kAlign - 1) / kAlign * kAlign; }
 
@@ -328,7 +330,11 @@ Plan makePlan(const zcgvs_search_desc& d) {
     // that keeps its keys within the merge's LDS capacity); each later phase
     // visits up to growth_cap times as many blocks as all phases before it.
     long long growth_cap = kPhaseGrowth;
-    while (growth_cap * 2 * batch * plan.width <= kCandidateBudget) {
+    // A phase yields about width * growth candidates per query; beyond kMergeLdsKeys (with the
+    // width keys kept from before) a query's merge walks its segments in global memory, once per
+    // radix pass, which costs far more than one more phase.
+    while (growth_cap * 2 * batch * plan.width <= kCandidateBudget &&
+           (growth_cap * 2 + 1) * plan.width <= kMergeLdsKeys) {
         growth_cap *= 2;
     }
     const long long blocks = (n + plan.block_rows - 1) / plan.block_rows;
