@@ -74,6 +74,9 @@ def test_fused_i8_reference_mode_with_mask(gpu):
     (40_000, 1024, 300, 16),    # two query launches, one n-block per wavefront
     (30_000, 256, 8, 1024),     # k at capacity
     (20_000, 96, 9, 25),        # dim outside the MFMA set: VALU int8 x int8 path
+    (300_000, 768, 1, 100),     # single query: VALU int8 x int8 path, several threshold phases
+    (50_000, 768, 7, 50),       # below the MFMA batch minimum
+    (50_000, 512, 8, 10),       # smallest MFMA batch
 ])
 def test_fused_i8i8_bit_exact(gpu, n, dim, batch, k):
     capi = gpu

@@ -40,22 +40,31 @@ __device__ __forceinline__ std::uint64_t selectThreshold(const SelectState& s) {
     return s.bits >= 64 ? s.prefix : (s.prefix << (64 - s.bits));
 }
 
+// Inclusive sum over the 64 lanes of a wavefront (lanes 0..l) with data-parallel moves: a
+// Hillis-Steele scan inside each 16-lane row (row shifts by 1, 2, 4, 8; lanes shifted in from
+// outside the row read 0), then lane 15 of each row is added to the next row and lane 31 to the
+// upper half. All lanes must be active.
+__device__ __forceinline__ std::uint32_t waveInclusiveSum(std::uint32_t value) {
+    int v = static_cast<int>(value);
+    v += __builtin_amdgcn_update_dpp(0, v, 0x111, 0xF, 0xF, true);  // row_shr:1
+    v += __builtin_amdgcn_update_dpp(0, v, 0x112, 0xF, 0xF, true);  // row_shr:2
+    v += __builtin_amdgcn_update_dpp(0, v, 0x114, 0xF, 0xF, true);  // row_shr:4
+    v += __builtin_amdgcn_update_dpp(0, v, 0x118, 0xF, 0xF, true);  // row_shr:8
+    v += __builtin_amdgcn_update_dpp(0, v, 0x142, 0xA, 0xF, false);  // row_bcast:15 into rows 1, 3
+    v += __builtin_amdgcn_update_dpp(0, v, 0x143, 0xC, 0xF, false);  // row_bcast:31 into rows 2, 3
+    return static_cast<std::uint32_t>(v);
+}
+
 // Inclusive sum of `value` over the block's threads in thread order (threads 0..t), for a block
-// of kThreads threads: a shuffle scan inside each wavefront, then the wavefront totals through
-// LDS (`wave_sums`, kThreads / kWave words). `total` receives the block's sum. Two barriers;
-// every thread must call it.
+// of kThreads threads: a wavefront scan, then the wavefront totals through LDS (`wave_sums`,
+// kThreads / kWave words). `total` receives the block's sum. Two barriers; every thread must
+// call it.
 template <int kThreads = kSelectThreads>
 __device__ inline std::uint32_t blockInclusiveSum(std::uint32_t value, std::uint32_t* wave_sums,
                                                   std::uint32_t* total) {
     const int lane = threadIdx.x & (kWave - 1);
     const int wave = threadIdx.x / kWave;
-#pragma unroll
-    for (int offset = 1; offset < kWave; offset <<= 1) {
-        const std::uint32_t other = __shfl_up(value, offset, kWave);
-        if (lane >= offset) {
-            value += other;
-        }
-    }
+    value = waveInclusiveSum(value);
     if (lane == kWave - 1) {
         wave_sums[wave] = value;
     }

@@ -244,29 +244,31 @@ __global__ __launch_bounds__(kMergeThreads) void selectMergeKernel(
         lds_state.count = 0u;
     }
     __syncthreads();
-    const std::uint32_t cap = 1u << in.seg_log2;
-    for (int s = t; s < in.n_seg; s += blockDim.x) {
-        const std::uint32_t c = in.seg_count[static_cast<std::size_t>(s) * batch + q];
-        lds_seg[s] = min(c, cap);
-        if (c > cap) {
-            lds_overflow = 1u;
-        }
-    }
-    __syncthreads();
-    // Exclusive scan of the segment counts: thread t owns a contiguous run of segments.
-    const int per_thread = (in.n_seg + kMergeThreads - 1) / kMergeThreads;
-    std::uint32_t run = 0u;
-    for (int i = 0; i < per_thread; ++i) {
-        const int s = t * per_thread + i;
-        run += s < in.n_seg ? lds_seg[s] : 0u;
-    }
     std::uint32_t seg_total = 0u;
-    std::uint32_t acc = blockInclusiveSum<kMergeThreads>(run, lds_scan, &seg_total) - run;
-    for (int i = 0; i < per_thread; ++i) {
-        const int s = t * per_thread + i;
-        if (s < in.n_seg) {
-            lds_offset[s] = acc;
-            acc += lds_seg[s];
+    if (in.n_seg > 0) {  // (uniform: a kernel argument)
+        const std::uint32_t cap = 1u << in.seg_log2;
+        for (int s = t; s < in.n_seg; s += blockDim.x) {
+            const std::uint32_t c = in.seg_count[static_cast<std::size_t>(s) * batch + q];
+            lds_seg[s] = min(c, cap);
+            if (c > cap) {
+                lds_overflow = 1u;
+            }
+        }
+        __syncthreads();
+        // Exclusive scan of the segment counts: thread t owns a contiguous run of segments.
+        const int per_thread = (in.n_seg + kMergeThreads - 1) / kMergeThreads;
+        std::uint32_t run = 0u;
+        for (int i = 0; i < per_thread; ++i) {
+            const int s = t * per_thread + i;
+            run += s < in.n_seg ? lds_seg[s] : 0u;
+        }
+        std::uint32_t acc = blockInclusiveSum<kMergeThreads>(run, lds_scan, &seg_total) - run;
+        for (int i = 0; i < per_thread; ++i) {
+            const int s = t * per_thread + i;
+            if (s < in.n_seg) {
+                lds_offset[s] = acc;
+                acc += lds_seg[s];
+            }
         }
     }
     const std::uint32_t k_prev = in.prev != nullptr ? static_cast<std::uint32_t>(in.k_prev) : 0u;
