@@ -161,8 +161,9 @@ struct MergeInputs {
     bool reset_overflow = false;
 };
 
-// Selects the best k keys of each query's candidate set; writes them sorted descending to
-// out_keys[q][0..k), sets threshold[q] to the k-th best key (0 if fewer than k keys exist) and
+// Selects the best k keys of each query's candidate set; writes them to out_keys[q][0..k)
+// (sorted descending when out_index is set, in no particular order otherwise; missing keys are
+// 0 at the end), sets threshold[q] to the k-th best key (0 if fewer than k keys exist) and
 // sets overflow[q] when a segment count exceeded its capacity (and clears it otherwise when
 // in.reset_overflow is set). When out_index/out_score are
 // non-null the selection is also written as (index, score) pairs [batch, k].

@@ -428,16 +428,37 @@ __global__ __launch_bounds__(kMergeThreads) void selectMergeKernel(
     const std::uint32_t taken = min(min(lds_state.count, static_cast<std::uint32_t>(kMaxK)),
                                     static_cast<std::uint32_t>(k));
     std::uint64_t* dst = out_keys + static_cast<std::size_t>(q) * k;
-    forEachRanked(lds_keys, taken, [&](std::uint32_t rank, std::uint64_t key) {
-        dst[rank] = key;
-        if (out_index != nullptr) {
+    if (out_index != nullptr) {
+        // the search's result: every key at its rank
+        forEachRanked(lds_keys, taken, [&](std::uint32_t rank, std::uint64_t key) {
+            dst[rank] = key;
             const std::size_t o = static_cast<std::size_t>(q) * k + rank;
             writeHit(key, &out_index[o], &out_score[o]);
+            if (threshold != nullptr && rank == static_cast<std::uint32_t>(k) - 1u) {
+                threshold[q] = key;
+            }
+        });
+    } else {
+        // Between phases only the set and its smallest key (the threshold) matter: the keys stay
+        // in collection order.
+        std::uint64_t lo = ~0ull;
+        for (std::uint32_t i = static_cast<std::uint32_t>(t); i < taken; i += blockDim.x) {
+            const std::uint64_t key = lds_keys[i];
+            dst[i] = key;
+            lo = min(lo, key);
         }
-        if (threshold != nullptr && rank == static_cast<std::uint32_t>(k) - 1u) {
-            threshold[q] = key;
+        lo = waveReduce64(lo, [](std::uint64_t a, std::uint64_t b) { return min(a, b); });
+        if ((t & (kWave - 1)) == 0) {
+            lds_wave_lo[t / kWave] = lo;
         }
-    });
+        __syncthreads();
+        if (t == 0 && threshold != nullptr && taken >= static_cast<std::uint32_t>(k)) {
+            for (int w = 0; w < kMergeThreads / kWave; ++w) {
+                lo = min(lo, lds_wave_lo[w]);
+            }
+            threshold[q] = lo;
+        }
+    }
     for (int i = static_cast<int>(taken) + t; i < k; i += blockDim.x) {
         dst[i] = 0ull;
         if (out_index != nullptr) {
