@@ -9,9 +9,11 @@
 // a lower bound of the final k-th best key, so no final hit is ever dropped.
 //
 // Emission. Each workgroup appends its candidates for query q to its own segment
-// seg[(wg * batch + q) << seg_log2 ...], counting with LDS atomics (no global atomics, so the
-// scan's memory pipeline never waits on a returning atomic), and stores its per-query counts
-// when it finishes. A count above the segment capacity is reported as overflow by the merge.
+// seg[(s * batch + q) << seg_log2 ...] (s = the workgroup; the int8 MFMA scan gives each workgroup
+// two segments, one per row half of a query's lanes, and counts in registers), counting with LDS
+// atomics (no global atomics, so the scan's memory pipeline never waits on a returning atomic),
+// and stores its per-query counts when it finishes. A count above the segment capacity is
+// reported as overflow by the merge.
 #pragma once
 
 #include "common.hpp"

@@ -4,8 +4,8 @@
 // Layout. A corpus row of `chunks` 16-byte chunks is read by a group of L consecutive lanes of a
 // 64-wide wavefront; lane g of the group reads chunks g, g+L, g+2L, ... so each load instruction
 // of the wave fetches 64/L rows x (L x 16 B) contiguous segments. L is chosen so that a lane reads
-// at most four chunks per row. The per-lane partial sums are combined with an xor butterfly
-// inside the group, which leaves the row's sum in every lane of the group.
+// at most four chunks per row (eight in the fused VALU scan). The per-lane partial sums are
+// combined inside the group by groupSum, which leaves the row's sum in every lane of the group.
 //
 // Arithmetic follows include/zcgvs/cuda/decode.cuh:22-42: the stored value is widened to float32
 // (int8 values are multiplied by the matrix-wide scale first), dot/cosine accumulate q * x and L2
