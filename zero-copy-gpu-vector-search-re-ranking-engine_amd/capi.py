@@ -263,6 +263,34 @@ class Event:
             pass
 
 
+class Graph:
+    """The work `record()` enqueues on `stream`, captured once (zcgvs_graph_begin_capture /
+    end_capture) and replayed with launch(); the reference's Searcher graph cache
+    (src/search/searcher.cpp:287-342) does the same for a repeated query shape."""
+
+    def __init__(self, stream: Stream, record):
+        call("zcgvs_graph_begin_capture", stream.handle)
+        handle = _vp()
+        try:
+            record()
+        finally:
+            # the capture must end even when recording failed; that error is the one raised
+            status = library().zcgvs_graph_end_capture(stream.handle, ctypes.byref(handle))
+        check(status)
+        self.handle = handle.value
+
+    def launch(self, stream: Stream) -> None:
+        call("zcgvs_graph_launch", self.handle, stream.handle)
+
+    def __del__(self):
+        try:
+            if getattr(self, "handle", None) and _lib is not None:
+                _lib.zcgvs_graph_destroy(self.handle)
+                self.handle = None
+        except Exception:
+            pass
+
+
 # ---- launcher wrappers (device pointers in, status checked) ---------------------------------
 
 def launch_similarity(corpus, dtype, scale, n, dim, queries, batch, mask, metric, scores, stream=None):
