@@ -33,6 +33,9 @@ constexpr int kSweepThreads = 256;
 constexpr int kSweepDocs = 1024;              // documents per sweep workgroup
 constexpr int kSweepPerThread = kSweepDocs / kSweepThreads;  // postings per thread per slot
 constexpr int kSweepSlotGroup = 8;            // slots whose postings are loaded together
+// Workgroups go to the XCDs (each with its own L2) round-robin in launch order; the sweep keeps
+// every query of a slice on one XCD (see bm25SweepKernel).
+constexpr int kXcds = 8;
 
 // Postings of term slot `slot` for each query (blockIdx.y) of the batch.
 __global__ __launch_bounds__(kPostingThreads) void bm25SlotKernel(
@@ -84,13 +87,17 @@ __device__ __forceinline__ std::int64_t lowerBound(const int* __restrict__ docs,
 
 // bounds[(q * term_stride + slot) * (slices + 1) + c] = first posting of the term in slot `slot`
 // of query q whose document is >= c * kSweepDocs (c = slices: >= doc_count); an unknown term
-// gets 0 everywhere (an empty range). One thread per entry, so all searches run at once.
+// gets 0 everywhere (an empty range). One thread per entry, so all searches run at once. Also
+// zeroes lexical_max[0, batch) (there are at least batch entries: slices + 1 >= 2, term_stride >= 1).
 __global__ void bm25BoundsKernel(const std::int64_t* __restrict__ offsets, const int* __restrict__ docs,
                                  const int* __restrict__ query_terms, int term_stride, int batch,
                                  int doc_count, int vocab_size, int slices,
-                                 std::int64_t* __restrict__ bounds) {
+                                 std::int64_t* __restrict__ bounds, float* __restrict__ lexical_max) {
     const long long total = static_cast<long long>(batch) * term_stride * (slices + 1);
     const long long i = static_cast<long long>(blockIdx.x) * blockDim.x + threadIdx.x;
+    if (i < batch) {
+        lexical_max[i] = 0.0f;  // the sweep that follows raises it
+    }
     if (i >= total) {
         return;
     }
@@ -108,16 +115,29 @@ __global__ void bm25BoundsKernel(const std::int64_t* __restrict__ offsets, const
 // BM25 scores of documents [blockIdx.x * kSweepDocs, + kSweepDocs) for query blockIdx.y from the
 // postings between the slice bounds; writes every score of the slice and raises lexical_max[q]
 // (zeroed beforehand) to the slice's max(0, max score). A slot's postings inside one slice are
-// distinct documents, so there are at most kSweepDocs of them: each thread loads up to
-// kSweepPerThread per slot, for kSweepSlotGroup slots at a time, before any is added, and the
-// additions of one slot touch distinct accumulator entries.
+// distinct documents, so there are at most kSweepDocs of them: thread t loads postings
+// begin + 4t .. + 3 with one 16-byte load of documents and one of weights (a range's last load
+// starts at end - 4, so no load leaves the range; ranges under 4 postings load them one by one),
+// for kSweepSlotGroup slots at a time, before any is added, and the additions of one slot touch
+// distinct accumulator entries.
+//
+// Queries share their frequent terms, whose postings cover most documents, so the launch's
+// queries of one slice run back to back on one XCD: workgroup w runs on XCD w % kXcds as that
+// XCD's (w / kXcds)-th, which takes query q_offset + (w / kXcds) % q_count of slice
+// kXcds * ((w / kXcds) / q_count) + w % kXcds; the later queries then find the slice's shared
+// postings in that XCD's L2. The grid has kXcds * ceil(slices / kXcds) * q_count workgroups.
 __global__ __launch_bounds__(kSweepThreads) void bm25SweepKernel(
     const int* __restrict__ docs, const float* __restrict__ weights, const std::int64_t* __restrict__ bounds,
-    int term_stride, int doc_count, int slices, float* __restrict__ scores, float* __restrict__ lexical_max) {
-    __shared__ float acc[kSweepDocs];
+    int term_stride, int doc_count, int slices, int q_offset, int q_count, float* __restrict__ scores,
+    float* __restrict__ lexical_max) {
+    __shared__ __attribute__((aligned(16))) float acc[kSweepDocs];
     __shared__ float partial[kSweepThreads / kWave];
-    const int q = blockIdx.y;
-    const int c = blockIdx.x;
+    const int xcd_rank = static_cast<int>(blockIdx.x / kXcds);
+    const int q = q_offset + xcd_rank % q_count;
+    const int c = kXcds * (xcd_rank / q_count) + static_cast<int>(blockIdx.x % kXcds);
+    if (c >= slices) {
+        return;
+    }
     const int t = threadIdx.x;
     const int d0 = c * kSweepDocs;
     const int d1 = min(d0 + kSweepDocs, doc_count);
@@ -131,9 +151,8 @@ __global__ __launch_bounds__(kSweepThreads) void bm25SweepKernel(
         float weight[kSweepSlotGroup][kSweepPerThread];
         std::int64_t begin[kSweepSlotGroup];
         std::int64_t end[kSweepSlotGroup];
-        // Every load of the group is issued before any loaded value is used: positions past a
-        // slot's range read its last posting (the range is uniform; an empty one loads nothing)
-        // and validity is decided later from the positions alone.
+        int first[kSweepSlotGroup];  // this thread's postings are entries [first, last) of its load
+        int last[kSweepSlotGroup];
 #pragma unroll
         for (int g = 0; g < kSweepSlotGroup; ++g) {  // all bounds first: one wait for all of them
             const int slot = g0 + g;
@@ -144,16 +163,27 @@ __global__ __launch_bounds__(kSweepThreads) void bm25SweepKernel(
                 end[g] = qb[static_cast<std::size_t>(slot) * (slices + 1) + c + 1];
             }
         }
+        // Every load of the group is issued before any loaded value is used.
 #pragma unroll
         for (int g = 0; g < kSweepSlotGroup; ++g) {
-            if (end[g] > begin[g]) {
+            const std::int64_t count = end[g] - begin[g];  // uniform over the workgroup
+            const std::int64_t p = begin[g] + static_cast<std::int64_t>(kSweepPerThread) * t;
+            first[g] = 0;
+            last[g] = 0;
+            if (count >= kSweepPerThread) {
+                const std::int64_t from = p < end[g] - kSweepPerThread ? p : end[g] - kSweepPerThread;
+                __builtin_memcpy(&doc[g][0], docs + from, sizeof(doc[g]));
+                __builtin_memcpy(&weight[g][0], weights + from, sizeof(weight[g]));
+                first[g] = static_cast<int>(p - from);
+                last[g] = static_cast<int>(min(end[g], p + kSweepPerThread) - from);
+            } else if (count > 0) {
 #pragma unroll
                 for (int j = 0; j < kSweepPerThread; ++j) {
-                    const std::int64_t p = begin[g] + t + j * kSweepThreads;
-                    const std::int64_t safe = p < end[g] ? p : end[g] - 1;
-                    doc[g][j] = docs[safe];
-                    weight[g][j] = weights[safe];
+                    const std::int64_t at = begin[g] + j < end[g] ? begin[g] + j : end[g] - 1;
+                    doc[g][j] = docs[at];
+                    weight[g][j] = weights[at];
                 }
+                last[g] = t == 0 ? static_cast<int>(count) : 0;
             }
         }
 #pragma unroll
@@ -162,10 +192,9 @@ __global__ __launch_bounds__(kSweepThreads) void bm25SweepKernel(
                 if (end[g] > begin[g]) {
 #pragma unroll
                     for (int j = 0; j < kSweepPerThread; ++j) {
-                        const std::int64_t p = begin[g] + t + j * kSweepThreads;
                         // distinct documents within a slot: plain adds do not race (and an
                         // LDS float atomic is several times slower here)
-                        if (p < end[g] && doc[g][j] >= d0 && doc[g][j] < d1) {
+                        if (j >= first[g] && j < last[g] && doc[g][j] >= d0 && doc[g][j] < d1) {
                             acc[doc[g][j] - d0] += weight[g][j];
                         }
                     }
@@ -184,11 +213,18 @@ __global__ __launch_bounds__(kSweepThreads) void bm25SweepKernel(
     }
     float best = 0.0f;
     float* row = scores + static_cast<std::size_t>(q) * doc_count + d0;
-    for (int i = t; i < d1 - d0; i += kSweepThreads) {
-        const float value = acc[i];
-        row[i] = value;
-        best = fmaxf(best, value);
+    if (d1 - d0 == kSweepDocs && (reinterpret_cast<std::uintptr_t>(row) & 15u) == 0) {
+        const float4 value = reinterpret_cast<const float4*>(acc)[t];
+        reinterpret_cast<float4*>(row)[t] = value;
+        best = fmaxf(fmaxf(value.x, value.y), fmaxf(value.z, value.w));
+    } else {
+        for (int i = t; i < d1 - d0; i += kSweepThreads) {
+            const float value = acc[i];
+            row[i] = value;
+            best = fmaxf(best, value);
+        }
     }
+    best = fmaxf(best, 0.0f);
 #pragma unroll
     for (int offset = kWave / 2; offset > 0; offset >>= 1) {
         best = fmaxf(best, waveXor(best, offset));
@@ -278,19 +314,26 @@ int launchLexicalScores(const std::int64_t* offsets, const int* docs, const floa
                         int vocab_size, const int* query_terms, int term_stride, int batch,
                         int doc_count, float* lexical, float* lexical_max, std::int64_t* bounds,
                         hipStream_t stream) {
-    zeroKernel<<<1, 256, 0, stream>>>(lexical_max, static_cast<std::size_t>(batch));
-    ZCGVS_LAUNCH_CHECK("lexical zero");
     if (bounds != nullptr) {
         const int slices = (doc_count + kSweepDocs - 1) / kSweepDocs;
         const long long entries = static_cast<long long>(batch) * term_stride * (slices + 1);
         bm25BoundsKernel<<<static_cast<unsigned>((entries + 255) / 256), 256, 0, stream>>>(
-            offsets, docs, query_terms, term_stride, batch, doc_count, vocab_size, slices, bounds);
+            offsets, docs, query_terms, term_stride, batch, doc_count, vocab_size, slices, bounds, lexical_max);
         ZCGVS_LAUNCH_CHECK("bm25 bounds");
-        bm25SweepKernel<<<dim3(static_cast<unsigned>(slices), static_cast<unsigned>(batch)), kSweepThreads, 0,
-                          stream>>>(docs, weights, bounds, term_stride, doc_count, slices, lexical, lexical_max);
+        // queries per launch: the grid's threads stay below 2^31
+        const long long per_query = static_cast<long long>((slices + kXcds - 1) / kXcds) * kXcds;
+        const int chunk = static_cast<int>(std::max<long long>(
+            1, std::min<long long>(batch, (1LL << 31) / (per_query * kSweepThreads))));
+        for (int q0 = 0; q0 < batch; q0 += chunk) {
+            const int count = std::min(chunk, batch - q0);
+            bm25SweepKernel<<<static_cast<unsigned>(per_query * count), kSweepThreads, 0, stream>>>(
+                docs, weights, bounds, term_stride, doc_count, slices, q0, count, lexical, lexical_max);
+        }
         ZCGVS_LAUNCH_CHECK("bm25 sweep");
         return ZCGVS_OK;
     }
+    zeroKernel<<<1, 256, 0, stream>>>(lexical_max, static_cast<std::size_t>(batch));
+    ZCGVS_LAUNCH_CHECK("lexical zero");
     const std::size_t elements = static_cast<std::size_t>(batch) * doc_count;
     zeroKernel<<<std::min<std::size_t>(8192, (elements + 255) / 256), 256, 0, stream>>>(lexical, elements);
     ZCGVS_LAUNCH_CHECK("lexical zero");
