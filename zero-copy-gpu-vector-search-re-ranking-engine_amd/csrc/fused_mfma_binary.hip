@@ -4,17 +4,22 @@
 // hammingScanKernel) and scores (d - 2h) / d (include/zcgvs/cuda/decode.cuh:45-47).
 //
 // Arithmetic. With r the row's bits and q the query's bits as 0/1 values,
-//   sum_k r_k (1 - 2 q_k) = popc(r) - 2 r.q,  so  h = popc(r) + popc(q) - 2 r.q = acc + popc(q)
-// where acc is the int8 MFMA product of the row as 0/1 bytes (A) with the query as +-1 bytes (B).
-// Integer arithmetic throughout, so h is exact; the score is the reference's IEEE division
+//   sum_k r_k (1 - 2 q_k) = popc(r) - 2 r.q,  so  h = popc(r) + popc(q) - 2 r.q = acc / 64 + popc(q)
+// where acc is the int8 MFMA product of the row's bytes (A) with the query's (B), which are
+// scaled so that every product is 64 r_k (1 - 2 q_k) (below). Integer arithmetic throughout, so
+// h is exact; the score is the reference's IEEE division
 // (d - 2h) / d. A threshold phase compares h itself with the integer threshold equivalent to the
 // query's key threshold (scores are strictly decreasing in h), so the division runs only for
 // keys that pass.
 //
-// Expansion. Each lane turns 16 bits of its row into 16 bytes per k-step: four nibbles, each
-// spread to the low bits of four bytes by (n * 0x204081) & 0x01010101 (the partial products
-// n << 0, 7, 14, 21 do not overlap). That VALU work is shared by the two query groups of 16 a
-// wavefront serves.
+// Expansion. Each lane turns one 32-bit word of its row into 16 bytes per k-step, half of the
+// word per step: dword j of step half p holds bit 8e + 4p + j of the word in byte e. That is a
+// fixed permutation of the word's dims, and the query's B operand uses the same one; a dot
+// product does not depend on the order of its dims. With s = 4p + j < 7 the dword is
+// word & (0x01010101 << s), bytes of 0 or 2^s, and the query's bytes are (1 - 2 q_k) 2^(6 - s);
+// with s = 7 it is (word >> 7) & 0x01010101 against (1 - 2 q_k) 64. So one AND per dword (and a
+// shift for s = 7), shared by the two query groups of 16 a wavefront serves, and every product
+// is 64 r_k (1 - 2 q_k) (|acc| <= 64 d fits int32 easily).
 //
 // Work split. 8 wavefronts; a wavefront serves a set of up to 32 queries (two groups of 16, B
 // operands in registers for the whole launch) and a share of each tile's 16-row blocks; with
@@ -22,7 +27,7 @@
 //
 // MFMA layout (v_mfma_i32_16x16x64_i8). Lane l supplies row (A) / query (B) l % 16 and 16 dims
 // of lane group h = l / 16 per step: 16-byte chunk h + 4j of the row covers steps 8j .. 8j + 7,
-// two 16-bit halves of each of its words in turn; A and B use the same assignment, so every
+// each of its words in turn, in two halves (above); A and B use the same assignment, so every
 // dim is counted once. D: lane l holds query l % 16 and rows 4h + i, i < 4.
 //
 // Corpus streaming as in the other MFMA scans (lds_copy.hpp): ~32 KB tiles HBM -> LDS by
@@ -71,39 +76,38 @@ struct BinaryTile {
     }
 };
 
-// 16 bits -> 16 bytes of 0/1 (byte e of dword j = bit 4j + e).
-__device__ __forceinline__ v4i spreadBits(std::uint32_t bits16) {
+// Half p of a row word -> 16 bytes: byte e of dword j is bit 8e + s (s = 4p + j) of the word,
+// times 2^s for s < 7 and times 1 for s = 7.
+__device__ __forceinline__ v4i spreadWord(std::uint32_t word, int p) {
     v4i out;
 #pragma unroll
     for (int j = 0; j < 4; ++j) {
-        const std::uint32_t nibble = __builtin_amdgcn_ubfe(bits16, 4 * j, 4);
-        out[j] = static_cast<int>(__umul24(nibble, 0x204081u) & 0x01010101u);
+        const int shift = 4 * p + j;
+        out[j] = static_cast<int>(shift < 7 ? word & (0x01010101u << shift) : (word >> 7) & 0x01010101u);
     }
     return out;
 }
 
-// 16 bits -> 16 bytes of +1 (bit clear) / -1 (bit set).
-__device__ __forceinline__ v4i signBytes(std::uint32_t bits16) {
+// The same 16 dims of a query word as spreadWord, as bytes of (1 - 2 bit) w with w = 2^(6 - s)
+// for s < 7 and w = 64 for s = 7, so that every product with spreadWord's byte is 64 r (1 - 2 q).
+__device__ __forceinline__ v4i signWord(std::uint32_t word, int p) {
     v4i out;
 #pragma unroll
     for (int j = 0; j < 4; ++j) {
-        std::uint32_t word = 0u;
-#pragma unroll
-        for (int e = 0; e < 4; ++e) {
-            const std::uint32_t bit = (bits16 >> (4 * j + e)) & 1u;
-            word |= (bit ? 0xFFu : 0x01u) << (8 * e);
-        }
-        out[j] = static_cast<int>(word);
+        const int shift = 4 * p + j;
+        const std::uint32_t w = shift < 7 ? 1u << (6 - shift) : 64u;
+        const std::uint32_t bits = (word >> shift) & 0x01010101u;
+        // per byte w (bit clear) or 256 - w (bit set, i.e. -w as int8); no carries between bytes
+        out[j] = static_cast<int>(w * 0x01010101u + bits * (256u - 2u * w));
     }
     return out;
 }
 
-// 16 bits of step t (lane group h) from the lane's chunk words: chunk jc = t / 8, word (t % 8) / 2,
-// half t % 2.
+// The word of step t (lane group h) from the lane's chunk words: chunk jc = t / 8, word
+// (t % 8) / 2; the step takes its half t % 2.
 template <int kLaneChunks>
-__device__ __forceinline__ std::uint32_t stepBits(const u32x4 (&chunk)[kLaneChunks], int t) {
-    const std::uint32_t word = chunk[t / 8][(t % 8) / 2];
-    return (t % 2) ? (word >> 16) : (word & 0xFFFFu);
+__device__ __forceinline__ std::uint32_t stepWord(const u32x4 (&chunk)[kLaneChunks], int t) {
+    return chunk[t / 8][(t % 8) / 2];
 }
 
 template <int kWords, bool kDense>
@@ -171,7 +175,7 @@ void mfmaBinaryScanKernel(ScanArgs scan, PhaseArgs phase, EmitArgs emit, int q_o
         popq[g] = pop;
 #pragma unroll
         for (int t = 0; t < kSteps; ++t) {
-            qb[g][t] = valid_of[g] ? signBytes(stepBits<kLaneChunks>(chunk, t)) : v4i{0, 0, 0, 0};
+            qb[g][t] = valid_of[g] ? signWord(stepWord<kLaneChunks>(chunk, t), t % 2) : v4i{0, 0, 0, 0};
         }
         h_limit[g] = kDim + 1;  // no threshold: every h passes
         row_limit[g] = 0xFFFFFFFFu;
@@ -192,11 +196,11 @@ void mfmaBinaryScanKernel(ScanArgs scan, PhaseArgs phase, EmitArgs emit, int q_o
             }
         }
     }
-    // acc threshold of the fast reject (invalid queries never pass)
+    // acc threshold of the fast reject (acc = 64 (h - popc(q)); invalid queries never pass)
     int acc_limit[2];
 #pragma unroll
     for (int g = 0; g < 2; ++g) {
-        acc_limit[g] = valid_of[g] ? h_limit[g] - popq[g] : -(kDim + 1);
+        acc_limit[g] = 64 * (valid_of[g] ? h_limit[g] - popq[g] : -(kDim + 1));
     }
     for (int i = tid; i < kQueriesPerLaunch; i += kThreads) {
         lds_count[i] = 0u;
@@ -269,7 +273,7 @@ void mfmaBinaryScanKernel(ScanArgs scan, PhaseArgs phase, EmitArgs emit, int q_o
         for (int i = 0; i < 4; ++i) {
             const int local = block * 16 + 4 * h + i;
             const long long row = row0 + local;
-            const int hd = acc[i] + popq[g];
+            const int hd = (acc[i] >> 6) + popq[g];  // acc is 64 times the +-1 dot, exactly
             if constexpr (kDense) {
                 std::uint64_t key = 0ull;
                 if (row < doc_count) {
@@ -315,13 +319,13 @@ void mfmaBinaryScanKernel(ScanArgs scan, PhaseArgs phase, EmitArgs emit, int q_o
                 // not reading, so the VALU work runs under the MFMAs instead of waiting for them
                 // to read their operands; a sched_barrier per step pins that order.
                 v4i a[2];
-                a[0] = spreadBits(stepBits<kLaneChunks>(chunk, 0));
+                a[0] = spreadWord(stepWord<kLaneChunks>(chunk, 0), 0);
 #pragma unroll
                 for (int t = 0; t < kSteps; ++t) {
                     acc0 = __builtin_amdgcn_mfma_i32_16x16x64_i8(a[t % 2], qb[0][t], acc0, 0, 0, 0);
                     acc1 = __builtin_amdgcn_mfma_i32_16x16x64_i8(a[t % 2], qb[1][t], acc1, 0, 0, 0);
                     if (t + 1 < kSteps) {
-                        a[(t + 1) % 2] = spreadBits(stepBits<kLaneChunks>(chunk, t + 1));
+                        a[(t + 1) % 2] = spreadWord(stepWord<kLaneChunks>(chunk, t + 1), (t + 1) % 2);
                         // keeps step t's operand allocated until the expansion is written, so
                         // the two buffers never share registers
                         asm volatile("" ::"v"(a[t % 2]));
@@ -334,7 +338,7 @@ void mfmaBinaryScanKernel(ScanArgs scan, PhaseArgs phase, EmitArgs emit, int q_o
                         emitKeys(acc1, 1, row0, block, item);
                     }
                 } else {
-                    // Fast reject: a key can pass only if acc <= h_limit - popc(q) (h = acc +
+                    // Fast reject: a key can pass only if acc <= 64 (h_limit - popc(q)) (h = acc / 64 +
                     // popc(q)); one ballot over the wavefront's 8 products usually ends here.
                     const int m0 = min(min(acc0[0], acc0[1]), min(acc0[2], acc0[3]));
                     const int m1 = min(min(acc1[0], acc1[1]), min(acc1[2], acc1[3]));
