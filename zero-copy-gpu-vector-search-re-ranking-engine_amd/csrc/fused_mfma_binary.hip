@@ -30,8 +30,9 @@
 // each of its words in turn, in two halves (above); A and B use the same assignment, so every
 // dim is counted once. D: lane l holds query l % 16 and rows 4h + i, i < 4.
 //
-// Corpus streaming as in the other MFMA scans (lds_copy.hpp): ~32 KB tiles HBM -> LDS by
-// global_load_lds_dwordx4 in a 4-deep ring. LDS slot s of row r holds chunk s ^ swz(r) with
+// Corpus streaming as in the other MFMA scans (lds_copy.hpp): 48 KB tiles HBM -> LDS by
+// global_load_lds_dwordx4 in a 3-deep ring (smaller tiles in deeper rings measured slower: the
+// per-tile barrier costs more than the extra copies in flight gain). LDS slot s of row r holds chunk s ^ swz(r) with
 // swz(r) = (r / (256 / row bytes)) & (chunks - 1), so the 16 rows of one ds_read_b128
 // quarter-wave hit 16 distinct 16-byte bank groups.
 #include <hip/hip_runtime.h>
@@ -53,7 +54,7 @@ constexpr int kThreads = 512;
 constexpr int kWaves = kThreads / kWave;
 constexpr int kSetQueries = 32;  // two MFMA query groups of 16 per wavefront
 constexpr int kQueriesPerLaunch = 4 * kSetQueries;
-constexpr int kTileBytesTarget = 32 * 1024;
+constexpr int kTileBytesTarget = 48 * 1024;
 constexpr int kMinBatch = 4;  // below this the VALU popcount scan does less work per row
 
 template <int kWords>
@@ -65,12 +66,12 @@ struct BinaryTile {
     static constexpr int kRows = kTileBytesTarget / kRowBytes;
     static constexpr int kRowBlocks = kRows / 16;
     static constexpr int kTileBytes = kRows * kRowBytes;
-    static constexpr int kDepth = 4;
+    static constexpr int kDepth = 3;
     static constexpr int kCopies = kTileBytes / 16 / kThreads;
     static constexpr int kRowsPerBankPeriod = 256 / kRowBytes;
     static_assert(kChunks % 4 == 0 && kChunks <= 8, "rows of 64 or 128 bytes (queries in registers)");
     static_assert(kTileBytes % (16 * kThreads) == 0, "tile must split over the lanes");
-    static_assert(3 * kCopies < 63, "copies in flight fit the vmcnt counter");
+    static_assert((kDepth - 1) * kCopies < 63, "copies in flight fit the vmcnt counter");
     __host__ __device__ static constexpr int swizzle(int row) {
         return (row / kRowsPerBankPeriod) & (kChunks - 1);
     }

@@ -58,22 +58,20 @@ __device__ constexpr int vmcntOnly(int n) {
     return (n & 0xF) | (0x7 << 4) | (0xF << 8) | ((n >> 4) << 14);
 }
 
-// Waits until at most `later * kPerTile` copies are pending (later <= kMaxLater, wave-uniform).
+// Waits until at most `later * kPerTile` copies are pending (later <= kMaxLater, wave-uniform;
+// kMaxLater * kPerTile fits the 6-bit vmcnt).
 template <int kPerTile, int kMaxLater>
 __device__ __forceinline__ void waitTiles(int later) {
-    if constexpr (kMaxLater >= 2) {
-        if (later >= 2) {
-            __builtin_amdgcn_s_waitcnt(vmcntOnly(2 * kPerTile));
-            return;
-        }
-    }
+    static_assert(kMaxLater * kPerTile <= 63, "vmcnt counts at most 63 operations");
     if constexpr (kMaxLater >= 1) {
-        if (later == 1) {
-            __builtin_amdgcn_s_waitcnt(vmcntOnly(kPerTile));
+        if (later >= kMaxLater) {
+            __builtin_amdgcn_s_waitcnt(vmcntOnly(kMaxLater * kPerTile));
             return;
         }
+        waitTiles<kPerTile, kMaxLater - 1>(later);
+    } else {
+        __builtin_amdgcn_s_waitcnt(vmcntOnly(0));
     }
-    __builtin_amdgcn_s_waitcnt(vmcntOnly(0));
 }
 
 // SIMD of the calling wavefront (HW_ID register, SIMD_ID field: bits 5:4).
