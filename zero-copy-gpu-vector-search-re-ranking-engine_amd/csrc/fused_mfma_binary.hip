@@ -21,9 +21,11 @@
 // shift for s = 7), shared by the two query groups of 16 a wavefront serves, and every product
 // is 64 r_k (1 - 2 q_k) (|acc| <= 64 d fits int32 easily).
 //
-// Work split. 8 wavefronts; a wavefront serves a set of up to 32 queries (two groups of 16, B
-// operands in registers for the whole launch) and a share of each tile's 16-row blocks; with
-// more than one set per launch (up to 4, 128 queries) the wavefronts of a set split the blocks.
+// Work split. Launches of up to 32 queries (one set, two MFMA query groups of 16) run
+// mfmaBinaryStreamKernel: the B operands sit in LDS and each of 16 wavefronts streams its own
+// rows into registers (no shared tile, no barrier). Larger launches (up to 4 sets, 128 queries)
+// run mfmaBinaryScanKernel: 8 wavefronts, each with one set's B operands in registers, share the
+// tiles below and split each tile's 16-row blocks among the wavefronts of a set.
 //
 // MFMA layout (v_mfma_i32_16x16x64_i8). Lane l supplies row (A) / query (B) l % 16 and 16 dims
 // of lane group h = l / 16 per step: 16-byte chunk h + 4j of the row covers steps 8j .. 8j + 7,
@@ -111,6 +113,29 @@ __device__ __forceinline__ std::uint32_t stepWord(const u32x4 (&chunk)[kLaneChun
     return chunk[t / 8][(t % 8) / 2];
 }
 
+// The integer form of query q's key threshold in a threshold phase: a key passes when h < h_limit,
+// or h == h_limit and its row is below row_limit (the lower index wins a tie); without a threshold
+// every h passes.
+template <int kDim>
+__device__ __forceinline__ void binaryThreshold(const EmitArgs& emit, int q, int& h_limit, std::uint32_t& row_limit) {
+    h_limit = kDim + 1;
+    row_limit = 0xFFFFFFFFu;
+    const std::uint64_t tau = emit.tau[q];
+    if (tau != 0ull) {
+        const float t_score = keyScore(tau);
+        // the h whose score (d - 2h) / d is exactly the threshold's score
+        const float estimate = (static_cast<float>(kDim) - t_score * static_cast<float>(kDim)) * 0.5f;
+        int ht = estimate >= 0.0f && estimate <= static_cast<float>(kDim) ? static_cast<int>(rintf(estimate)) : 0;
+        for (int c = max(0, ht - 2); c <= min(kDim, ht + 2); ++c) {
+            if (static_cast<float>(kDim - 2 * c) / static_cast<float>(kDim) == t_score) {
+                ht = c;
+            }
+        }
+        h_limit = ht;
+        row_limit = 0xFFFFFFFFu - static_cast<std::uint32_t>(tau);
+    }
+}
+
 template <int kWords, bool kDense>
 __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(2, 2)))
 void mfmaBinaryScanKernel(ScanArgs scan, PhaseArgs phase, EmitArgs emit, int q_offset, int q_count) {
@@ -181,20 +206,7 @@ void mfmaBinaryScanKernel(ScanArgs scan, PhaseArgs phase, EmitArgs emit, int q_o
         h_limit[g] = kDim + 1;  // no threshold: every h passes
         row_limit[g] = 0xFFFFFFFFu;
         if constexpr (!kDense) {
-            const std::uint64_t tau = emit.tau[q];
-            if (tau != 0ull) {
-                const float t_score = keyScore(tau);
-                // the h whose score (d - 2h) / d is exactly the threshold's score
-                const float estimate = (static_cast<float>(kDim) - t_score * static_cast<float>(kDim)) * 0.5f;
-                int ht = estimate >= 0.0f && estimate <= static_cast<float>(kDim) ? static_cast<int>(rintf(estimate)) : 0;
-                for (int c = max(0, ht - 2); c <= min(kDim, ht + 2); ++c) {
-                    if (static_cast<float>(kDim - 2 * c) / static_cast<float>(kDim) == t_score) {
-                        ht = c;
-                    }
-                }
-                h_limit[g] = ht;
-                row_limit[g] = 0xFFFFFFFFu - static_cast<std::uint32_t>(tau);
-            }
+            binaryThreshold<kDim>(emit, q, h_limit[g], row_limit[g]);
         }
     }
     // acc threshold of the fast reject (acc = 64 (h - popc(q)); invalid queries never pass)
@@ -363,6 +375,212 @@ void mfmaBinaryScanKernel(ScanArgs scan, PhaseArgs phase, EmitArgs emit, int q_o
     }
 }
 
+
+constexpr int kStreamThreads = 1024;
+constexpr int kStreamWaves = kStreamThreads / kWave;
+
+// One query set (<= 32 queries): the set's B operands sit in LDS, shared by the workgroup's 16
+// wavefronts, and each wavefront streams its own rows from HBM straight into registers, 32 rows
+// (two 16-row blocks) at a time, the next pair loaded while the current one is multiplied. No
+// tile is shared, so there is no LDS ring and no barrier in the loop, and with the queries out of
+// the registers four wavefronts fit a SIMD, whose loads hide each other's latency. Each B
+// fragment read from LDS feeds four MFMAs (two blocks x two query groups). Wavefront w of
+// workgroup b takes pairs b * 16 + w, + 16 * gridDim.x, ... of the phase's items (an item's
+// pairs in order).
+template <int kWords, bool kDense>
+__global__ __launch_bounds__(kStreamThreads)
+void mfmaBinaryStreamKernel(ScanArgs scan, PhaseArgs phase, EmitArgs emit, int q_offset, int q_count) {
+    using Tile = BinaryTile<kWords>;
+    constexpr int kRows = Tile::kRows;
+    constexpr int kRowBytes = Tile::kRowBytes;
+    constexpr int kLaneChunks = Tile::kLaneChunks;
+    constexpr int kSteps = Tile::kSteps;
+    constexpr int kPairs = Tile::kRowBlocks / 2;
+    constexpr int kDim = kWords * 32;
+    static_assert(Tile::kRowBlocks % 2 == 0, "an item splits into 32-row pairs");
+
+    __shared__ v4i qlds[kSteps][2][kWave];  // B operand of (step, query group, lane)
+    __shared__ std::uint32_t lds_count[kSetQueries];
+
+    const int tid = threadIdx.x;
+    const int lane = tid & (kWave - 1);
+    const int wave = tid / kWave;
+    const int r16 = lane & 15;
+    const int h = lane >> 4;
+    const bool two_groups = 16 < q_count;  // launch-uniform
+    const long long doc_count = scan.doc_count;
+    const std::uint8_t* corpus = static_cast<const std::uint8_t*>(scan.corpus);
+    const std::uint32_t* qwords = static_cast<const std::uint32_t*>(scan.queries);
+
+    // B operands: lane l of group g at step t supplies query g * 16 + l % 16, half t % 2 of word
+    // (t % 8) / 2 of its chunk l / 16 + 4 (t / 8) (as the A operand's lanes do for their rows)
+    for (int e = tid; e < kSteps * 2 * kWave; e += kStreamThreads) {
+        const int t = e / (2 * kWave);
+        const int g = (e / kWave) % 2;
+        const int l = e % kWave;
+        const int qlocal = g * 16 + (l & 15);
+        v4i value = {0, 0, 0, 0};
+        if (qlocal < q_count) {
+            const std::uint32_t word = qwords[static_cast<std::size_t>(q_offset + qlocal) * kWords +
+                                              4 * ((l >> 4) + 4 * (t / 8)) + (t % 8) / 2];
+            value = signWord(word, t % 2);
+        }
+        qlds[t][g][l] = value;
+    }
+    for (int i = tid; i < kSetQueries; i += kStreamThreads) {
+        lds_count[i] = 0u;
+    }
+    // this lane's two queries (column r16 of each group's D): popc(q) and the integer threshold
+    int popq[2];
+    int q_of[2];
+    bool valid_of[2];
+    int h_limit[2];
+    std::uint32_t row_limit[2];
+    int acc_limit[2];
+#pragma unroll
+    for (int g = 0; g < 2; ++g) {
+        const int qlocal = g * 16 + r16;
+        valid_of[g] = qlocal < q_count;
+        const int q = q_offset + min(qlocal, q_count - 1);
+        q_of[g] = q;
+        const std::uint32_t* qrow = qwords + static_cast<std::size_t>(q) * kWords;
+        // the four lane groups hold disjoint chunks h + 4 jc of the query
+        int pop = 0;
+#pragma unroll
+        for (int jc = 0; jc < kLaneChunks; ++jc) {
+            const u32x4 words = *reinterpret_cast<const u32x4*>(qrow + 4 * (h + 4 * jc));
+            pop += __popc(words[0]) + __popc(words[1]) + __popc(words[2]) + __popc(words[3]);
+        }
+        pop += waveXor(pop, 16);
+        pop += waveXor(pop, 32);
+        popq[g] = pop;
+        h_limit[g] = kDim + 1;
+        row_limit[g] = 0xFFFFFFFFu;
+        if constexpr (!kDense) {
+            binaryThreshold<kDim>(emit, q, h_limit[g], row_limit[g]);
+        }
+        acc_limit[g] = 64 * (valid_of[g] ? h_limit[g] - popq[g] : -(kDim + 1));
+    }
+    __syncthreads();
+
+    auto emitKeys = [&](const v4i& acc, int g, long long row0, int local0, long long item_) {
+        if (!valid_of[g]) {
+            return;
+        }
+        const int q = q_of[g];
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+            const int local = local0 + 4 * h + i;  // row within the item
+            const long long row = row0 + local;
+            const int hd = (acc[i] >> 6) + popq[g];  // acc is 64 times the +-1 dot, exactly
+            if constexpr (kDense) {
+                std::uint64_t key = 0ull;
+                if (row < doc_count) {
+                    const float score = static_cast<float>(kDim - 2 * hd) / static_cast<float>(kDim);
+                    key = makeKey(score, static_cast<std::uint32_t>(row));
+                }
+                emit.dense[static_cast<std::size_t>(q) * emit.dense_stride + item_ * kRows + local] = key;
+            } else {
+                const std::uint32_t r32 = static_cast<std::uint32_t>(row);
+                const bool pass = hd < h_limit[g] || (hd == h_limit[g] && r32 < row_limit[g]);
+                if (pass && row < doc_count) {
+                    const float score = static_cast<float>(kDim - 2 * hd) / static_cast<float>(kDim);
+                    appendCandidate(emit, lds_count, q, q_offset, scan.batch, makeKey(score, r32));
+                }
+            }
+        }
+    };
+    // rows past the corpus re-read its last row (their keys are never emitted)
+    auto loadPair = [&](long long p, u32x4 (&dst)[2][kLaneChunks]) {
+        const long long it = p / kPairs;
+        const long long row0 = phaseBlock(it, phase.stride, phase.skip) * kRows + 32 * (p % kPairs);
+#pragma unroll
+        for (int b = 0; b < 2; ++b) {
+            const long long row = min(row0 + 16 * b + r16, doc_count - 1);
+            const u32x4* src = reinterpret_cast<const u32x4*>(corpus + static_cast<std::size_t>(row) * kRowBytes);
+#pragma unroll
+            for (int jc = 0; jc < kLaneChunks; ++jc) {
+                dst[b][jc] = __builtin_nontemporal_load(src + h + 4 * jc);
+            }
+        }
+    };
+    auto processPair = [&](const u32x4 (&cur)[2][kLaneChunks], long long p) {
+        v4i acc[2][2] = {};
+        v4i a[2];
+        a[0] = spreadWord(stepWord<kLaneChunks>(cur[0], 0), 0);
+        a[1] = spreadWord(stepWord<kLaneChunks>(cur[1], 0), 0);
+#pragma unroll
+        for (int t = 0; t < kSteps; ++t) {
+            const v4i b0 = qlds[t][0][lane];
+            const v4i b1 = qlds[t][1][lane];
+            acc[0][0] = __builtin_amdgcn_mfma_i32_16x16x64_i8(a[0], b0, acc[0][0], 0, 0, 0);
+            acc[0][1] = __builtin_amdgcn_mfma_i32_16x16x64_i8(a[0], b1, acc[0][1], 0, 0, 0);
+            acc[1][0] = __builtin_amdgcn_mfma_i32_16x16x64_i8(a[1], b0, acc[1][0], 0, 0, 0);
+            acc[1][1] = __builtin_amdgcn_mfma_i32_16x16x64_i8(a[1], b1, acc[1][1], 0, 0, 0);
+            if (t + 1 < kSteps) {
+                a[0] = spreadWord(stepWord<kLaneChunks>(cur[0], t + 1), (t + 1) % 2);
+                a[1] = spreadWord(stepWord<kLaneChunks>(cur[1], t + 1), (t + 1) % 2);
+            }
+            // step by step: the compiler would otherwise hoist every step's B reads up front
+            __builtin_amdgcn_sched_barrier(0);
+        }
+        const long long it = p / kPairs;
+        const long long row0 = phaseBlock(it, phase.stride, phase.skip) * kRows;
+        const int pair_row = 32 * static_cast<int>(p % kPairs);
+#pragma unroll
+        for (int b = 0; b < 2; ++b) {
+            if constexpr (kDense) {
+                emitKeys(acc[b][0], 0, row0, pair_row + 16 * b, it);
+                if (two_groups) {
+                    emitKeys(acc[b][1], 1, row0, pair_row + 16 * b, it);
+                }
+            } else {
+                // fast reject: a key can pass only if acc <= 64 (h_limit - popc(q))
+                const int m0 = min(min(acc[b][0][0], acc[b][0][1]), min(acc[b][0][2], acc[b][0][3]));
+                const int m1 = min(min(acc[b][1][0], acc[b][1][1]), min(acc[b][1][2], acc[b][1][3]));
+                if (__builtin_amdgcn_ballot_w64(m0 <= acc_limit[0] || m1 <= acc_limit[1]) != 0) {
+                    emitKeys(acc[b][0], 0, row0, pair_row + 16 * b, it);
+                    if (two_groups) {
+                        emitKeys(acc[b][1], 1, row0, pair_row + 16 * b, it);
+                    }
+                }
+            }
+        }
+    };
+
+    const long long pairs = phase.items * kPairs;
+    const long long stride = static_cast<long long>(gridDim.x) * kStreamWaves;
+    long long p = static_cast<long long>(blockIdx.x) * kStreamWaves + wave;
+    // ping-pong between two register buffers, so no buffer is copied while its loads are in flight
+    u32x4 buf0[2][kLaneChunks];
+    u32x4 buf1[2][kLaneChunks];
+    if (p < pairs) {
+        loadPair(p, buf0);
+    }
+    while (p < pairs) {
+        if (p + stride < pairs) {
+            loadPair(p + stride, buf1);
+        }
+        processPair(buf0, p);
+        p += stride;
+        if (p >= pairs) {
+            break;
+        }
+        if (p + stride < pairs) {
+            loadPair(p + stride, buf0);
+        }
+        processPair(buf1, p);
+        p += stride;
+    }
+
+    if constexpr (!kDense) {
+        __syncthreads();
+        for (int i = tid; i < q_count; i += kStreamThreads) {
+            emit.seg_count[static_cast<std::size_t>(blockIdx.x) * scan.batch + q_offset + i] = lds_count[i];
+        }
+    }
+}
+
 template <int kWords>
 int launchShape(const ScanArgs& scan, const PhaseArgs& phase, const EmitArgs& emit, int workgroups,
                 hipStream_t stream) {
@@ -370,7 +588,14 @@ int launchShape(const ScanArgs& scan, const PhaseArgs& phase, const EmitArgs& em
     const dim3 grid(static_cast<unsigned>(std::max(1LL, wanted)));
     for (int q0 = 0; q0 < scan.batch; q0 += kQueriesPerLaunch) {
         const int count = std::min(kQueriesPerLaunch, scan.batch - q0);
-        if (phase.dense) {
+        if (count <= kSetQueries) {
+            // one query set: the streaming kernel
+            if (phase.dense) {
+                mfmaBinaryStreamKernel<kWords, true><<<grid, kStreamThreads, 0, stream>>>(scan, phase, emit, q0, count);
+            } else {
+                mfmaBinaryStreamKernel<kWords, false><<<grid, kStreamThreads, 0, stream>>>(scan, phase, emit, q0, count);
+            }
+        } else if (phase.dense) {
             mfmaBinaryScanKernel<kWords, true><<<grid, kThreads, 0, stream>>>(scan, phase, emit, q0, count);
         } else {
             mfmaBinaryScanKernel<kWords, false><<<grid, kThreads, 0, stream>>>(scan, phase, emit, q0, count);
