@@ -107,6 +107,10 @@ def test_fused_i8i8_mask(gpu):
 @pytest.mark.parametrize("n,dim,batch,k", [
     (200_000, 1024, 32, 1000),  # binary configuration shape: massive ties at the top-1000 cut
     (100_000, 384, 3, 10),
+    (60_000, 1024, 100, 50),    # more than 32 queries per launch: shared-tile kernel, last set partial
+    (80_000, 512, 17, 20),      # one query set, second group of 16 holds a single query
+    (50_000, 512, 64, 10),      # 512 dims, two query sets
+    (70_000, 1024, 16, 100),    # one query group
 ])
 def test_fused_hamming_bit_exact(gpu, n, dim, batch, k):
     capi = gpu
