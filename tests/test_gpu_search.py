@@ -111,6 +111,7 @@ def test_fused_i8i8_mask(gpu):
     (80_000, 512, 17, 20),      # one query set, second group of 16 holds a single query
     (50_000, 512, 64, 10),      # 512 dims, two query sets
     (70_000, 1024, 16, 100),    # one query group
+    (12_000, 1024, 8, 500),     # few blocks per threshold phase, wide selection: small segments
 ])
 def test_fused_hamming_bit_exact(gpu, n, dim, batch, k):
     capi = gpu

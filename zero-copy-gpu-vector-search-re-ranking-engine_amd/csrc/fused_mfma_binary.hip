@@ -385,8 +385,8 @@ constexpr int kStreamWaves = kStreamThreads / kWave;
 // tile is shared, so there is no LDS ring and no barrier in the loop, and with the queries out of
 // the registers four wavefronts fit a SIMD, whose loads hide each other's latency. Each B
 // fragment read from LDS feeds four MFMAs (two blocks x two query groups). Wavefront w of
-// workgroup b takes pairs b * 16 + w, + 16 * gridDim.x, ... of the phase's items (an item's
-// pairs in order).
+// workgroup b takes pairs w * gridDim.x + b, + 16 * gridDim.x, ... of the phase's items (an
+// item's pairs in order), so the pairs spread over the workgroups first.
 template <int kWords, bool kDense>
 __global__ __launch_bounds__(kStreamThreads)
 void mfmaBinaryStreamKernel(ScanArgs scan, PhaseArgs phase, EmitArgs emit, int q_offset, int q_count) {
@@ -550,7 +550,8 @@ void mfmaBinaryStreamKernel(ScanArgs scan, PhaseArgs phase, EmitArgs emit, int q
 
     const long long pairs = phase.items * kPairs;
     const long long stride = static_cast<long long>(gridDim.x) * kStreamWaves;
-    long long p = static_cast<long long>(blockIdx.x) * kStreamWaves + wave;
+    // workgroup-first: with few pairs every workgroup (candidate segment) still gets its share
+    long long p = static_cast<long long>(wave) * gridDim.x + blockIdx.x;
     // ping-pong between two register buffers, so no buffer is copied while its loads are in flight
     u32x4 buf0[2][kLaneChunks];
     u32x4 buf1[2][kLaneChunks];
