@@ -54,6 +54,8 @@ WORKLOADS = {
                        name="float16 1M x 384, batch 64, k=10"),
     "binary-50m": dict(kind="binary", n=50_000_000, dim=1024, batch=32, k=10, candidates=1000,
                        name="binary 50M x 1024 + float16 rescore of 1000, batch 32, k=10"),
+    "binary-50m-b1": dict(kind="binary", n=50_000_000, dim=1024, batch=1, k=10, candidates=1000,
+                          name="binary 50M x 1024 + float16 rescore of 1000, batch 1, k=10"),
     "hybrid-1m": dict(kind="hybrid", n=1_000_000, dim=384, batch=16, k=10, vocab=30_000, terms=8,
                       dense_weight=0.5,
                       name="hybrid BM25 (V=30,000, 8-term queries) + float16 1M x 384 cosine, batch 16, k=10"),

@@ -22,6 +22,9 @@ constexpr int kKindBinary = ZCGVS_DTYPE_BINARY;
 constexpr int kKindI8I8 = 4;
 
 constexpr int kMaxChunksPerLane = 8;
+// At least 8 lanes (128 contiguous bytes) per row: with one lane per short row (binary, small
+// int8) every load instruction of a wavefront touched 64 cache lines for 16 bytes each.
+constexpr int kMinRowLanes = 8;
 constexpr std::size_t kValuQueryLds = 60 * 1024;
 
 int kindOf(const ScanArgs& scan) {
@@ -299,10 +302,12 @@ void launchKind(int lanes, dim3 grid, std::size_t shared, hipStream_t stream, co
 ValuShape valuShape(const ScanArgs& scan) {
     ValuShape shape;
     const int chunks = chunksOf(scan);
-    shape.lanes = lanesPerRow(chunks, kMaxChunksPerLane);
+    shape.lanes = lanesPerRow(chunks, kMaxChunksPerLane, kMinRowLanes);
     const int rows_per_iter = (kScanThreads / kWave) * (kWave / shape.lanes);
     shape.block_rows = rows_per_iter * std::max(1, 64 / rows_per_iter);
-    shape.workgroups = deviceComputeUnits() * 4;
+    // 8 workgroups (32 wavefronts) per CU: the kernels of short rows fit 7 wavefronts per SIMD,
+    // whose extra loads in flight were worth 6% on binary rows; the rest queue behind them
+    shape.workgroups = deviceComputeUnits() * 8;
     const int kind = kindOf(scan);
     const std::size_t per_query = queryStageBytes(kind, chunks) + 8 + 4 + 4 + 4;
     int group = static_cast<int>(kValuQueryLds / per_query);
@@ -322,7 +327,7 @@ bool valuSupported(const ScanArgs& scan) {
         return false;
     }
     const int chunks = static_cast<int>(bytes / 16);
-    const int lanes = lanesPerRow(chunks, kMaxChunksPerLane);
+    const int lanes = lanesPerRow(chunks, kMaxChunksPerLane, kMinRowLanes);
     return (chunks + lanes - 1) / lanes <= kMaxChunksPerLane;
 }
 

@@ -152,10 +152,11 @@ __device__ __forceinline__ T groupSum(T value) {
 }
 
 // Lanes per row for a row of `chunks` 16-byte chunks: the smallest power of two giving each
-// lane at most `per_lane` chunks, capped at a full wavefront.
-inline int lanesPerRow(int chunks, int per_lane = 4) {
+// lane at most `per_lane` chunks, capped at a full wavefront, and at least min_lanes (or as
+// many as the row has chunks), so one load instruction reads whole cache lines of a row.
+inline int lanesPerRow(int chunks, int per_lane = 4, int min_lanes = 1) {
     int lanes = 1;
-    while (lanes < kWave && (chunks + lanes - 1) / lanes > per_lane) {
+    while (lanes < kWave && ((chunks + lanes - 1) / lanes > per_lane || (lanes < min_lanes && lanes < chunks))) {
         lanes <<= 1;
     }
     return lanes;
