@@ -22,6 +22,16 @@ constexpr int kKindBinary = ZCGVS_DTYPE_BINARY;
 constexpr int kKindI8I8 = 4;
 
 constexpr int kMaxChunksPerLane = 8;
+// Binary rows are short (at most 16 chunks): a lane holds at most 2 of a row's chunks, and the
+// loads of kBinarySets rows per lane are issued before any of them is scored, so a wavefront keeps
+// as many bytes in flight as on the longer float rows.
+constexpr int kBinaryChunksPerLane = 2;
+constexpr int kBinarySets = 4;
+
+__host__ __device__ constexpr int chunksPerLaneOf(int kind) {
+    return kind == ZCGVS_DTYPE_BINARY ? kBinaryChunksPerLane : kMaxChunksPerLane;
+}
+__host__ __device__ constexpr int rowSetsOf(int kind) { return kind == ZCGVS_DTYPE_BINARY ? kBinarySets : 1; }
 // At least 8 lanes (128 contiguous bytes) per row: with one lane per short row (binary, small
 // int8) every load instruction of a wavefront touched 64 cache lines for 16 bytes each.
 constexpr int kMinRowLanes = 8;
@@ -126,25 +136,36 @@ __global__ __launch_bounds__(kScanThreads) void valuScanKernel(ScanArgs scan, Ph
     const long long doc_count = scan.doc_count;
     const std::uint8_t* corpus = static_cast<const std::uint8_t*>(scan.corpus);
 
+    constexpr int kPerLane = chunksPerLaneOf(kKind);
+    constexpr int kSets = rowSetsOf(kKind);
     for (long long item = blockIdx.x; item < phase.items; item += gridDim.x) {
         const long long row0 = phaseBlock(item, phase.stride, phase.skip) * phase.block_rows;
-        for (int it = 0; it < iters; ++it) {
-            const int local = it * kRowsPerIter + wave * kRowsPerWave + lane / L;
+        for (int it0 = 0; it0 < iters; it0 += kSets) {
+            // the loads of kSets row sets first (iters is a multiple of kSets)
+            uint4 raws[kSets][kPerLane];
+#pragma unroll
+            for (int set = 0; set < kSets; ++set) {
+                const int local = (it0 + set) * kRowsPerIter + wave * kRowsPerWave + lane / L;
+                const long long row = row0 + local;
+                const bool live = row < doc_count && !(scan.mask != nullptr && scan.mask[row] == 0);
+#pragma unroll
+                for (int t = 0; t < kPerLane; ++t) {
+                    const int c = group + t * L;
+                    raws[set][t] = make_uint4(0u, 0u, 0u, 0u);
+                    if (live && c < chunks) {
+                        raws[set][t] = loadChunkStreaming(corpus + static_cast<std::size_t>(row) * row_bytes +
+                                                          static_cast<std::size_t>(c) * 16);
+                    }
+                }
+            }
+#pragma unroll
+            for (int set = 0; set < kSets; ++set) {
+            const int local = (it0 + set) * kRowsPerIter + wave * kRowsPerWave + lane / L;
             const long long row = row0 + local;
             const bool valid = row < doc_count;
             const bool masked = valid && scan.mask != nullptr && scan.mask[row] == 0;
             const bool live = valid && !masked;
-
-            uint4 raw[kMaxChunksPerLane];
-#pragma unroll
-            for (int t = 0; t < kMaxChunksPerLane; ++t) {
-                const int c = group + t * L;
-                raw[t] = make_uint4(0u, 0u, 0u, 0u);
-                if (live && c < chunks) {
-                    raw[t] = loadChunkStreaming(corpus + static_cast<std::size_t>(row) * row_bytes +
-                                                static_cast<std::size_t>(c) * 16);
-                }
-            }
+            const uint4 (&raw)[kPerLane] = raws[set];
             float row_scale = 1.0f;
             if constexpr (kKind == kKindI8I8) {
                 row_scale = live ? scan.row_scales[row] : 0.0f;
@@ -160,7 +181,7 @@ __global__ __launch_bounds__(kScanThreads) void valuScanKernel(ScanArgs scan, Ph
                         acc[q] = 0;
                     }
 #pragma unroll
-                    for (int t = 0; t < kMaxChunksPerLane; ++t) {
+                    for (int t = 0; t < kPerLane; ++t) {
                         const int c = group + t * L;
                         if (c < chunks) {
 #pragma unroll
@@ -205,7 +226,7 @@ __global__ __launch_bounds__(kScanThreads) void valuScanKernel(ScanArgs scan, Ph
                     }
                     const float* fstaged = reinterpret_cast<const float*>(staged);
 #pragma unroll
-                    for (int t = 0; t < kMaxChunksPerLane; ++t) {
+                    for (int t = 0; t < kPerLane; ++t) {
                         const int c = group + t * L;
                         if (c < chunks) {
                             float v[E];
@@ -262,6 +283,7 @@ __global__ __launch_bounds__(kScanThreads) void valuScanKernel(ScanArgs scan, Ph
                     }
                 }
             }
+            }
         }
     }
     if (!phase.dense) {
@@ -302,14 +324,14 @@ void launchKind(int lanes, dim3 grid, std::size_t shared, hipStream_t stream, co
 ValuShape valuShape(const ScanArgs& scan) {
     ValuShape shape;
     const int chunks = chunksOf(scan);
-    shape.lanes = lanesPerRow(chunks, kMaxChunksPerLane, kMinRowLanes);
+    const int kind_of = kindOf(scan);
+    shape.lanes = lanesPerRow(chunks, chunksPerLaneOf(kind_of), kMinRowLanes);
     const int rows_per_iter = (kScanThreads / kWave) * (kWave / shape.lanes);
-    shape.block_rows = rows_per_iter * std::max(1, 64 / rows_per_iter);
+    shape.block_rows = rows_per_iter * std::max(rowSetsOf(kind_of), 64 / rows_per_iter);
     // 8 workgroups (32 wavefronts) per CU: the kernels of short rows fit 7 wavefronts per SIMD,
     // whose extra loads in flight were worth 6% on binary rows; the rest queue behind them
     shape.workgroups = deviceComputeUnits() * 8;
-    const int kind = kindOf(scan);
-    const std::size_t per_query = queryStageBytes(kind, chunks) + 8 + 4 + 4 + 4;
+    const std::size_t per_query = queryStageBytes(kind_of, chunks) + 8 + 4 + 4 + 4;
     int group = static_cast<int>(kValuQueryLds / per_query);
     group = std::max(1, std::min(group, scan.batch));
     if (group < scan.batch && group >= kQueryTile) {
@@ -327,8 +349,9 @@ bool valuSupported(const ScanArgs& scan) {
         return false;
     }
     const int chunks = static_cast<int>(bytes / 16);
-    const int lanes = lanesPerRow(chunks, kMaxChunksPerLane, kMinRowLanes);
-    return (chunks + lanes - 1) / lanes <= kMaxChunksPerLane;
+    const int per_lane = chunksPerLaneOf(kindOf(scan));
+    const int lanes = lanesPerRow(chunks, per_lane, kMinRowLanes);
+    return (chunks + lanes - 1) / lanes <= per_lane;
 }
 
 int launchValuScan(const ScanArgs& scan, const PhaseArgs& phase, const EmitArgs& emit,
