@@ -587,9 +587,12 @@ int searchTopk(const zcgvs_search_desc* desc, void* d_workspace, std::size_t wor
         const long long n = d.corpus.doc_count;
         const long long padded = (n + kMfmaBlockRows - 1) / kMfmaBlockRows * kMfmaBlockRows;
         if (plan.direct_scales) {
-            mergeMaskedScalesKernel<<<1, kMfmaBlockRows, 0, s>>>(d.corpus.row_scales, nullptr, n,
-                                                                 padded - kMfmaBlockRows, kMfmaBlockRows,
-                                                                 at<float>(ws, plan.mscales));
+            // the padded scales of a partial last tile (none when the corpus fills whole tiles)
+            if (padded != n) {
+                mergeMaskedScalesKernel<<<1, kMfmaBlockRows, 0, s>>>(d.corpus.row_scales, nullptr, n,
+                                                                     padded - kMfmaBlockRows, kMfmaBlockRows,
+                                                                     at<float>(ws, plan.mscales));
+            }
         } else {
             mergeMaskedScalesKernel<<<static_cast<unsigned>(std::min<long long>(8192, (padded + 255) / 256)), 256, 0, s>>>(
                 d.corpus.row_scales, d.mask, n, 0, padded, at<float>(ws, plan.mscales));
