@@ -1,7 +1,7 @@
 """CPU oracle of the zero-copy search hot path - TEST INFRASTRUCTURE ONLY.
 
 Only tests/, __graft_entry__.smoke() and bench.py's cpu_baseline leg may import this package,
-and only as the checker (or the timed CPU baseline); the product path never calls it.
+and only to check results (or as the timed CPU baseline); the product path never calls it.
 
 `oracle.c` (built to _build/liboracle.so by the Makefile) restates the reference's CPU semantics
 function by function; `ref` gives the reference's own tests/cpp/cpu_reference.hpp compiled from

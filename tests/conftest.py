@@ -38,7 +38,7 @@ def capi():
 
 @pytest.fixture(scope="session")
 def gpu(capi):
-    # A test marked gpu runs on a GPU box; without a device it fails rather than passing vacuously.
+    # A test marked gpu needs a HIP device; without one it fails rather than passing vacuously.
     if capi.device_count() <= 0:
         pytest.fail("no HIP device visible to a test marked gpu")
     return capi
