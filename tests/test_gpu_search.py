@@ -112,6 +112,8 @@ def test_fused_i8i8_mask(gpu):
     (50_000, 512, 64, 10),      # 512 dims, two query sets
     (70_000, 1024, 16, 100),    # one query group
     (12_000, 1024, 8, 500),     # few blocks per threshold phase, wide selection: small segments
+    (300_000, 1024, 1, 100),    # single query: VALU popcount scan, four row sets per lane, several phases
+    (200_000, 512, 2, 50),      # VALU popcount scan, four lanes per 64-byte row
 ])
 def test_fused_hamming_bit_exact(gpu, n, dim, batch, k):
     capi = gpu
