@@ -552,24 +552,23 @@ void mfmaBinaryStreamKernel(ScanArgs scan, PhaseArgs phase, EmitArgs emit, int q
     const long long stride = static_cast<long long>(gridDim.x) * kStreamWaves;
     // workgroup-first: with few pairs every workgroup (candidate segment) still gets its share
     long long p = static_cast<long long>(wave) * gridDim.x + blockIdx.x;
-    // ping-pong between two register buffers, so no buffer is copied while its loads are in flight
+    // Ping-pong between two register buffers, so no buffer is copied while its loads are in flight.
+    // The next pair is loaded unconditionally (past the phase's end, its last pair again): with a
+    // conditional load the loop head would be reached with two different load counts, and the
+    // compiler would then wait for the prefetch halfway through the current pair's products.
     u32x4 buf0[2][kLaneChunks];
     u32x4 buf1[2][kLaneChunks];
     if (p < pairs) {
         loadPair(p, buf0);
     }
     while (p < pairs) {
-        if (p + stride < pairs) {
-            loadPair(p + stride, buf1);
-        }
+        loadPair(min(p + stride, pairs - 1), buf1);
         processPair(buf0, p);
         p += stride;
         if (p >= pairs) {
             break;
         }
-        if (p + stride < pairs) {
-            loadPair(p + stride, buf0);
-        }
+        loadPair(min(p + stride, pairs - 1), buf0);
         processPair(buf1, p);
         p += stride;
     }
