@@ -223,6 +223,51 @@ def cpu_baseline(capi, w, corpus, keep, queries, gpu_idx, gpu_val, budget_s):
     return baseline, parity
 
 
+def vendor_yardstick(w, steps: int, warmup: int) -> int:
+    """The fp32 score matrix by the vendor BLAS (torch on ROCm calls rocBLAS / hipBLASLt): the
+    MI355X analog of the reference's cuBLAS backend (src/cuda/cublas_similarity.cpp:42-49, sgemv at
+    batch 1 and sgemm otherwise; fp32, cosine/dot, no mask), timed the way
+    apps/bench_kernels.cu:188-208 times it. A yardstick only: it writes the [batch, N] scores and
+    selects nothing, so it is not a search step and never the bench's value."""
+    import torch
+
+    if w["kind"] != "f32":
+        raise SystemExit("bench.py: --vendor-yardstick takes fp32 workloads only (as the reference's cuBLAS backend)")
+    dev = torch.device("cuda", 0)
+    gen = torch.Generator(device=dev).manual_seed(1)
+    corpus = torch.randn(w["n"], w["dim"], device=dev, generator=gen)
+    corpus /= corpus.norm(dim=1, keepdim=True)
+    queries = torch.randn(w["batch"], w["dim"], device=dev, generator=gen)
+    queries /= queries.norm(dim=1, keepdim=True)
+
+    def step():
+        if w["batch"] == 1:
+            return torch.mv(corpus, queries[0])
+        return torch.mm(queries, corpus.t())
+
+    for _ in range(warmup):
+        step()
+    torch.cuda.synchronize()
+    events = [(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)) for _ in range(steps)]
+    for begin, end in events:
+        begin.record()
+        step()
+        end.record()
+    torch.cuda.synchronize()
+    ms = [begin.elapsed_time(end) for begin, end in events]
+    mean = statistics.mean(ms)
+    moved = w["n"] * w["dim"] * 4 + w["batch"] * w["n"] * 4  # corpus read + scores written
+    print(json.dumps({
+        "metric": "vendor fp32 score matrix (torch -> rocBLAS/hipBLASLt), yardstick only",
+        "value": round(moved / (mean * 1e-3) / 1e9, 1), "unit": "GB/s", "n_gpus": 1, "steps": steps,
+        "warmup": warmup, "ms_per_step": round(mean, 4), "p50_ms": round(statistics.median(ms), 4),
+        "higher_is_better": True, "dtype": "f32", "data": "synthetic (torch.randn rows, L2-normalized)",
+        "config": {"workload": w["name"], "N": w["n"], "dim": w["dim"], "batch": w["batch"],
+                   "op": "sgemv" if w["batch"] == 1 else "sgemm", "output": "[batch, N] fp32 scores, no top-k"},
+    }), flush=True)
+    return 0
+
+
 def main(argv=None) -> int:
     parser = argparse.ArgumentParser(description=__doc__, formatter_class=argparse.RawDescriptionHelpFormatter)
     parser.add_argument("--gpus", type=int, default=1)
@@ -237,12 +282,18 @@ def main(argv=None) -> int:
     parser.add_argument("--graph", action="store_true",
                         help="time replays of one captured HIP graph of the search instead of direct "
                              "calls (the per-phase kernel times still come from direct calls)")
+    parser.add_argument("--vendor-yardstick", action="store_true",
+                        help="time the fp32 [batch, N] score matrix by the vendor BLAS instead (the analog "
+                             "of the reference's cuBLAS backend; fp32 workloads; scores only, no top-k)")
     args = parser.parse_args(argv)
     if args.gpus != 1:
         print(f"bench.py: this build runs on one GPU; --gpus {args.gpus} is not supported "
               "(the corpus would shard by rows, with one gather of batch*k hits per GPU)",
               file=sys.stderr)
         return 2
+
+    if args.vendor_yardstick:
+        return vendor_yardstick(WORKLOADS[args.workload], args.steps, args.warmup)
 
     load_package()
     from zcgvs_amd import capi
