@@ -57,6 +57,8 @@ public:
     bool lastSearchUsedGraph() const { return used_graph_; }
     std::uint64_t graphCaptureCount() const { return graph_captures_; }
     std::uint64_t graphLaunchCount() const { return graph_launches_; }
+    // Queries whose result came from the device's exact fallback (candidate buffers overflowed),
+    // counted when results are copied to the host.
     std::uint64_t exactRecomputeCount() const { return exact_recomputes_; }
 
     bool hasRescoreStore() const { return rescore_store_ != nullptr; }
@@ -90,7 +92,6 @@ private:
     void run(const float* device_queries, int dim, int batch, const SearchParams& params,
              const HipStream& stream);
     void destroyGraph() noexcept;
-    void recomputeExact(int query, const HipStream& stream);
 
     const EmbeddingStore& store_;
     const EmbeddingStore* rescore_store_ = nullptr;
@@ -100,7 +101,6 @@ private:
     DeviceBuffer<float> d_queries_;
     DeviceBuffer<int> d_query_terms_;
     DeviceBuffer<std::uint8_t> d_workspace_;
-    DeviceBuffer<std::uint8_t> d_exact_workspace_;
     DeviceBuffer<int> d_out_indices_;
     DeviceBuffer<float> d_out_values_;
     PinnedBuffer<float> h_queries_;

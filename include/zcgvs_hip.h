@@ -99,6 +99,15 @@ int zcgvs_get_device(int* device);
 int zcgvs_device_query(int device, zcgvs_device_info* out); /* src/core/cuda_context.cpp:23-45 */
 int zcgvs_device_synchronize(void);
 
+/* Measured HBM rates of the current device, the achievable counterpart of peak_bandwidth_gbs
+ * (the reference derives only that nominal peak, include/zcgvs/core/cuda_context.hpp:20-23, and
+ * prints each scan's GB/s against it, apps/bench_kernels.cu:133-143). A streaming read and a
+ * streaming copy over two `bytes`-byte buffers (at least 64 MiB; use several times the 256 MiB
+ * last-level cache) are each timed `iterations` times at a few grid sizes; the best launch gives
+ * *read_gbs (bytes read per second) and *copy_gbs (bytes read + written per second), in 1e9
+ * bytes/s. Allocates, frees and synchronizes: never call it inside a graph capture. */
+int zcgvs_measure_hbm_bandwidth(size_t bytes, int iterations, double* read_gbs, double* copy_gbs);
+
 int zcgvs_malloc(void** ptr, size_t bytes);           /* device_buffer.hpp:40-56 */
 int zcgvs_free(void* ptr);
 int zcgvs_host_alloc(void** ptr, size_t bytes);       /* pinned_buffer.hpp:14-67 */
@@ -186,7 +195,7 @@ int zcgvs_launch_remap_indices(const int* d_candidate_indices, const int* d_loca
                                int candidate_count, int k, int batch, int* d_out_indices,
                                zcgvs_stream_t stream);
 
-/* src/cuda/lexical.cu:227-241 launchBm25. Scatter-adds the posting weights of the query's terms
+/* src/cuda/lexical.cu:78-92 launchBm25. Scatter-adds the posting weights of the query's terms
  * into d_scores (zeroed by the caller). Terms < 0 are skipped, as are documents outside
  * [0, doc_count); term ids must be below the index's vocabulary size, as in the reference.
  * Terms are accumulated in slot order, so every document's sum is formed in the same order on
@@ -202,17 +211,17 @@ int zcgvs_launch_bm25_batched(const int64_t* d_offsets, const int* d_docs,
                               const float* d_weights, const int* d_query_terms, int term_stride,
                               int batch, int doc_count, float* d_scores, zcgvs_stream_t stream);
 
-/* src/cuda/lexical.cu:243-254 launchMaxPositive: *d_max = max(*d_max, max_i values[i]) for
+/* src/cuda/lexical.cu:94-105 launchMaxPositive: *d_max = max(*d_max, max_i values[i]) for
  * values >= 0 (caller zeroes *d_max). */
 int zcgvs_launch_max_positive(const float* d_values, int count, float* d_max,
                               zcgvs_stream_t stream);
 
-/* src/cuda/lexical.cu:256-272 launchFuseScores, in place:
+/* src/cuda/lexical.cu:107-123 launchFuseScores, in place:
  * dense[i] = weight * dense[i] + (1 - weight) * lexical[i] * (max > 0 ? 1/max : 0). */
 int zcgvs_launch_fuse_scores(float* d_dense, const float* d_lexical, const float* d_lexical_max,
                              float weight, int count, zcgvs_stream_t stream);
 
-/* src/cuda/convert.cu:332-368 launchConvertF32ToF16 / launchConvertF32ToI8 / launchPackBinary. */
+/* src/cuda/convert.cu:55-93 launchConvertF32ToF16 / launchConvertF32ToI8 / launchPackBinary. */
 int zcgvs_launch_convert_f32_to_f16(const float* d_src, void* d_dst_half, size_t count,
                                     zcgvs_stream_t stream);
 int zcgvs_launch_convert_f32_to_i8(const float* d_src, void* d_dst_int8, size_t count,
@@ -265,23 +274,38 @@ typedef struct zcgvs_search_desc {
 
 /* zcgvs_search_desc.flags. ZCGVS_SEARCH_MATERIALIZE runs the reference-order pipeline (a
  * [batch, doc_count] score matrix in the workspace, then zcgvs_launch_topk) instead of the fused
- * scan; its workspace is correspondingly larger. It never overflows, so it is the exact
- * recompute for queries zcgvs_search_overflow_flags reports.
- * By default the BM25 stage reads each query term's postings in document-range slices, which
- * needs every term's postings in ascending document order, one per document (as the reference's
- * index builder writes them, python/zcgvs_tools/build_lexical.py:147-163).
- * ZCGVS_SEARCH_UNSORTED_POSTINGS lifts that requirement: the postings are then scattered term
- * slot by term slot, in any order. */
-enum zcgvs_search_flags { ZCGVS_SEARCH_MATERIALIZE = 1, ZCGVS_SEARCH_UNSORTED_POSTINGS = 2 };
+ * scan; its workspace is correspondingly larger.
+ * By default the BM25 stage scatters each query's postings term slot by term slot, which takes
+ * postings in any order, like the reference's launchBm25 (src/cuda/lexical.cu:78-92).
+ * ZCGVS_SEARCH_SORTED_POSTINGS states that every term's postings ascend strictly by document, one
+ * per document (the layout the reference's index builder writes,
+ * python/zcgvs_tools/build_lexical.py:147-163); the stage then reads them in document-range
+ * slices instead, with no atomics and no clearing pass. Scores are bit-identical between the
+ * two forms; with the flag set on postings that break the contract they are undefined.
+ * ZCGVS_SEARCH_UNSORTED_POSTINGS names the default explicitly; setting it together with
+ * ZCGVS_SEARCH_SORTED_POSTINGS is an invalid argument.
+ * ZCGVS_SEARCH_FORCE_EXACT_PASS runs the exact device fallback (see zcgvs_search_topk) for every
+ * query instead of only the ones whose candidate buffers overflowed; for tests and verification.
+ * ZCGVS_SEARCH_TEST_TINY_SEGMENTS gives every candidate segment two slots, so that almost every
+ * query overflows and takes the fallback through its overflow flag; for tests only. */
+enum zcgvs_search_flags {
+    ZCGVS_SEARCH_MATERIALIZE = 1,
+    ZCGVS_SEARCH_UNSORTED_POSTINGS = 2,
+    ZCGVS_SEARCH_SORTED_POSTINGS = 4,
+    ZCGVS_SEARCH_FORCE_EXACT_PASS = 8,
+    ZCGVS_SEARCH_TEST_TINY_SEGMENTS = 16
+};
 
 /* Bytes of device workspace zcgvs_search_topk needs for this descriptor (0 on error). */
 size_t zcgvs_search_workspace_bytes(const zcgvs_search_desc* desc);
 
 /* Runs the fused pipeline. d_out_indices/d_out_values are [batch, k]. The workspace must be
  * zcgvs_search_workspace_bytes(desc) bytes; its contents need no initialization. Capture safe.
- * The pipeline bounds its candidate buffers; for inputs whose score order defeats the bound,
- * the affected queries are flagged in the workspace, and zcgvs_search_overflow reports them
- * after the stream has completed. */
+ * The result is the exact top-k for every input: the scan keeps only candidates above a sampled
+ * threshold in bounded per-workgroup buffers, and a query whose buffers overflowed (a corpus whose
+ * best rows crowd into a few blocks) is recomputed on the device, in the same call and stream,
+ * by an exact fallback that selects over recomputed scores (one workgroup per such query, a few
+ * corpus reads). zcgvs_search_overflow_flags tells which queries took that path. */
 int zcgvs_search_topk(const zcgvs_search_desc* desc, void* d_workspace, size_t workspace_bytes,
                       int* d_out_indices, float* d_out_values, zcgvs_stream_t stream);
 
@@ -301,9 +325,10 @@ int zcgvs_search_topk_profiled(const zcgvs_search_desc* desc, void* d_workspace,
 int zcgvs_search_phase_rows(const zcgvs_search_desc* desc, long long* rows, int max_phases,
                             int* phases);
 
-/* Device address of the [batch] uint32 overflow flags inside a workspace laid out for `desc`
- * (non-zero: that query's result is incomplete and must be recomputed exactly, e.g. with
- * zcgvs_launch_similarity + zcgvs_launch_topk). */
+/* Device address of the [batch] uint32 overflow flags inside a workspace laid out for `desc`,
+ * valid after the stream has completed the search: non-zero when that query's candidate buffers
+ * overflowed and its result came from the exact device fallback (the result is exact either way;
+ * the flags are for monitoring). */
 int zcgvs_search_overflow_flags(const zcgvs_search_desc* desc, void* d_workspace,
                                 uint32_t** d_flags);
 

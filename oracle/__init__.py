@@ -236,3 +236,8 @@ def bm25_weight(doc_count, df, tf, length, average_length, k1=1.2, b=0.75) -> fl
 def threads() -> int:
     """OpenMP threads the parallel score loops use."""
     return int(lib().zo_threads())
+
+
+def set_threads(count: int) -> None:
+    """Thread count of the parallel loops (every result is independent of it)."""
+    lib().zo_set_threads(ctypes.c_int(count))

@@ -474,3 +474,12 @@ int zo_threads(void) {
     return 1;
 #endif
 }
+
+/* Sets the thread count of the OpenMP loops (results do not depend on it). */
+void zo_set_threads(int threads) {
+#ifdef _OPENMP
+    omp_set_num_threads(threads > 0 ? threads : 1);
+#else
+    (void)threads;
+#endif
+}

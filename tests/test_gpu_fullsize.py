@@ -1,6 +1,7 @@
 """Parity at the benchmark configurations' full sizes: 1M x 384 float32/float16 (batch 1 and 64),
-10M x 768 per-vector int8 (batch 256, k=100) and 50M x 1024 binary with a float16 rescore of 1000
-candidates (batch 32, k=10). Inputs are generated on the device at their real shapes by the seeded
+10M x 768 per-vector int8 (batch 256, k=100), 50M x 1024 binary with a float16 rescore of 1000
+candidates (batch 32, k=10) and the 1M-document hybrid BM25 + float16 configuration (batch 16,
+k=10). Inputs are generated on the device at their real shapes by the seeded
 generator the benchmark uses. The CPU oracle checks sampled queries against the whole corpus
 (copied to the host); every query is checked for the properties that hold at any size (ids unique
 and in range, scores sorted, each returned score equal to the oracle's score of that id)."""
@@ -83,18 +84,61 @@ def test_fifty_million_binary_with_fp16_rescore(gpu):
         exact = oracle.rescore(got, host_q[b:b + 1], np.arange(k, dtype=np.int32)[None, :])[0]
         tol = float_tolerance(host_q[b:b + 1], got, oracle.COSINE)[0]
         assert np.all(np.abs(val[b].astype(np.float64) - exact) <= tol), f"query {b}: rescore differs"
-    # sampled queries: Hamming top-1000 over all 50M rows, then the float16 rescore and top-10
+    # sampled queries (8, spread over the batch): the Hamming top-1000 stage alone (the same
+    # search without the rescore, k = 1000) equals the oracle's top-1000 over all 50M rows, ids
+    # and scores bit for bit; then the float16 rescore of those candidates gives the top-10
+    sample = [0, 5, 9, 14, 18, 23, 27, 31]
     qwords = oracle.pack_binary(host_q)
-    for b in (0, 31):
-        cand, _ = oracle.topk(oracle.scores_hamming(words, qwords[b:b + 1], dim), c)
-        rows = rows_of(cand[0])
+    stage1 = capi.search_desc(capi.store_desc(corpus, w["n"], dim, capi.BINARY), queries, w["batch"], c,
+                              capi.COSINE)
+    cand_idx, cand_val, flags = capi.search(stage1)
+    assert not flags.any()
+    ref_cand, ref_cand_val = oracle.topk(oracle.scores_hamming(words, qwords[sample], dim), c)
+    assert np.array_equal(cand_idx[sample], ref_cand), "Hamming top-1000 ids differ from the oracle's"
+    assert np.array_equal(cand_val[sample], ref_cand_val), "Hamming top-1000 scores differ"
+    for i, b in enumerate(sample):
+        cand = ref_cand[i]
+        rows = rows_of(cand)
         rescored = oracle.rescore(rows, host_q[b:b + 1], np.arange(c, dtype=np.int32)[None, :])
         tol = float_tolerance(host_q[b:b + 1], rows, oracle.COSINE)
         ref_local, ref_val = oracle.topk(rescored, k)
-        position = {int(g): i for i, g in enumerate(cand[0])}
+        position = {int(g): j for j, g in enumerate(cand)}
         for r in range(k):
-            g, e = int(idx[b, r]), int(cand[0][ref_local[0, r]])
+            g, e = int(idx[b, r]), int(cand[ref_local[0, r]])
             assert g in position, f"query {b} rank {r}: id {g} is not a Hamming top-{c} candidate"
             if g != e:
                 assert abs(float(rescored[0, position[g]]) - float(ref_val[0, r])) <= (
                     tol[0, position[g]] + tol[0, ref_local[0, r]]), f"query {b} rank {r}: not a near-tie"
+
+
+def test_one_million_hybrid_bm25_fp16(gpu):
+    """The hybrid configuration at its stated size: N = 1,000,000 documents, vocabulary 30,000,
+    Poisson(200) lengths, Zipf(1.1) tokens, 8 distinct Zipf terms per query, BM25 k1 = 1.2,
+    b = 0.75, fp16 d = 384 cosine, fusion weight 0.5, batch 16, k = 10 - the sliced BM25 sweep over
+    sorted postings (about 977 slices, head terms with df near N) against the oracle's BM25,
+    maximum and fusion (src/cuda/lexical.cu:17-74, tests/cuda/test_lexical.cu:71-93), then the
+    same search with the postings scattered (the default, any order), bit-identical."""
+    capi = gpu
+    w = bench.WORKLOADS["hybrid-1m"]
+    n, k, weight = w["n"], w["k"], w["dense_weight"]
+    desc, corpus, queries, keep = bench.build_inputs(capi, w)
+    assert desc.flags == capi.SEARCH_SORTED_POSTINGS
+    idx, val, flags = capi.search(desc)
+    assert not flags.any()
+    _ranked(idx, val, n)
+    index, terms = keep["index"], keep["terms_host"]
+    assert index["offsets"][-1] > 100_000_000 and terms.shape == (w["batch"], 8)
+    desc.flags = 0
+    idx2, val2, flags = capi.search(desc)
+    assert not flags.any()
+    assert np.array_equal(idx, idx2) and np.array_equal(val, val2), "sorted sweep and scatter differ"
+    decoded = corpus.to_host().astype(np.float32)
+    host_q = queries.to_host()
+    dense = oracle.scores_f32(decoded, host_q, oracle.COSINE)
+    fused = np.empty_like(dense)
+    for b in range(w["batch"]):
+        lex = oracle.bm25(index["offsets"], index["posting_docs"], index["posting_weights"], terms[b], n)
+        assert lex.max() > 0.0
+        fused[b] = oracle.fuse(dense[b], lex, oracle.max_positive(lex), weight)
+    tol = np.float32(weight) * float_tolerance(host_q, decoded, oracle.COSINE) + 1e-6
+    assert_topk_equivalent(idx, val, fused, k, tol)

@@ -1,6 +1,6 @@
 """The C++17 host layer (zcgvs_engine: Engine, EmbeddingStore, LexicalIndex over libzcgvs.so) on the
 GPU: artifacts written by the NumPy tools load through the C++ readers and search to the oracle's
-result; graph replay is bit-identical; overflowing queries are recomputed exactly."""
+result; graph replay is bit-identical; a monotone corpus is searched exactly."""
 
 from __future__ import annotations
 
@@ -163,9 +163,11 @@ def test_add_vectors_grows_the_corpus(zc, tmp_path):
     assert [hits[0].doc_id for hits in response.results] == [f"new-{i}" for i in range(5)]
 
 
-def test_overflowing_queries_are_recomputed_exactly(zc, gpu, tmp_path):
-    # Scores rise with the row index, so every later phase finds more candidates than the
-    # segments hold: the fused scan flags the query and the Searcher recomputes it.
+def test_monotone_corpus_is_exact(zc, gpu, tmp_path):
+    # Scores rise with the row index, so each threshold phase's candidates sit together in the
+    # last few blocks: the segments hold a full block each, and a query that still overflowed
+    # would be recomputed by the device's exact fallback. Either way the result is exact, through
+    # the C ABI and through the Engine.
     capi = gpu
     n, dim, k = 200_000, 64, 10
     theta = (np.pi / 2) * (n - np.arange(n, dtype=np.float64)) / n
@@ -175,17 +177,15 @@ def test_overflowing_queries_are_recomputed_exactly(zc, gpu, tmp_path):
     query = np.zeros((1, dim), dtype=np.float32)
     query[0, 0] = 1.0
     d_corpus, d_query = capi.DeviceArray.from_host(corpus), capi.DeviceArray.from_host(query)
-    desc = capi.search_desc(capi.store_desc(d_corpus, n, dim, capi.F32), d_query, 1, k)
-    _, _, flags = capi.search(desc)
-    assert flags.any(), "the monotone corpus should overflow the fused scan's segments"
-    exact_desc = capi.search_desc(capi.store_desc(d_corpus, n, dim, capi.F32), d_query, 1, k,
-                                  flags=capi.SEARCH_MATERIALIZE)
-    idx, val, exact_flags = capi.search(exact_desc)
-    assert not exact_flags.any()
     # q = e0 makes every score exactly x_r0 in any summation order, so the comparison is exact;
     # the last ~31 rows round to cos = 1.0f and tie, and ties go to the lowest index
     ref = oracle.scores_f32(corpus, query)
-    assert_topk_equivalent(idx, val, ref, k)
+    for flags in (0, capi.SEARCH_TEST_TINY_SEGMENTS, capi.SEARCH_MATERIALIZE):
+        desc = capi.search_desc(capi.store_desc(d_corpus, n, dim, capi.F32), d_query, 1, k, flags=flags)
+        idx, val, overflow = capi.search(desc)
+        assert_topk_equivalent(idx, val, ref, k)
+        if flags == capi.SEARCH_TEST_TINY_SEGMENTS:
+            assert overflow.any()
     engine = _engine(zc, tmp_path, corpus)
     got_ids, got_scores = _ids_scores(engine.search_vectors(query, _options(zc, engine, k)))
     assert_topk_equivalent(got_ids, got_scores, ref, k)

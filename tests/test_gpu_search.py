@@ -12,6 +12,7 @@ import pytest
 
 import oracle
 from helpers import assert_scores_close, assert_topk_equivalent, float_tolerance, normalized
+from zcgvs_tools import lexical
 
 pytestmark = pytest.mark.gpu
 
@@ -190,25 +191,13 @@ def test_rescore_binary_to_f16(gpu):
 
 
 def zipf_lexical_index(n, vocab, seed):
-    """Synthetic BM25 index: doc length ~ Poisson(200), terms ~ Zipf(1.1) over ranks 1..V."""
-    rng = np.random.default_rng(seed)
-    lengths = np.maximum(rng.poisson(200, size=n), 1)
+    """Synthetic BM25 index of the hybrid configuration's token model: doc length ~ Poisson(200),
+    i.i.d. tokens ~ Zipf(1.1) over ranks 1..V (zcgvs_tools.lexical.synthetic_index, which the
+    CPU tests check against the list-based builder and the oracle's BM25 weight)."""
+    index = lexical.synthetic_index(n, vocab, seed=seed)
     p = 1.0 / np.arange(1, vocab + 1) ** 1.1
     p /= p.sum()
-    tokens = rng.choice(vocab, size=int(lengths.sum()), p=p).astype(np.int64)
-    doc_of = np.repeat(np.arange(n, dtype=np.int64), lengths)
-    pair = np.unique(tokens * n + doc_of, return_counts=True)
-    terms, docs = pair[0] // n, pair[0] % n
-    tf = pair[1]
-    df = np.bincount(terms, minlength=vocab)
-    avg = float(lengths.mean())
-    k1, b = 1.2, 0.75
-    norm = k1 * (1.0 - b + b * lengths[docs] / avg)
-    idf = np.log(1.0 + (n - df[terms] + 0.5) / (df[terms] + 0.5))
-    weights = (idf * (tf * (k1 + 1.0)) / (tf + norm)).astype(np.float32)
-    offsets = np.zeros(vocab + 1, np.int64)
-    offsets[1:] = np.cumsum(df)
-    return offsets, docs.astype(np.int32), weights, p
+    return index["offsets"], index["posting_docs"], index["posting_weights"], p
 
 
 def test_hybrid_bm25_fused(gpu):
@@ -238,10 +227,10 @@ def test_hybrid_bm25_fused(gpu):
 
 
 def test_hybrid_sweep_matches_unsorted_scatter(gpu):
-    # The default BM25 stage reads document-range slices of sorted postings; with
-    # SEARCH_UNSORTED_POSTINGS the postings are scattered slot by slot in any order. Both add a
-    # document's weights in slot order, so a shuffled copy of the index gives bit-identical
-    # results. Term lists padded with -1 and an out-of-vocabulary id are skipped by both.
+    # With SEARCH_SORTED_POSTINGS the BM25 stage reads document-range slices of sorted postings;
+    # by default the postings are scattered slot by slot in any order. Both add a document's
+    # weights in slot order, so a shuffled copy of the index gives bit-identical results. Term
+    # lists padded with -1 and an out-of-vocabulary id are skipped by both.
     capi = gpu
     n, vocab, dim, batch, k, w = 70_001, 30_000, 384, 12, 10, 0.25
     offsets, docs, weights, p = zipf_lexical_index(n, vocab, 21)
@@ -259,8 +248,8 @@ def test_hybrid_sweep_matches_unsorted_scatter(gpu):
     queries = normalized(batch, dim, 24)
     d_half = capi.DeviceArray.from_host(half)
     results = []
-    for doc_array, weight_array, flags in ((docs, weights, 0),
-                                           (shuffled_docs, shuffled_weights, capi.SEARCH_UNSORTED_POSTINGS)):
+    for doc_array, weight_array, flags in ((docs, weights, capi.SEARCH_SORTED_POSTINGS),
+                                           (shuffled_docs, shuffled_weights, 0)):
         results.append(run_search(capi, d_half, n, dim, capi.F16, queries, k,
                                   lex_offsets=capi.DeviceArray.from_host(offsets),
                                   lex_docs=capi.DeviceArray.from_host(doc_array),
@@ -278,6 +267,17 @@ def test_hybrid_sweep_matches_unsorted_scatter(gpu):
         fused[b] = oracle.fuse(dense[b], lex, oracle.max_positive(lex), w)
     tol = np.float32(w) * float_tolerance(queries, decoded, 0) + 1e-6
     assert_topk_equivalent(results[0][0], results[0][1], fused, k, tol)
+
+
+def test_postings_cannot_be_both_sorted_and_unsorted(gpu):
+    capi = gpu
+    store = capi.store_desc(1 << 20, 5000, 64, capi.F16)
+    desc = capi.search_desc(store, 1 << 20, 2, 10, lex_offsets=1 << 20, lex_docs=1 << 20,
+                            lex_weights=1 << 20, lex_doc_count=5000, lex_vocab_size=10,
+                            query_terms=1 << 20, lexical_stride=4,
+                            flags=capi.SEARCH_SORTED_POSTINGS | capi.SEARCH_UNSORTED_POSTINGS)
+    with pytest.raises(ValueError, match="both sorted and unsorted"):
+        capi.search_workspace_bytes(desc)
 
 
 @pytest.mark.parametrize("bad,match", [

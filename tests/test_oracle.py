@@ -41,12 +41,18 @@ def test_pack_binary_zero_sign_and_nan():
 
 # ---- the reference's own CPU path -----------------------------------------------------------
 
-ref = oracle.ref()
-needs_ref = pytest.mark.skipif(ref is None, reason="reference CPU path was not built here")
+# Loaded by the tests that use it (never at collection), so a run that selects none of them
+# does not map the library.
+needs_ref = pytest.mark.skipif(not oracle.REF_PATH.exists(), reason="reference CPU path was not built here")
+
+
+@pytest.fixture(scope="module")
+def ref():
+    return oracle.ref()
 
 
 @needs_ref
-def test_scores_match_reference_cpu_bitwise():
+def test_scores_match_reference_cpu_bitwise(ref):
     import ctypes
     corpus = normalized(512, 384)
     query = normalized(1, 384)
@@ -59,7 +65,7 @@ def test_scores_match_reference_cpu_bitwise():
 
 @needs_ref
 @pytest.mark.parametrize("quantized", [False, True])
-def test_topk_matches_reference_stable_sort(quantized):
+def test_topk_matches_reference_stable_sort(ref, quantized):
     import ctypes
     scores = RNG.uniform(-100, 100, size=5000).astype(np.float32)
     if quantized:  # heavy ties: only 41 distinct values
@@ -74,7 +80,7 @@ def test_topk_matches_reference_stable_sort(quantized):
 
 
 @needs_ref
-def test_quantize_dequantize_matches_reference():
+def test_quantize_dequantize_matches_reference(ref):
     import ctypes
     x = RNG.standard_normal(4096).astype(np.float32)
     # include exact half-way points: (n + 0.5) * scale
@@ -88,7 +94,7 @@ def test_quantize_dequantize_matches_reference():
 
 
 @needs_ref
-def test_pack_and_hamming_match_reference():
+def test_pack_and_hamming_match_reference(ref):
     import ctypes
     x = RNG.standard_normal((64, 100)).astype(np.float32)
     expected = np.empty((64, 4), dtype=np.uint32)
@@ -102,7 +108,7 @@ def test_pack_and_hamming_match_reference():
 
 
 @needs_ref
-def test_l2_normalize_matches_reference():
+def test_l2_normalize_matches_reference(ref):
     import ctypes
     x = RNG.standard_normal((4, 97)).astype(np.float32)
     got = oracle.l2_normalize(x)
@@ -210,12 +216,40 @@ def test_topk_pads_when_k_exceeds_n():
     assert val[0, 2] == -np.finfo(np.float32).max
 
 
-def test_bm25_weight_formula():
-    for df, tf, length in [(1, 1, 200), (5000, 3, 150), (999999, 12, 400)]:
-        n, avg, k1, b = 1_000_000, 201.5, 1.2, 0.75
-        idf = math.log(1.0 + (n - df + 0.5) / (df + 0.5))
-        expected = np.float32(idf * (tf * (k1 + 1.0)) / (tf + k1 * (1.0 - b + b * length / avg)))
-        assert oracle.bm25_weight(n, df, tf, length, avg, k1, b) == expected
+def test_bm25_weight_pinned_by_its_special_cases():
+    """python/zcgvs_tools/build_lexical.py:143-154: w = idf * tf (k1 + 1) / (tf + k1 (1 - b +
+    b len / avgdl)), idf = ln(1 + (N - df + 0.5) / (df + 0.5)), in float64, cast to float32.
+    Each check below is fixed by the mathematics, not by the formula's text: a dropped term, a
+    swapped operand or a wrong constant fails one of them."""
+    n, avg = 1_000_000, 201.5
+    w = oracle.bm25_weight
+    # a term absent from the document contributes nothing
+    assert w(n, 10, 0, 150, avg) == 0.0
+    # idf alone, from the three closed forms below (k1 = 0 removes the saturation factor)
+    for df in (1, 17, 5000, n // 2, n):
+        idf = math.log1p((n - df + 0.5) / (df + 0.5))
+        for tf in (1, 2, 4, 64):
+            assert w(n, df, tf, 123, avg, k1=0.0) == np.float32(idf)
+    # a term in every document keeps only the +0.5 smoothing: idf = ln(1 + 0.5 / (N + 0.5))
+    assert w(n, n, 1, 100, avg, k1=0.0) == np.float32(math.log1p(0.5 / (n + 0.5)))
+    # one document holding the term out of two: idf = ln(1 + 1.5 / 1.5) = ln 2
+    assert w(2, 1, 1, 5, 5, k1=0.0) == np.float32(math.log(2.0))
+    # b = 0 makes the weight independent of the document length
+    base = w(n, 300, 3, 10, avg, b=0.0)
+    assert all(w(n, 300, 3, length, avg, b=0.0) == base for length in (1, 200, 5000))
+    # at length == avgdl the length factor is 1 for every b: tf (k1 + 1) / (tf + k1)
+    idf = math.log1p((n - 300 + 0.5) / (300 + 0.5))
+    for b in (0.0, 0.3, 0.75, 1.0):
+        assert w(n, 300, 2, avg, avg, b=b) == np.float32(idf * 2 * 2.2 / (2 + 1.2))
+    # strictly increasing in tf, bounded by (and tending to) idf * (k1 + 1)
+    series = [w(n, 300, tf, 180, avg) for tf in (1, 2, 3, 5, 10, 100, 10_000, 10**8)]
+    assert all(a < b for a, b in zip(series, series[1:-1]))
+    assert series[-1] <= np.float32(idf * 2.2) and abs(series[-1] - idf * 2.2) < 1e-6 * idf
+    # longer documents weigh less (b > 0), rarer terms weigh more
+    assert w(n, 300, 3, 100, avg) > w(n, 300, 3, 400, avg)
+    assert w(n, 30, 3, 100, avg) > w(n, 300, 3, 100, avg) > w(n, 3000, 3, 100, avg)
+    # doubling the length and avgdl together changes nothing
+    assert w(n, 300, 3, 150, avg) == w(n, 300, 3, 300, 2 * avg)
 
 
 def test_bm25_accumulates_in_term_order():

@@ -22,6 +22,9 @@ F32, F16, I8, BINARY = 0, 1, 2, 3
 INT8_REFERENCE, INT8_PER_VECTOR = 0, 1
 SEARCH_MATERIALIZE = 1
 SEARCH_UNSORTED_POSTINGS = 2
+SEARCH_SORTED_POSTINGS = 4
+SEARCH_FORCE_EXACT_PASS = 8
+SEARCH_TEST_TINY_SEGMENTS = 16
 
 _vp = ctypes.c_void_p
 _i32 = ctypes.c_int
@@ -60,6 +63,7 @@ _SIGNATURES = {
     "zcgvs_get_device": (_i32, [ctypes.POINTER(_i32)]),
     "zcgvs_device_query": (_i32, [_i32, ctypes.POINTER(DeviceInfo)]),
     "zcgvs_device_synchronize": (_i32, []),
+    "zcgvs_measure_hbm_bandwidth": (_i32, [_sz, _i32, ctypes.POINTER(ctypes.c_double), ctypes.POINTER(ctypes.c_double)]),
     "zcgvs_malloc": (_i32, [ctypes.POINTER(_vp), _sz]),
     "zcgvs_free": (_i32, [_vp]),
     "zcgvs_host_alloc": (_i32, [ctypes.POINTER(_vp), _sz]),
@@ -219,6 +223,13 @@ def device_info(device: int = 0) -> DeviceInfo:
     info = DeviceInfo()
     call("zcgvs_device_query", device, ctypes.byref(info))
     return info
+
+
+def measure_hbm_bandwidth(nbytes: int = 4 << 30, iterations: int = 5) -> tuple[float, float]:
+    """(read GB/s, copy GB/s) of the current device, measured by streaming kernels."""
+    read, copy = ctypes.c_double(0.0), ctypes.c_double(0.0)
+    call("zcgvs_measure_hbm_bandwidth", nbytes, iterations, ctypes.byref(read), ctypes.byref(copy))
+    return read.value, copy.value
 
 
 class Stream:

@@ -1,4 +1,4 @@
-// Index-side conversions (src/cuda/convert.cu:17-53, 332-368), the per-row int8 quantizer of the
+// Index-side conversions (src/cuda/convert.cu:17-53, 55-93), the per-row int8 quantizer of the
 // per-vector mode, and the on-device synthetic generator.
 #include <hip/hip_fp16.h>
 #include <hip/hip_runtime.h>

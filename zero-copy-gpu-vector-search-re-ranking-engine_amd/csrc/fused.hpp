@@ -136,4 +136,19 @@ int mfmaBinaryBlockRows(const ScanArgs& scan);
 int launchMfmaBinaryScan(const ScanArgs& scan, const PhaseArgs& phase, const EmitArgs& emit,
                          int workgroups, hipStream_t stream);
 
+// Exact device fallback (recover.hip): the top-`width` of every query whose flag is set (every
+// query with `force`) over the whole corpus, written sorted to out_keys [batch, width] and, when
+// out_index is set, as (index, score) pairs [batch, width]. The scan arguments are the VALU
+// scan's: original row scales and allow-mask, device-prepared queries, lexical scores.
+struct RecoverArgs {
+    const std::uint32_t* flags = nullptr;
+    bool force = false;
+    int width = 0;
+    std::uint64_t* out_keys = nullptr;
+    int* out_index = nullptr;
+    float* out_score = nullptr;
+};
+bool recoverSupported(const ScanArgs& scan);
+int launchRecover(const ScanArgs& scan, const RecoverArgs& args, hipStream_t stream);
+
 }  // namespace zcgvs_hip

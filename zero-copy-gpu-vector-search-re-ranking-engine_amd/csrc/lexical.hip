@@ -1,6 +1,6 @@
-// Hybrid lexical stage: BM25 over CSR postings (src/cuda/lexical.cu:17-42, 227-241), the
-// per-query positive maximum (lexical.cu:44-65, 243-254) and the convex fusion with the dense
-// score (lexical.cu:67-74, 256-272).
+// Hybrid lexical stage: BM25 over CSR postings (src/cuda/lexical.cu:17-42, 78-92), the
+// per-query positive maximum (lexical.cu:44-65, 94-105) and the convex fusion with the dense
+// score (lexical.cu:67-74, 107-123).
 //
 // Determinism. The reference launches one block per query term and scatter-adds with float
 // atomics, so a document hit by several terms sums them in a run-dependent order. Here the term
@@ -202,7 +202,9 @@ __global__ __launch_bounds__(kSweepThreads) void bm25SweepKernel(
                         }
                     }
                     // More than kSweepDocs postings in one slice can only come from repeated
-                    // documents (outside the sorted-index contract); they are still all added.
+                    // documents, which the sorted-postings contract excludes: their additions
+                    // race with the plain adds above, so such an index gives undefined sums
+                    // (the caller states the contract with ZCGVS_SEARCH_SORTED_POSTINGS).
                     for (std::int64_t p = begin[g] + kSweepDocs + t; p < end[g]; p += kSweepThreads) {
                         const int extra = docs[p];
                         if (extra >= d0 && extra < d1) {

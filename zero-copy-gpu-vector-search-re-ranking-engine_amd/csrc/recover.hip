@@ -1,0 +1,325 @@
+// Exact device fallback of the fused search: the top-`width` of one query over the whole corpus,
+// with no candidate buffer that could overflow, for the queries whose threshold-phase segments
+// overflowed (or for every query, with ZCGVS_SEARCH_FORCE_EXACT_PASS).
+//
+// One 1024-thread workgroup per query, launched for the whole batch after the phased scan; a
+// workgroup whose query did not overflow returns at once, so the launch costs a few microseconds
+// when nothing overflowed. A flagged query's workgroup selects by radix passes over recomputed
+// scores: three histogram passes over the ordered 32-bit score (11, 11 and 10 bits) find the
+// score t of the width-th best key and how many keys scoring exactly t it must take; a final pass
+// keeps every key above t and the first of those at t in index order (the lowest-index tie rule
+// of tests/cpp/cpu_reference.hpp:26-34). A pass stops early once its bucket holds exactly the
+// keys still needed. Each pass re-reads the corpus, so a recovered query costs a few corpus
+// reads by one workgroup: slow, but exact for any input and with no memory beyond the result.
+//
+// Scores are computed as the VALU scan computes them (same lanes per row, chunk order and lane
+// group sums, scan_core.hpp), so for every kind they equal that scan's bit for bit.
+#include <hip/hip_runtime.h>
+
+#include "common.hpp"
+#include "fused.hpp"
+#include "scan_core.hpp"
+#include "select.hpp"
+
+namespace zcgvs_hip {
+
+namespace {
+
+constexpr int kRecoverThreads = kMergeThreads;  // 1024
+constexpr int kRecoverChunksPerLane = 8;
+constexpr int kRecoverMinLanes = 8;
+constexpr int kKindI8I8 = 4;
+
+__host__ __device__ constexpr int stagedWordsPerChunk(int kind) {
+    // float32 words of one staged 16-byte chunk of the query, or packed words for integer kinds
+    return kind == ZCGVS_DTYPE_F32 ? 4 : kind == ZCGVS_DTYPE_F16 ? 8 : kind == ZCGVS_DTYPE_I8 ? 16 : 4;
+}
+
+template <int kKind, int L>
+__global__ __launch_bounds__(kRecoverThreads) void recoverKernel(ScanArgs scan, RecoverArgs args,
+                                                                 int chunks) {
+    extern __shared__ std::uint32_t lds_query[];
+    __shared__ std::uint32_t lds_hist[kSelectBins];
+    __shared__ std::uint32_t lds_scan[kRecoverThreads / kWave];
+    __shared__ std::uint64_t lds_keys[kMaxK];
+    __shared__ SelectState lds_state;
+    __shared__ std::uint32_t lds_taken_equal;
+
+    const int q = blockIdx.x;
+    if (!args.force && args.flags[q] == 0u) {
+        return;
+    }
+    const int t = threadIdx.x;
+    const int dim = scan.dim;
+    const int width = args.width;
+    const long long n = scan.doc_count;
+    const int words = chunks * stagedWordsPerChunk(kKind);
+
+    // ---- the query, staged as the VALU scan stages it ----
+    if constexpr (kKind == ZCGVS_DTYPE_BINARY) {
+        const std::uint32_t* src = static_cast<const std::uint32_t*>(scan.queries) + static_cast<std::size_t>(q) * words;
+        for (int i = t; i < words; i += kRecoverThreads) {
+            lds_query[i] = src[i];
+        }
+    } else if constexpr (kKind == kKindI8I8) {
+        const std::int8_t* src = static_cast<const std::int8_t*>(scan.queries) + static_cast<std::size_t>(q) * dim;
+        for (int w = t; w < words; w += kRecoverThreads) {
+            std::uint32_t packed = 0u;
+#pragma unroll
+            for (int b = 0; b < 4; ++b) {
+                const int j = 4 * w + b;
+                const int value = j < dim ? static_cast<int>(src[j]) : 0;
+                packed |= static_cast<std::uint32_t>(value & 0xFF) << (8 * b);
+            }
+            lds_query[w] = packed;
+        }
+    } else {
+        const float* src = static_cast<const float*>(scan.queries) + static_cast<std::size_t>(q) * dim;
+        float* staged = reinterpret_cast<float*>(lds_query);
+        for (int i = t; i < words; i += kRecoverThreads) {
+            staged[i] = i < dim ? src[i] : 0.0f;
+        }
+    }
+    if (t == 0) {
+        lds_state.prefix = 0ull;
+        lds_state.bits = 0u;
+        lds_state.need = static_cast<std::uint32_t>(width);
+        lds_state.done = 0u;
+        lds_state.count = 0u;
+        lds_taken_equal = 0u;
+    }
+    float inverse = 0.0f;
+    if (scan.lexical != nullptr) {
+        const float peak = scan.lexical_max[q];
+        inverse = peak > 0.0f ? 1.0f / peak : 0.0f;
+    }
+    const float qscale = scan.query_scales != nullptr ? scan.query_scales[q] : 1.0f;
+    __syncthreads();
+
+    const int lane = t & (kWave - 1);
+    const int group = lane % L;
+    constexpr int kRowsPerPass = kRecoverThreads / L;
+    constexpr int kPer = kRecoverChunksPerLane;
+    const std::size_t row_bytes = static_cast<std::size_t>(chunks) * 16;
+    const std::uint8_t* corpus = static_cast<const std::uint8_t*>(scan.corpus);
+    const bool l2 = scan.metric == ZCGVS_METRIC_L2;
+
+    // Key of `row` (valid rows only), identical on the L lanes of the row's group.
+    auto keyOf = [&](long long row) -> std::uint64_t {
+        const bool masked = scan.mask != nullptr && scan.mask[row] == 0;
+        uint4 raw[kPer];
+#pragma unroll
+        for (int i = 0; i < kPer; ++i) {
+            const int c = group + i * L;
+            raw[i] = make_uint4(0u, 0u, 0u, 0u);
+            if (!masked && c < chunks) {
+                raw[i] = loadChunk(corpus + static_cast<std::size_t>(row) * row_bytes + static_cast<std::size_t>(c) * 16);
+            }
+        }
+        float score;
+        if constexpr (kKind == ZCGVS_DTYPE_BINARY || kKind == kKindI8I8) {
+            int acc = 0;
+#pragma unroll
+            for (int i = 0; i < kPer; ++i) {
+                const int c = group + i * L;
+                if (c < chunks) {
+                    const uint4 qw = *reinterpret_cast<const uint4*>(lds_query + 4 * c);
+                    if constexpr (kKind == ZCGVS_DTYPE_BINARY) {
+                        acc += __popc(raw[i].x ^ qw.x) + __popc(raw[i].y ^ qw.y) + __popc(raw[i].z ^ qw.z) +
+                               __popc(raw[i].w ^ qw.w);
+                    } else {
+                        acc = __builtin_amdgcn_sdot4(static_cast<int>(raw[i].x), static_cast<int>(qw.x), acc, false);
+                        acc = __builtin_amdgcn_sdot4(static_cast<int>(raw[i].y), static_cast<int>(qw.y), acc, false);
+                        acc = __builtin_amdgcn_sdot4(static_cast<int>(raw[i].z), static_cast<int>(qw.z), acc, false);
+                        acc = __builtin_amdgcn_sdot4(static_cast<int>(raw[i].w), static_cast<int>(qw.w), acc, false);
+                    }
+                }
+            }
+            const int total = groupSum<L>(acc);
+            if constexpr (kKind == ZCGVS_DTYPE_BINARY) {
+                score = static_cast<float>(dim - 2 * total) / static_cast<float>(dim);
+            } else {
+                const float row_scale = masked ? 0.0f : scan.row_scales[row];
+                const float combined = qscale * row_scale;
+                score = static_cast<float>(total) * combined;
+            }
+        } else {
+            using Traits = ChunkTraits<kKind>;
+            constexpr int E = Traits::kElems;
+            const float* staged = reinterpret_cast<const float*>(lds_query);
+            float acc = 0.0f;
+#pragma unroll
+            for (int i = 0; i < kPer; ++i) {
+                const int c = group + i * L;
+                if (c < chunks) {
+                    float v[E];
+                    Traits::decode(raw[i], scan.scale, v);
+                    const float* qv = staged + c * E;
+                    if (l2) {
+#pragma unroll
+                        for (int e = 0; e < E; ++e) {
+                            const float d = qv[e] - v[e];
+                            acc = fmaf(d, d, acc);
+                        }
+                    } else {
+#pragma unroll
+                        for (int e = 0; e < E; ++e) {
+                            acc = fmaf(qv[e], v[e], acc);
+                        }
+                    }
+                }
+            }
+            const float total = groupSum<L>(acc);
+            score = l2 ? -total : total;
+        }
+        float value = masked ? kMaskedScore : score;
+        if (scan.lexical != nullptr) {
+            const float lex = scan.lexical[static_cast<std::size_t>(q) * n + row];
+            value = fuseHybrid(value, lex, scan.dense_weight, inverse);
+        }
+        return makeKey(value, static_cast<std::uint32_t>(row));
+    };
+
+    // Visits every row in index order, kRowsPerPass rows per step; f(key, row, leader) is called
+    // by every thread of a step (key 0 for threads past the corpus; leader: the row's first lane).
+    auto sweep = [&](auto&& f) {
+        for (long long base = 0; base < n; base += kRowsPerPass) {
+            const long long row = base + t / L;
+            const bool valid = row < n;
+            std::uint64_t key = 0ull;
+            if (__any(valid)) {
+                key = keyOf(valid ? row : n - 1);
+            }
+            f(valid ? key : 0ull, row, valid && group == 0);
+        }
+    };
+
+    // ---- histogram passes over the ordered score (the key's upper 32 bits) ----
+    for (int pass = 0; pass < 3; ++pass) {
+        const int digit = selectDigitWidth(pass);
+        for (int i = t; i < (1 << digit); i += kRecoverThreads) {
+            lds_hist[i] = 0u;
+        }
+        __syncthreads();
+        if (lds_state.done) {
+            break;  // uniform: read after a barrier, written only between barriers
+        }
+        const std::uint32_t bits = lds_state.bits;
+        const std::uint64_t prefix = lds_state.prefix;
+        const int shift = 64 - static_cast<int>(bits) - digit;
+        sweep([&](std::uint64_t key, long long, bool leader) {
+            if (leader && (bits == 0u || (key >> (64 - bits)) == prefix)) {
+                atomicAdd(&lds_hist[(key >> shift) & ((1u << digit) - 1u)], 1u);
+            }
+        });
+        __syncthreads();
+        selectPickBucket<kRecoverThreads>(lds_hist, digit, &lds_state, lds_scan);
+    }
+    __syncthreads();
+
+    // ---- collection: every key above the cut, plus the first `need` keys at a tied score ----
+    const bool tied = !lds_state.done;  // all 32 score bits decided, more keys at t than needed
+    const std::uint64_t cut = selectThreshold(lds_state);  // lower edge of the chosen bucket
+    const std::uint32_t need_equal = tied ? lds_state.need : 0u;
+    const std::uint32_t above_needed = static_cast<std::uint32_t>(width) - need_equal;
+    (void)above_needed;
+    sweep([&](std::uint64_t key, long long, bool leader) {
+        const std::uint32_t score_bits = static_cast<std::uint32_t>(key >> 32);
+        const std::uint32_t cut_bits = static_cast<std::uint32_t>(cut >> 32);
+        bool take = leader && (tied ? score_bits > cut_bits : key >= cut);
+        if (tied) {
+            // tied keys in index order: a block-wide prefix count over this step's rows (thread
+            // order is row order inside a step)
+            const bool equal = leader && score_bits == cut_bits;
+            std::uint32_t step_total = 0u;
+            const std::uint32_t through = blockInclusiveSum<kRecoverThreads>(equal ? 1u : 0u, lds_scan, &step_total);
+            const std::uint32_t rank = lds_taken_equal + through - 1u;
+            take = take || (equal && rank < need_equal);
+            __syncthreads();
+            if (t == 0) {
+                lds_taken_equal += step_total;
+            }
+        }
+        if (take) {
+            const std::uint32_t slot = atomicAdd(&lds_state.count, 1u);
+            if (slot < static_cast<std::uint32_t>(kMaxK)) {
+                lds_keys[slot] = key;
+            }
+        }
+    });
+    __syncthreads();
+
+    const std::uint32_t taken = min(min(lds_state.count, static_cast<std::uint32_t>(kMaxK)),
+                                    static_cast<std::uint32_t>(width));
+    std::uint64_t* dst = args.out_keys + static_cast<std::size_t>(q) * width;
+    forEachRanked(lds_keys, taken, [&](std::uint32_t rank, std::uint64_t key) {
+        dst[rank] = key;
+        if (args.out_index != nullptr) {
+            const std::size_t o = static_cast<std::size_t>(q) * width + rank;
+            writeHit(key, &args.out_index[o], &args.out_score[o]);
+        }
+    });
+    for (int i = static_cast<int>(taken) + t; i < width; i += kRecoverThreads) {
+        dst[i] = 0ull;
+        if (args.out_index != nullptr) {
+            const std::size_t o = static_cast<std::size_t>(q) * width + i;
+            writeHit(0ull, &args.out_index[o], &args.out_score[o]);
+        }
+    }
+}
+
+int kindOf(const ScanArgs& scan) {
+    if (scan.dtype == ZCGVS_DTYPE_I8 && scan.row_scales != nullptr) {
+        return kKindI8I8;
+    }
+    return scan.dtype;
+}
+
+template <int kKind>
+int launchKind(int lanes, std::size_t shared, const ScanArgs& scan, const RecoverArgs& args, int chunks,
+               hipStream_t stream) {
+    const dim3 grid(static_cast<unsigned>(scan.batch));
+    switch (lanes) {
+        case 8: recoverKernel<kKind, 8><<<grid, kRecoverThreads, shared, stream>>>(scan, args, chunks); break;
+        case 16: recoverKernel<kKind, 16><<<grid, kRecoverThreads, shared, stream>>>(scan, args, chunks); break;
+        case 32: recoverKernel<kKind, 32><<<grid, kRecoverThreads, shared, stream>>>(scan, args, chunks); break;
+        default: recoverKernel<kKind, 64><<<grid, kRecoverThreads, shared, stream>>>(scan, args, chunks); break;
+    }
+    ZCGVS_LAUNCH_CHECK("exact recovery");
+    return ZCGVS_OK;
+}
+
+}  // namespace
+
+bool recoverSupported(const ScanArgs& scan) {
+    const std::size_t bytes = rowBytes(scan.dtype, scan.dim);
+    if (bytes % 16 != 0 || !aligned16(scan.corpus)) {
+        return false;
+    }
+    const int chunks = static_cast<int>(bytes / 16);
+    const int lanes = lanesPerRow(chunks, kRecoverChunksPerLane, kRecoverMinLanes);
+    const std::size_t staged = static_cast<std::size_t>(chunks) * stagedWordsPerChunk(kindOf(scan)) * 4;
+    return (chunks + lanes - 1) / lanes <= kRecoverChunksPerLane && staged <= 48 * 1024;
+}
+
+int launchRecover(const ScanArgs& scan, const RecoverArgs& args, hipStream_t stream) {
+    if (args.width <= 0 || args.width > kMaxK || scan.batch <= 0) {
+        return setError(ZCGVS_ERR_RUNTIME, "zcgvs recovery: width out of range");
+    }
+    if (!recoverSupported(scan)) {
+        return setError(ZCGVS_ERR_RUNTIME, "zcgvs recovery: row layout not supported");
+    }
+    const int chunks = static_cast<int>(rowBytes(scan.dtype, scan.dim) / 16);
+    const int lanes = lanesPerRow(chunks, kRecoverChunksPerLane, kRecoverMinLanes);
+    const int kind = kindOf(scan);
+    const std::size_t shared = static_cast<std::size_t>(chunks) * stagedWordsPerChunk(kind) * 4;
+    switch (kind) {
+        case ZCGVS_DTYPE_F16: return launchKind<ZCGVS_DTYPE_F16>(lanes, shared, scan, args, chunks, stream);
+        case ZCGVS_DTYPE_I8: return launchKind<ZCGVS_DTYPE_I8>(lanes, shared, scan, args, chunks, stream);
+        case ZCGVS_DTYPE_BINARY: return launchKind<ZCGVS_DTYPE_BINARY>(lanes, shared, scan, args, chunks, stream);
+        case kKindI8I8: return launchKind<kKindI8I8>(lanes, shared, scan, args, chunks, stream);
+        default: return launchKind<ZCGVS_DTYPE_F32>(lanes, shared, scan, args, chunks, stream);
+    }
+}
+
+}  // namespace zcgvs_hip

@@ -72,6 +72,7 @@ struct Plan {
     bool use_mfma_binary = false;
     bool direct_scales = false;  // MFMA path without a mask: only the tail tile's scales are copied
     bool lex_sorted = false;     // hybrid with postings ascending by document: sliced BM25 stage
+    bool recover = false;        // threshold phases ran: the exact fallback follows them
     int width = 0;  // keys selected by the scan stage
     int block_rows = 64;
     int workgroups = 1;
@@ -175,6 +176,9 @@ Plan validate(const zcgvs_search_desc& d) {
         }
     }
     plan.hybrid = d.query_terms != nullptr && d.lexical_stride > 0;
+    if ((d.flags & ZCGVS_SEARCH_SORTED_POSTINGS) != 0 && (d.flags & ZCGVS_SEARCH_UNSORTED_POSTINGS) != 0) {
+        return fail(ZCGVS_ERR_INVALID_ARGUMENT, "zcgvs: postings cannot be both sorted and unsorted");
+    }
     if (plan.hybrid) {
         if (d.lex_offsets == nullptr || d.lex_docs == nullptr || d.lex_weights == nullptr) {
             return fail(ZCGVS_ERR_INVALID_ARGUMENT, "zcgvs: lexical index pointers are null");
@@ -226,6 +230,18 @@ ScanArgs scanArgsOf(const zcgvs_search_desc& d, const Plan& plan, std::uint8_t* 
     return scan;
 }
 
+// The scan arguments of the exact fallback: those of the VALU scan (the caller's row scales and
+// allow-mask, never the MFMA scan's padded scale copy).
+ScanArgs recoverArgsOf(const zcgvs_search_desc& d, const Plan& plan, std::uint8_t* ws) {
+    Plan valu = plan;
+    valu.use_mfma = false;
+    ScanArgs scan = scanArgsOf(d, valu, ws);
+    scan.row_scales = plan.per_vector ? d.corpus.row_scales : nullptr;
+    scan.tail_scales = nullptr;
+    scan.mask = d.mask;
+    return scan;
+}
+
 Plan makePlan(const zcgvs_search_desc& d) {
     Plan plan = validate(d);
     if (plan.status != ZCGVS_OK) {
@@ -254,6 +270,15 @@ Plan makePlan(const zcgvs_search_desc& d) {
     plan.use_mfma_binary = !forced && mfmaBinarySupported(probe);
     plan.materialized = forced || (!plan.use_mfma && !plan.use_mfma_float && !plan.use_mfma_binary &&
                                    !valuSupported(probe));
+    if (!plan.materialized) {
+        ScanArgs fallback = probe;
+        fallback.row_scales = plan.per_vector ? d.corpus.row_scales : nullptr;
+        fallback.mask = d.mask;
+        if (!recoverSupported(fallback)) {
+            plan.materialized = true;  // no exact fallback for this row layout
+            plan.use_mfma = plan.use_mfma_float = plan.use_mfma_binary = false;
+        }
+    }
     if (plan.per_vector && plan.materialized && dim % 16 != 0) {
         return fail(ZCGVS_ERR_INVALID_ARGUMENT,
                     "zcgvs: per-vector int8 mode needs dim % 16 == 0 and a 16-byte aligned corpus");
@@ -275,7 +300,7 @@ Plan makePlan(const zcgvs_search_desc& d) {
         }
     }
     plan.overflow = layout.add(static_cast<std::size_t>(batch) * 4);
-    if (plan.hybrid && (d.flags & ZCGVS_SEARCH_UNSORTED_POSTINGS) == 0) {
+    if (plan.hybrid && (d.flags & ZCGVS_SEARCH_SORTED_POSTINGS) != 0) {
         plan.lex_sorted = true;
         plan.lexbounds = layout.add(lexicalBoundsBytes(batch, d.lexical_stride, static_cast<int>(n)));
     }
@@ -368,8 +393,16 @@ Plan makePlan(const zcgvs_search_desc& d) {
     plan.segments = plan.workgroups * (plan.use_mfma ? mfmaSegmentsPerWorkgroup() : 1);
     // Segment capacity: 4x the expected candidates per (segment, query) of the widest phase.
     const long long expected = (static_cast<long long>(plan.width) * growth) / plan.segments;
+    // At least one full work item of candidates (two tiles of the int8 MFMA scan, whose segments
+    // take half a tile's rows each) per segment, so a corpus whose best rows sit together in a few
+    // blocks (sorted or clustered rows) does not overflow the segments.
+    const long long item_rows = plan.use_mfma ? kMfmaBlockRows : plan.block_rows;
     // (at most 2^23 slots: the int8 MFMA scan packs a slot, a half and an 8-bit query into 32 bits)
-    plan.seg_log2 = std::min(23, std::max(5, ceilLog2(4 * expected + 16)));
+    plan.seg_log2 = std::min(23, std::max({6, ceilLog2(4 * expected + 16), ceilLog2(item_rows)}));
+    if ((d.flags & ZCGVS_SEARCH_TEST_TINY_SEGMENTS) != 0) {
+        plan.seg_log2 = 1;  // tests: overflow nearly every query so the fallback runs from its flags
+    }
+    plan.recover = plan.phases.size() > 1 || (d.flags & ZCGVS_SEARCH_FORCE_EXACT_PASS) != 0;
 
     if (plan.hybrid) {
         plan.lex = layout.add(static_cast<std::size_t>(batch) * n * 4);
@@ -663,7 +696,22 @@ int searchTopk(const zcgvs_search_desc* desc, void* d_workspace, std::size_t wor
         }
     }
 
-    // 4. rescore
+    // 4. the exact fallback for queries whose segments overflowed (a near-empty launch otherwise)
+    if (plan.recover) {
+        RecoverArgs recovery;
+        recovery.flags = overflow;
+        recovery.force = (d.flags & ZCGVS_SEARCH_FORCE_EXACT_PASS) != 0;
+        recovery.width = plan.width;
+        recovery.out_keys = keys;
+        recovery.out_index = plan.rescore ? nullptr : d_out_indices;
+        recovery.out_score = plan.rescore ? nullptr : d_out_values;
+        status = launchRecover(recoverArgsOf(d, plan, ws), recovery, s);
+        if (status != ZCGVS_OK) {
+            return status;
+        }
+    }
+
+    // 5. rescore
     if (plan.rescore) {
         std::uint64_t* rescored = at<std::uint64_t>(ws, plan.rescored);
         status = launchRescoreKeys(d.rescore.data, d.rescore.dtype, d.rescore.scale,

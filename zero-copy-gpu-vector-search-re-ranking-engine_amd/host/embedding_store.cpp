@@ -89,6 +89,16 @@ EmbeddingStore EmbeddingStore::loadFromFile(const std::string& path) {
     if (store.per_row_ && store.dtype_ != ScalarType::Int8) {
         throw std::runtime_error("zcgvs: per-row scales are defined for int8 rows only");
     }
+    // A short file is rejected before any device memory is taken for it.
+    const std::size_t payload = static_cast<std::size_t>(doc_count) * stride +
+                                (store.per_row_ ? static_cast<std::size_t>(doc_count) * sizeof(float) : 0);
+    const std::streampos here = in.tellg();
+    in.seekg(0, std::ios::end);
+    const std::streamoff available = in.tellg() - here;
+    in.seekg(here);
+    if (available < 0 || static_cast<std::size_t>(available) < payload) {
+        throw std::runtime_error("zcgvs binary: unexpected end of stream");
+    }
 
     store.rows_.allocate(static_cast<std::size_t>(doc_count) * stride);
     streamToDevice(reader, store.rows_.data(), static_cast<std::size_t>(doc_count) * stride);

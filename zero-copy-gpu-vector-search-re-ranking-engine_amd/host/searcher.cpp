@@ -162,8 +162,8 @@ zcgvs_search_desc Searcher::describe(const float* queries, int batch, const Sear
         desc.lex_weights = lexical_index_->devicePostingWeights();
         desc.lex_doc_count = lexical_index_->docCount();
         desc.lex_vocab_size = lexical_index_->vocabSize();
-        if (!lexical_index_->postingsSorted()) {
-            desc.flags |= ZCGVS_SEARCH_UNSORTED_POSTINGS;
+        if (lexical_index_->postingsSorted()) {  // checked when the index was loaded
+            desc.flags |= ZCGVS_SEARCH_SORTED_POSTINGS;
         }
         desc.query_terms = d_query_terms_.data();
         desc.lexical_stride = params.lexical_stride;
@@ -286,24 +286,6 @@ void Searcher::run(const float* device_queries, int dim, int batch, const Search
     current_batch_ = batch;
 }
 
-void Searcher::recomputeExact(int query, const HipStream& stream) {
-    zcgvs_search_desc desc = last_desc_;
-    desc.batch = 1;
-    desc.queries = last_desc_.queries + static_cast<std::size_t>(query) * static_cast<std::size_t>(dim_);
-    if (desc.query_terms != nullptr) {
-        desc.query_terms += static_cast<std::size_t>(query) * static_cast<std::size_t>(desc.lexical_stride);
-    }
-    desc.flags |= ZCGVS_SEARCH_MATERIALIZE;
-    grow(d_exact_workspace_, workspaceBytes(desc));
-    const std::size_t row = static_cast<std::size_t>(query) * static_cast<std::size_t>(current_k_);
-    check(zcgvs_search_topk(&desc, d_exact_workspace_.data(), d_exact_workspace_.size(), d_out_indices_.data() + row,
-                            d_out_values_.data() + row, stream.get()));
-    d_out_indices_.copyToHost(h_out_indices_.data() + row, static_cast<std::size_t>(current_k_), stream.get(), row);
-    d_out_values_.copyToHost(h_out_values_.data() + row, static_cast<std::size_t>(current_k_), stream.get(), row);
-    stream.synchronize();
-    ++exact_recomputes_;
-}
-
 HostTopK Searcher::copyResultToHost(const HipStream& stream) {
     if (current_k_ == 0 || current_batch_ == 0) {
         throw std::runtime_error("zcgvs: copyResultToHost called before search");
@@ -325,10 +307,9 @@ HostTopK Searcher::copyResultToHost(const HipStream& stream) {
     stream.synchronize();
     last_gpu_ms_ = static_cast<double>(ev_end_.elapsedSince(ev_start_));
 
+    // the device already replaced these queries' results with its exact fallback's
     for (int q = 0; q < current_batch_; ++q) {
-        if (h_overflow_.data()[q] != 0u) {
-            recomputeExact(q, stream);
-        }
+        exact_recomputes_ += h_overflow_.data()[q] != 0u ? 1u : 0u;
     }
 
     HostTopK result;

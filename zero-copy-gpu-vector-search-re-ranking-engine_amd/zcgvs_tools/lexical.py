@@ -1,5 +1,5 @@
-"""BM25 CSR index builder over documents given as term-id lists, and the synthetic corpus of the
-hybrid configuration (Poisson(200) document lengths, Zipf(1.1) term draws over a 30,000-term
+"""BM25 CSR index builder over documents given as term-id lists, and the synthetic index of the
+hybrid configuration (Poisson(200) document lengths, i.i.d. Zipf(1.1) tokens over a 30,000-term
 vocabulary, 8 distinct Zipf terms per query).
 
 Weights follow python/zcgvs_tools/build_lexical.py:143-154 of the reference, in float64, cast to
@@ -45,10 +45,35 @@ def build_bm25(doc_terms: list[np.ndarray], vocab_size: int, k1: float = 1.2, b:
 
 def zipf_terms(rng: np.random.Generator, count: int, vocab_size: int, s: float = 1.1) -> np.ndarray:
     """`count` term ids with P(rank r) proportional to r^-s over ranks 1..vocab_size (id = rank - 1)."""
-    ranks = np.arange(1, vocab_size + 1, dtype=np.float64)
-    cdf = np.cumsum(ranks ** -s)
-    cdf /= cdf[-1]
-    return np.minimum(np.searchsorted(cdf, rng.random(count), side="right"), vocab_size - 1).astype(np.int64)
+    return _ZipfSampler(vocab_size, s).draw(rng.random(count)).astype(np.int64)
+
+
+class _ZipfSampler:
+    """Inverse-CDF sampling, searchsorted(cdf, u, 'right') capped at vocab_size - 1, through a
+    table of 2^20 equal-width buckets of u: a bucket holding no CDF point maps all of its u to
+    one term (u * 2^20 is exact, so the bucket of u is exact); only the u in the few buckets that
+    hold a CDF point are searched. Results equal the plain search for every u."""
+
+    BITS = 20
+
+    def __init__(self, vocab_size: int, s: float):
+        ranks = np.arange(1, vocab_size + 1, dtype=np.float64)
+        cdf = np.cumsum(ranks ** -s)
+        cdf /= cdf[-1]
+        self.cdf = cdf
+        self.vocab_size = vocab_size
+        edges = np.arange((1 << self.BITS) + 1, dtype=np.float64) / float(1 << self.BITS)
+        below = np.searchsorted(cdf, edges[:-1], side="right")   # count(cdf <= bucket start)
+        inside = np.searchsorted(cdf, edges[1:], side="left")    # count(cdf < bucket end)
+        self.table = below.astype(np.int32)
+        self.mixed = inside != below
+
+    def draw(self, u: np.ndarray) -> np.ndarray:
+        bucket = (u * float(1 << self.BITS)).astype(np.int64)
+        out = self.table[bucket]
+        hard = np.flatnonzero(self.mixed[bucket])
+        out[hard] = np.searchsorted(self.cdf, u[hard], side="right")
+        return np.minimum(out, self.vocab_size - 1)
 
 
 def synthetic_corpus(doc_count: int, vocab_size: int = 30_000, mean_length: float = 200.0, s: float = 1.1,
@@ -59,75 +84,76 @@ def synthetic_corpus(doc_count: int, vocab_size: int = 30_000, mean_length: floa
     return np.split(flat, np.cumsum(lengths)[:-1])
 
 
-def zero_truncated_poisson(rng: np.random.Generator, lam: np.ndarray) -> np.ndarray:
-    """One draw of Poisson(lam) conditioned on >= 1 per element, by inverting its CDF; each
-    round continues only with the elements whose draw exceeds the current count."""
-    lam = np.asarray(lam, dtype=np.float64)
-    out = np.ones(lam.size, dtype=np.int64)
-    u = rng.random(lam.size)
-    denom = -np.expm1(-lam)
-    term = lam * np.exp(-lam) / denom  # P(k = 1 | k >= 1)
-    cum = term.copy()
-    live = np.flatnonzero(u > cum)
-    term, cum, lam_live, u_live = term[live], cum[live], lam[live], u[live]
-    k = 1
-    while live.size and k < 1000:
-        k += 1
-        term *= lam_live / k
-        cum += term
-        out[live] = k
-        keep = u_live > cum
-        live, term, cum, lam_live, u_live = live[keep], term[keep], cum[keep], lam_live[keep], u_live[keep]
-    return out
-
-
 def synthetic_index(doc_count: int, vocab_size: int = 30_000, mean_length: float = 200.0, s: float = 1.1,
-                    seed: int = 7, k1: float = 1.2, b: float = 0.75) -> dict:
-    """The BM25 index of synthetic_corpus's model, generated term by term without tokens.
+                    seed: int = 7, k1: float = 1.2, b: float = 0.75, chunk_docs: int = 65_536,
+                    with_counts: bool = False) -> dict:
+    """The BM25 index of the synthetic token model, built exactly: document lengths ~
+    Poisson(mean_length), every token an i.i.d. Zipf(s) term (zipf_terms), tf = the number of
+    times a term occurs in a document, length = the document's token count (the reference's
+    builder counts tokens the same way, python/zcgvs_tools/build_lexical.py:128-154).
 
-    With document lengths ~ Poisson(mean_length) and tokens drawn i.i.d. from the Zipf law p_t,
-    the term counts n_{d,t} are independent Poisson(mean_length * p_t) (Poisson splitting), and
-    a document's length is the sum of its counts. So each term's postings are drawn directly: the
-    documents holding a frequent term are a Bernoulli(1 - exp(-lambda_t)) subset; a rare term
-    gets a binomial number of uniform documents (a document drawn twice for one term counts
-    once, which at these rates changes almost nothing); counts are zero-truncated
-    Poisson(lambda_t). The cost is linear in the postings (about 1.2e8 at 1M documents), not in
-    the 2e8 tokens. Weights and layout are those of build_bm25."""
+    Documents are tokenized and counted in chunks of `chunk_docs` documents: one sort of
+    (term, document) inside the chunk gives its postings term-major with documents ascending and
+    their counts as run lengths; the chunks, taken in document order, are then placed term by term
+    behind each other, so every term's documents ascend. Memory stays proportional to one chunk's
+    tokens plus the postings. With `with_counts` the result also holds the per-posting term counts
+    ("tf") and the document lengths ("lengths")."""
     rng = np.random.default_rng(seed)
-    ranks = np.arange(1, vocab_size + 1, dtype=np.float64)
-    p = ranks ** -s
-    p /= p.sum()
-    lam = mean_length * p
-    present = -np.expm1(-lam)  # P(n_{d,t} >= 1)
-    frequent = np.flatnonzero(present > 0.05)
-    rare = np.flatnonzero(present <= 0.05)
-    term_parts, doc_parts = [], []
-    for t in frequent:
-        docs = np.flatnonzero(rng.random(doc_count) < present[t])
-        term_parts.append(np.full(docs.size, t, dtype=np.int64))
-        doc_parts.append(docs.astype(np.int64))
-    sizes = rng.binomial(doc_count, present[rare])
-    rare_terms = np.repeat(rare.astype(np.int64), sizes)
-    rare_keys = np.unique(rare_terms * doc_count + rng.integers(0, doc_count, size=rare_terms.size))
-    term_parts.append(rare_keys // doc_count)
-    doc_parts.append(rare_keys % doc_count)
-    terms = np.concatenate(term_parts)
-    docs = np.concatenate(doc_parts)
-    order = np.argsort(terms, kind="stable")  # frequent terms come first; rare keys are sorted
-    terms, docs = terms[order], docs[order].astype(np.int32)
-    tfs = zero_truncated_poisson(rng, lam[terms]).astype(np.float64)
-    counts = np.bincount(terms, minlength=vocab_size)
-    lengths = np.bincount(docs, weights=tfs, minlength=doc_count)
+    lengths = rng.poisson(mean_length, size=doc_count).astype(np.int64)
+    sampler = _ZipfSampler(vocab_size, s)
+    shift = max(1, int(chunk_docs - 1).bit_length())
+    key_type = np.uint32 if (vocab_size << shift) <= (1 << 32) else np.uint64
+    chunks = []
+    df = np.zeros(vocab_size, dtype=np.int64)
+    for d0 in range(0, doc_count, chunk_docs):
+        d1 = min(doc_count, d0 + chunk_docs)
+        counts = lengths[d0:d1]
+        tokens = sampler.draw(rng.random(int(counts.sum()))).astype(key_type)
+        keys = (tokens << key_type(shift)) | np.repeat(np.arange(d1 - d0, dtype=key_type), counts)
+        del tokens
+        keys.sort()
+        if keys.size == 0:
+            continue
+        starts = np.flatnonzero(np.concatenate(([True], keys[1:] != keys[:-1])))
+        uniq = keys[starts]
+        tf = np.diff(np.append(starts, keys.size)).astype(np.int32)
+        del keys, starts
+        terms = (uniq >> key_type(shift)).astype(np.int32)
+        docs = (d0 + (uniq & key_type((1 << shift) - 1)).astype(np.int64)).astype(np.int32)
+        df += np.bincount(terms, minlength=vocab_size)
+        chunks.append((terms, docs, tf))
+    offsets = np.zeros(vocab_size + 1, dtype=np.int64)
+    offsets[1:] = np.cumsum(df)
+    nnz = int(offsets[-1])
+    docs_out = np.empty(nnz, dtype=np.int32)
+    tf_out = np.empty(nnz, dtype=np.int32)
+    cursor = offsets[:-1].copy()
+    for terms, docs, tf in chunks:
+        # postings of the chunk are term-major: rank within the term's run + the term's cursor
+        run = np.flatnonzero(np.concatenate(([True], terms[1:] != terms[:-1])))
+        run_length = np.diff(np.append(run, terms.size))
+        rank = np.arange(terms.size, dtype=np.int64) - np.repeat(run, run_length)
+        position = cursor[terms] + rank
+        docs_out[position] = docs
+        tf_out[position] = tf
+        cursor[terms[run]] += run_length
+    chunks.clear()
     avgdl = float(lengths.mean()) if doc_count else 1.0
     avgdl = avgdl if avgdl > 0.0 else 1.0
-    offsets = np.zeros(vocab_size + 1, dtype=np.int64)
-    offsets[1:] = np.cumsum(counts)
-    df = counts.astype(np.float64)
-    idf = np.log(1.0 + (doc_count - df[terms] + 0.5) / (df[terms] + 0.5))
-    norm = k1 * (1.0 - b + b * lengths[docs] / avgdl)
-    weights = (idf * (tfs * (k1 + 1.0)) / (tfs + norm)).astype(np.float32)
-    return {"offsets": offsets, "posting_docs": docs, "posting_weights": weights, "doc_count": doc_count,
-            "vocab_size": vocab_size, "k1": k1, "b": b, "average_doc_length": avgdl}
+    term_of = np.repeat(np.arange(vocab_size, dtype=np.int64), df)
+    dfp = df[term_of].astype(np.float64)
+    del term_of
+    idf = np.log(1.0 + (doc_count - dfp + 0.5) / (dfp + 0.5))
+    del dfp
+    tf64 = tf_out.astype(np.float64)
+    norm = k1 * (1.0 - b + b * lengths[docs_out].astype(np.float64) / avgdl)
+    weights = (idf * (tf64 * (k1 + 1.0)) / (tf64 + norm)).astype(np.float32)
+    index = {"offsets": offsets, "posting_docs": docs_out, "posting_weights": weights, "doc_count": doc_count,
+             "vocab_size": vocab_size, "k1": k1, "b": b, "average_doc_length": avgdl}
+    if with_counts:
+        index["tf"] = tf_out
+        index["lengths"] = lengths
+    return index
 
 
 def synthetic_queries(batch: int, terms: int = 8, vocab_size: int = 30_000, s: float = 1.1,
