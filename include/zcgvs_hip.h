@@ -309,6 +309,18 @@ size_t zcgvs_search_workspace_bytes(const zcgvs_search_desc* desc);
 int zcgvs_search_topk(const zcgvs_search_desc* desc, void* d_workspace, size_t workspace_bytes,
                       int* d_out_indices, float* d_out_values, zcgvs_stream_t stream);
 
+/* No counterpart in the reference. For callers that cannot allocate device memory (code under
+ * HIP graph capture, tight serving loops, harnesses that forbid hipMalloc): zcgvs_search_topk with
+ * its workspace in a library-owned static device array of zcgvs_static_scratch_bytes() bytes
+ * (64 MiB) per device instead of a caller's buffer. A search whose workspace
+ * (zcgvs_search_workspace_bytes) exceeds that size is rejected with ZCGVS_ERR_INVALID_ARGUMENT;
+ * nothing is allocated or freed, on the host's HIP side or the device. Every call on one device
+ * shares that device's array: calls that overlap on one GPU (concurrent streams, threads) race
+ * and must be serialized by the caller. The results equal zcgvs_search_topk's. */
+size_t zcgvs_static_scratch_bytes(void);
+int zcgvs_search_topk_noalloc(const zcgvs_search_desc* desc, int* d_out_indices, float* d_out_values,
+                              zcgvs_stream_t stream);
+
 /* Measurement hook: zcgvs_search_topk that also records events[2p] and events[2p + 1] on `stream`
  * immediately before and after the scan launches of phase p, for p < max_phases, and returns the
  * number of phases in *phases. The events must have been created with zcgvs_event_create. Not

@@ -108,6 +108,8 @@ _SIGNATURES = {
     "zcgvs_launch_quantize_rows_i8": (_i32, [_vp, _i32, _i32, _vp, _vp, _vp]),
     "zcgvs_search_workspace_bytes": (_sz, [ctypes.POINTER(SearchDesc)]),
     "zcgvs_search_topk": (_i32, [ctypes.POINTER(SearchDesc), _vp, _sz, _vp, _vp, _vp]),
+    "zcgvs_search_topk_noalloc": (_i32, [ctypes.POINTER(SearchDesc), _vp, _vp, _vp]),
+    "zcgvs_static_scratch_bytes": (_sz, []),
     "zcgvs_search_overflow_flags": (_i32, [ctypes.POINTER(SearchDesc), _vp, ctypes.POINTER(_vp)]),
     "zcgvs_search_topk_profiled": (_i32, [ctypes.POINTER(SearchDesc), _vp, _sz, _vp, _vp, _vp,
                                           ctypes.POINTER(_vp), _i32, ctypes.POINTER(_i32)]),

@@ -15,6 +15,7 @@
 #include <hip/hip_runtime.h>
 
 #include <algorithm>
+#include <mutex>
 #include <string>
 #include <vector>
 
@@ -520,6 +521,47 @@ __global__ void zeroWordsKernel(std::uint32_t* __restrict__ dst, std::size_t cou
     }
 }
 
+// Workspace of zcgvs_search_topk_noalloc: one library-owned array per device, so a caller that
+// cannot allocate still runs the pipeline. Its size caps the searches that entry point accepts.
+constexpr std::size_t kStaticScratchBytes = std::size_t(64) << 20;
+
+}  // namespace
+
+}  // namespace zcgvs_hip
+
+// In host code `scratch` names a host-side stand-in, not device memory: its device address comes
+// from hipGetSymbolAddress, once per device (scratchAddress below).
+static __device__ __align__(256) std::uint8_t scratch[zcgvs_hip::kStaticScratchBytes];
+
+namespace zcgvs_hip {
+
+namespace {
+
+std::mutex g_scratch_mutex;
+std::vector<void*> g_scratch_address;  // indexed by device; null until first looked up
+
+// Device address of this device's `scratch`, looked up with that device current on its first use.
+int scratchAddress(void** address) {
+    int device = 0;
+    ZCGVS_HIP_RETURN(hipGetDevice(&device));
+    std::lock_guard<std::mutex> lock(g_scratch_mutex);
+    if (static_cast<int>(g_scratch_address.size()) <= device) {
+        g_scratch_address.resize(static_cast<std::size_t>(device) + 1, nullptr);
+    }
+    void*& cached = g_scratch_address[static_cast<std::size_t>(device)];
+    if (cached == nullptr) {
+        void* found = nullptr;
+        const hipError_t status = hipGetSymbolAddress(&found, HIP_SYMBOL(scratch));
+        if (status != hipSuccess || found == nullptr) {
+            return hipFailure(status != hipSuccess ? status : hipErrorInvalidSymbol,
+                              "hipGetSymbolAddress(scratch)", __FILE__, __LINE__);
+        }
+        cached = found;
+    }
+    *address = cached;
+    return ZCGVS_OK;
+}
+
 }  // namespace
 
 }  // namespace zcgvs_hip
@@ -773,6 +815,33 @@ int zcgvs_search_phase_rows(const zcgvs_search_desc* desc, long long* rows, int 
         rows[p] = r;
     }
     return clearError();
+}
+
+std::size_t zcgvs_static_scratch_bytes(void) { return kStaticScratchBytes; }
+
+int zcgvs_search_topk_noalloc(const zcgvs_search_desc* desc, int* d_out_indices, float* d_out_values,
+                              zcgvs_stream_t stream) {
+    if (desc == nullptr) {
+        return setError(ZCGVS_ERR_INVALID_ARGUMENT, "zcgvs: descriptor must not be null");
+    }
+    const Plan plan = makePlan(*desc);
+    if (plan.status != ZCGVS_OK) {
+        return setError(plan.status, plan.error);
+    }
+    if (plan.total > kStaticScratchBytes) {
+        return setError(ZCGVS_ERR_INVALID_ARGUMENT,
+                        "zcgvs: this search needs " + std::to_string(plan.total) +
+                            " bytes of workspace, more than the " + std::to_string(kStaticScratchBytes) +
+                            "-byte static scratch of zcgvs_search_topk_noalloc; pass a workspace to "
+                            "zcgvs_search_topk instead");
+    }
+    void* address = nullptr;
+    const int status = scratchAddress(&address);
+    if (status != ZCGVS_OK) {
+        return status;
+    }
+    return searchTopk(desc, address, kStaticScratchBytes, d_out_indices, d_out_values, stream, nullptr, 0,
+                      nullptr);
 }
 
 }  // extern "C"
