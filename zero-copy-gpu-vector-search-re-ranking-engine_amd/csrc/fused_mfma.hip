@@ -336,37 +336,43 @@ void mfmaScanKernel(ScanArgs scan, PhaseArgs phase, EmitArgs emit, int q_offset,
             if (examine_all) {
                 return 0xFFFFFFFFu;
             }
-            // First the lane's largest relaxed score: the slot set is needed only when it reaches
-            // the lane's threshold somewhere in the wavefront.
-            float best = -INFINITY;
+            // Per lane the largest relaxed score of each group of four value slots (one float4 of
+            // row scales); the slot set is needed only when some group reaches the lane's threshold
+            // somewhere in the wavefront, and then only inside the groups that do.
+            float group_best[8];
 #pragma unroll
             for (int mb = 0; mb < 2; ++mb) {
 #pragma unroll
                 for (int g = 0; g < 4; ++g) {
                     const float4 rs = *reinterpret_cast<const float4*>(scales + mb * 32 + 8 * g + 4 * half);
                     const float rsv[4] = {rs.x, rs.y, rs.z, rs.w};
+                    float p[4];
 #pragma unroll
                     for (int j = 0; j < 4; ++j) {
                         const int dot = mb == 0 ? acc0[4 * g + j] : acc1[4 * g + j];
-                        best = fmaxf(best, static_cast<float>(dot) * rsv[j]);
+                        p[j] = static_cast<float>(dot) * rsv[j];
                     }
+                    group_best[4 * mb + g] = fmaxf(fmaxf(p[0], p[1]), fmaxf(p[2], p[3]));
                 }
             }
+            const float best = fmaxf(fmaxf(fmaxf(group_best[0], group_best[1]), fmaxf(group_best[2], group_best[3])),
+                                     fmaxf(fmaxf(group_best[4], group_best[5]), fmaxf(group_best[6], group_best[7])));
             if (!__any(best >= relaxed_floor)) {
                 return 0u;
             }
             std::uint32_t passing = 0u;
 #pragma unroll
-            for (int mb = 0; mb < 2; ++mb) {
-#pragma unroll
-                for (int g = 0; g < 4; ++g) {
-                    const float4 rs = *reinterpret_cast<const float4*>(scales + mb * 32 + 8 * g + 4 * half);
+            for (int grp = 0; grp < 8; ++grp) {
+                if (__any(group_best[grp] >= relaxed_floor)) {
+                    // the group's products again (same operations, same values)
+                    const float4 rs = *reinterpret_cast<const float4*>(scales + (grp / 4) * 32 + 8 * (grp % 4) + 4 * half);
                     const float rsv[4] = {rs.x, rs.y, rs.z, rs.w};
 #pragma unroll
                     for (int j = 0; j < 4; ++j) {
-                        const int dot = mb == 0 ? acc0[4 * g + j] : acc1[4 * g + j];
+                        const int slot = 4 * grp + j;
+                        const int dot = slot < 16 ? acc0[slot] : acc1[slot - 16];
                         const bool pass = static_cast<float>(dot) * rsv[j] >= relaxed_floor;
-                        passing |= (__builtin_amdgcn_ballot_w64(pass) != 0 ? 1u : 0u) << (16 * mb + 4 * g + j);
+                        passing |= (__builtin_amdgcn_ballot_w64(pass) != 0 ? 1u : 0u) << slot;
                     }
                 }
             }
@@ -400,26 +406,36 @@ void mfmaScanKernel(ScanArgs scan, PhaseArgs phase, EmitArgs emit, int q_offset,
                 }
             }
         };
-        // Exact scores and keys of the value slots `passing` marks; keys above the threshold are
-        // appended.
+        // Exact scores and keys of the value slots `passing` marks (slot 4 grp + j: row block
+        // grp / 4, rows 32 (grp / 4) + 8 (grp % 4) + 4 half + j); keys above the threshold are
+        // appended. A group's four row scales come in one LDS read.
         auto exact = [&](const v16i& acc0, const v16i& acc1, const float* scales, long long row0,
                          std::uint32_t passing) {
             // Tile-relative rows in 32 bits; the empty asm keeps the compiler from hoisting the
-            // 32 per-row constants out of the scan loop into registers.
+            // per-row constants out of the scan loop into registers.
             int hb = 4 * half;
             asm volatile("" : "+v"(hb));
             const int valid_rows = static_cast<int>(min(static_cast<long long>(kRows), doc_count - row0));
             const std::uint32_t row_base = static_cast<std::uint32_t>(row0);
 #pragma unroll
-            for (int slot = 0; slot < 32; ++slot) {
-                if (passing & (1u << slot)) {
-                    const int rl = (slot / 16) * 32 + 8 * ((slot % 16) / 4) + hb + slot % 4;
-                    const float rs = scales[rl];
-                    const int dot = slot < 16 ? acc0[slot] : acc1[slot - 16];
-                    const float combined = qscale * rs;
-                    const float score = rs == rs ? static_cast<float>(dot) * combined : kMaskedScore;
-                    const std::uint64_t key = makeKey(score, row_base + static_cast<std::uint32_t>(rl));
-                    stageCandidates(q_valid && rl < valid_rows && score >= tau_floor && key > tau, key);
+            for (int grp = 0; grp < 8; ++grp) {
+                if ((passing >> (4 * grp)) & 0xFu) {
+                    const int rl0 = (grp / 4) * 32 + 8 * (grp % 4) + hb;
+                    const float4 rs4 = *reinterpret_cast<const float4*>(scales + rl0);
+                    const float rsv[4] = {rs4.x, rs4.y, rs4.z, rs4.w};
+#pragma unroll
+                    for (int j = 0; j < 4; ++j) {
+                        const int slot = 4 * grp + j;
+                        if (passing & (1u << slot)) {
+                            const int rl = rl0 + j;
+                            const float rs = rsv[j];
+                            const int dot = slot < 16 ? acc0[slot] : acc1[slot - 16];
+                            const float combined = qscale * rs;
+                            const float score = rs == rs ? static_cast<float>(dot) * combined : kMaskedScore;
+                            const std::uint64_t key = makeKey(score, row_base + static_cast<std::uint32_t>(rl));
+                            stageCandidates(q_valid && rl < valid_rows && score >= tau_floor && key > tau, key);
+                        }
+                    }
                 }
             }
         };
