@@ -44,6 +44,9 @@ WORKLOADS = {
                      name="per-vector int8 10M x 768, batch 256, k=100"),
     "int8-10m-b1": dict(kind="i8i8", n=10_000_000, dim=768, batch=1, k=100,
                         name="per-vector int8 10M x 768, batch 1, k=100"),
+    "int8-10m-sorted": dict(kind="i8i8", n=10_000_000, dim=768, batch=256, k=100, sort_rows=True,
+                            name="per-vector int8 10M x 768 with rows sorted by their first coordinate, "
+                                 "batch 256, k=100"),
     "f32-1m-b1": dict(kind="f32", n=1_000_000, dim=384, batch=1, k=10,
                       name="float32 1M x 384, batch 1, k=10"),
     "f16-1m-b1": dict(kind="f16", n=1_000_000, dim=384, batch=1, k=10,
@@ -104,6 +107,18 @@ def build_inputs(capi, w):
             capi.launch_convert_f32_to_f16(stage, rescore.ptr + start * dim * 2, rows * dim)
         capi.synchronize()
     stage.free()
+    if w.get("sort_rows"):
+        # a clustered corpus: rows in ascending order of their first coordinate, so a query's
+        # best rows crowd into one end of the corpus instead of being spread over it
+        log("sorting the corpus rows by their first coordinate")
+        codes = corpus.to_host()
+        order = np.argsort(codes[:, 0], kind="stable")
+        codes = np.ascontiguousarray(codes[order])
+        capi.call("zcgvs_memcpy_h2d", corpus.ptr, codes.ctypes.data, codes.nbytes, None)
+        row_scales = np.ascontiguousarray(keep["scales"].to_host()[order])
+        capi.call("zcgvs_memcpy_h2d", keep["scales"].ptr, row_scales.ctypes.data, row_scales.nbytes, None)
+        capi.synchronize()
+        del codes, row_scales, order
     queries = capi.DeviceArray((batch, dim), np.float32)
     capi.generate_normalized(queries, batch, dim, QUERY_SEED, 0)
     capi.synchronize()

@@ -61,6 +61,28 @@ def test_ten_million_by_768_per_vector_int8(gpu):
     assert_topk_equivalent(idx[sample], val[sample], ref, w["k"])
 
 
+def test_ten_million_sorted_rows_are_exact(gpu):
+    """The per-vector int8 configuration on a clustered corpus (rows sorted by their first
+    coordinate): every result is exact whether or not a query's candidate buffers overflowed
+    (overflowed queries take the device's exact fallback inside the same call)."""
+    w = bench.WORKLOADS["int8-10m-sorted"]
+    desc, corpus, queries, keep = bench.build_inputs(gpu, w)
+    idx, val, flags = gpu.search(desc)
+    print(f"queries through the exact fallback: {int(np.count_nonzero(flags))} of {w['batch']}", flush=True)
+    _ranked(idx, val, w["n"])
+    codes = corpus.to_host()
+    scales = keep["scales"].to_host()
+    assert np.all(np.diff(codes[:, 0].astype(np.int32)) >= 0), "the corpus rows are not sorted"
+    qcodes, qscales = oracle.quantize_rows_i8(queries.to_host())
+    for b in range(w["batch"]):
+        rows = idx[b]
+        exact = oracle.scores_i8i8(codes[rows], scales[rows], qcodes[b:b + 1], qscales[b:b + 1])[0]
+        assert np.array_equal(val[b], exact), f"query {b}: scores differ from the oracle's"
+    sample = [0, 3, 100, 200, 255] + [int(b) for b in np.flatnonzero(flags)[:3]]
+    ref = oracle.scores_i8i8(codes, scales, qcodes[sample], qscales[sample])
+    assert_topk_equivalent(idx[sample], val[sample], ref, w["k"])
+
+
 def test_fifty_million_binary_with_fp16_rescore(gpu):
     capi = gpu
     w = bench.WORKLOADS["binary-50m"]

@@ -107,7 +107,7 @@ void mfmaScanKernel(ScanArgs scan, PhaseArgs phase, EmitArgs emit, int q_offset,
 
     const int tid = threadIdx.x;
     const int lane = tid & (kWave - 1);
-    const int wave = tid / kWave;
+    const int wave = __builtin_amdgcn_readfirstlane(tid / kWave);  // wave-uniform: scalar indexing
     const int half = lane >> 5;
     const int col = lane & 31;
     const int batch = scan.batch;

@@ -155,7 +155,7 @@ void mfmaBinaryScanKernel(ScanArgs scan, PhaseArgs phase, EmitArgs emit, int q_o
 
     const int tid = threadIdx.x;
     const int lane = tid & (kWave - 1);
-    const int wave = tid / kWave;
+    const int wave = __builtin_amdgcn_readfirstlane(tid / kWave);  // wave-uniform: scalar indexing
     const int r16 = lane & 15;
     const int h = lane >> 4;
     const int sets = (q_count + kSetQueries - 1) / kSetQueries;
@@ -404,7 +404,8 @@ void mfmaBinaryStreamKernel(ScanArgs scan, PhaseArgs phase, EmitArgs emit, int q
 
     const int tid = threadIdx.x;
     const int lane = tid & (kWave - 1);
-    const int wave = tid / kWave;
+    // wave-uniform (a scalar register), so the pair indexing below runs on the scalar unit
+    const int wave = __builtin_amdgcn_readfirstlane(tid / kWave);
     const int r16 = lane & 15;
     const int h = lane >> 4;
     const bool two_groups = 16 < q_count;  // launch-uniform
@@ -491,9 +492,11 @@ void mfmaBinaryStreamKernel(ScanArgs scan, PhaseArgs phase, EmitArgs emit, int q
         }
     };
     // rows past the corpus re-read its last row (their keys are never emitted)
+    // (pair indices stay below 2^31: 32-bit division by the constant kPairs)
     auto loadPair = [&](long long p, u32x4 (&dst)[2][kLaneChunks]) {
-        const long long it = p / kPairs;
-        const long long row0 = phaseBlock(it, phase.stride, phase.skip) * kRows + 32 * (p % kPairs);
+        const std::uint32_t p32 = static_cast<std::uint32_t>(p);
+        const std::uint32_t it = p32 / kPairs;
+        const long long row0 = phaseBlock(it, phase.stride, phase.skip) * kRows + 32 * static_cast<int>(p32 - it * kPairs);
 #pragma unroll
         for (int b = 0; b < 2; ++b) {
             const long long row = min(row0 + 16 * b + r16, doc_count - 1);
@@ -524,9 +527,10 @@ void mfmaBinaryStreamKernel(ScanArgs scan, PhaseArgs phase, EmitArgs emit, int q
             // step by step: the compiler would otherwise hoist every step's B reads up front
             __builtin_amdgcn_sched_barrier(0);
         }
-        const long long it = p / kPairs;
+        const std::uint32_t p32 = static_cast<std::uint32_t>(p);
+        const std::uint32_t it = p32 / kPairs;
         const long long row0 = phaseBlock(it, phase.stride, phase.skip) * kRows;
-        const int pair_row = 32 * static_cast<int>(p % kPairs);
+        const int pair_row = 32 * static_cast<int>(p32 - it * kPairs);
 #pragma unroll
         for (int b = 0; b < 2; ++b) {
             if constexpr (kDense) {

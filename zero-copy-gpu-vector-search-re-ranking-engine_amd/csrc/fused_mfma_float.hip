@@ -116,7 +116,7 @@ void mfmaFloatScanKernel(ScanArgs scan, PhaseArgs phase, EmitArgs emit, int q_of
 
     const int tid = threadIdx.x;
     const int lane = tid & (kWave - 1);
-    const int wave = tid / kWave;
+    const int wave = __builtin_amdgcn_readfirstlane(tid / kWave);  // wave-uniform: scalar indexing
     const int r16 = lane & 15;
     const int h = lane >> 4;
     const int groups = (q_count + kGroupQueries - 1) / kGroupQueries;
