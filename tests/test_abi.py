@@ -154,3 +154,21 @@ def test_phase_rows_cover_the_corpus_once(capi, n, dtype, int8_mode, batch, k):
     assert len(rows) >= 2
     assert sum(rows) == n  # the phases partition the corpus
     assert all(r > 0 for r in rows)
+
+
+@pytest.mark.parametrize("with_roctx", [False, True])
+def test_trace_ranges_compile_in_and_out(tmp_path, with_roctx):
+    # include/zcgvs/core/trace_range.hpp: empty ranges by default, roctx push/pop with
+    # ZCGVS_WITH_ROCTX (the counterpart of the reference's NVTX ranges)
+    import shutil
+    import subprocess
+    if shutil.which("g++") is None:
+        pytest.skip("no host C++ compiler")
+    source = tmp_path / "ranges.cpp"
+    source.write_text('#include "zcgvs/core/trace_range.hpp"\nint f() { ZCGVS_TRACE_RANGE("zcgvs::test"); return 1; }\n')
+    flags = ["-DZCGVS_WITH_ROCTX", "-I/opt/rocm/include"] if with_roctx else []
+    if with_roctx and not Path("/opt/rocm/include/rocprofiler-sdk-roctx/roctx.h").exists():
+        pytest.skip("roctx header not installed")
+    result = subprocess.run(["g++", "-std=c++17", "-fsyntax-only", f"-I{ROOT / 'include'}", *flags, str(source)],
+                            capture_output=True, text=True)
+    assert result.returncode == 0, result.stderr

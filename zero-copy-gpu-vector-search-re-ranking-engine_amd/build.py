@@ -5,7 +5,10 @@
                              (g++; reaches the GPU only through libzcgvs_hip.so)
     zcgvs_engine*.so         pybind11 module with the reference's Python names
 
-Usage: python build.py [--jobs N] [--only hip|host|bindings]
+Usage: python build.py [--jobs N] [--only hip|host|bindings] [--roctx]
+
+--roctx (or ZCGVS_WITH_ROCTX=1) compiles the host's profiler ranges in (include/zcgvs/core/
+trace_range.hpp) and links librocprofiler-sdk-roctx; the default build has no profiler dependency.
 """
 
 from __future__ import annotations
@@ -26,6 +29,7 @@ LIB = PKG / "lib"
 OBJ = PKG / "_build"
 ARCH = os.environ.get("ZCGVS_OFFLOAD_ARCH", "gfx950")
 
+ROCM = os.environ.get("ROCM_PATH", "/opt/rocm")
 HIPCC = os.environ.get("HIPCC", "/opt/rocm/bin/hipcc")
 CXX = os.environ.get("CXX", "g++")
 
@@ -73,18 +77,20 @@ def build_hip(workers: int) -> Path:
     return target
 
 
-def build_host(workers: int) -> Path | None:
+def build_host(workers: int, roctx: bool = False) -> Path | None:
     sources = sorted((PKG / "host").glob("*.cpp"))
     if not sources:
         return None
     OBJ.mkdir(exist_ok=True)
     objects = [OBJ / (src.stem + ".host.o") for src in sources]
-    _compile_all([[CXX, *CXX_FLAGS, "-c", str(s), "-o", str(o)] for s, o in zip(sources, objects)],
+    trace = ["-DZCGVS_WITH_ROCTX", f"-I{ROCM}/include"] if roctx else []
+    _compile_all([[CXX, *CXX_FLAGS, *trace, "-c", str(s), "-o", str(o)] for s, o in zip(sources, objects)],
                  workers)
     target = LIB / "libzcgvs.so"
     tmp = target.with_suffix(".so.tmp")
+    trace_lib = [f"-L{ROCM}/lib", "-lrocprofiler-sdk-roctx", f"-Wl,-rpath,{ROCM}/lib"] if roctx else []
     _run([CXX, "-shared", "-fPIC", *map(str, objects), "-o", str(tmp), f"-L{LIB}", "-lzcgvs_hip",
-          "-Wl,-rpath,$ORIGIN"])
+          *trace_lib, "-Wl,-rpath,$ORIGIN"])
     os.replace(tmp, target)
     return target
 
@@ -109,13 +115,15 @@ def main(argv: list[str] | None = None) -> int:
     parser = argparse.ArgumentParser(description=__doc__, formatter_class=argparse.RawDescriptionHelpFormatter)
     parser.add_argument("--jobs", type=int, default=min(8, os.cpu_count() or 4))
     parser.add_argument("--only", choices=["hip", "host", "bindings"], default=None)
+    parser.add_argument("--roctx", action="store_true", default=os.environ.get("ZCGVS_WITH_ROCTX") == "1",
+                        help="compile the host's roctx profiler ranges in")
     args = parser.parse_args(argv)
     if shutil.which(HIPCC) is None and not Path(HIPCC).exists():
         raise SystemExit(f"hipcc not found at {HIPCC}")
     if args.only in (None, "hip"):
         print("built", build_hip(args.jobs))
     if args.only in (None, "host"):
-        built = build_host(args.jobs)
+        built = build_host(args.jobs, args.roctx)
         if built:
             print("built", built)
     if args.only in (None, "bindings"):

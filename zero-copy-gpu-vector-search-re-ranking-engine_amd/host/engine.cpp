@@ -2,6 +2,8 @@
 // src/engine/engine.cpp, over the Searcher.
 #include "zcgvs/engine/engine.hpp"
 
+#include "zcgvs/core/trace_range.hpp"
+
 #include <algorithm>
 #include <chrono>
 #include <stdexcept>
@@ -189,6 +191,7 @@ std::vector<SearchHit> Engine::assemble(const HostTopK& selection, int query, co
 BatchSearchResponse Engine::runBatch(const float* queries, int batch, const SearchOptions& options,
                                      const std::vector<std::vector<int>>& terms, double embed_ms,
                                      double tokenize_ms) const {
+    ZCGVS_TRACE_RANGE("zcgvs::searchBatch");
     const auto t_start = Clock::now();
     const std::int64_t n = corpus_.size();
     const Resolved resolved = resolve(options, n);
@@ -259,6 +262,7 @@ BatchSearchResponse Engine::searchVectors(const float* queries, int batch, int d
 
 std::vector<Candidate> Engine::retrieveVectors(const float* query, int dim, int k, Metric metric,
                                                const std::vector<int>& allow_ids) const {
+    ZCGVS_TRACE_RANGE("zcgvs::retrieve");
     std::lock_guard<std::mutex> lock(mutex_);
     if (k <= 0) {
         throw std::invalid_argument("zcgvs: k must be positive");

@@ -1,6 +1,8 @@
 // Searcher over the fused C-ABI pipeline (src/search/searcher.cpp).
 #include "zcgvs/search/searcher.hpp"
 
+#include "zcgvs/core/trace_range.hpp"
+
 #include <algorithm>
 #include <cstring>
 #include <stdexcept>
@@ -213,6 +215,7 @@ void Searcher::searchDevice(const float* device_queries, int dim, int batch, con
 
 void Searcher::run(const float* device_queries, int dim, int batch, const SearchParams& params,
                    const HipStream& stream) {
+    ZCGVS_TRACE_RANGE("zcgvs::search");
     validate(dim, batch, params, store_.docCount());
     if (lexicalEnabled(params)) {
         const std::size_t terms = static_cast<std::size_t>(batch) * static_cast<std::size_t>(params.lexical_stride);
@@ -287,6 +290,7 @@ void Searcher::run(const float* device_queries, int dim, int batch, const Search
 }
 
 HostTopK Searcher::copyResultToHost(const HipStream& stream) {
+    ZCGVS_TRACE_RANGE("zcgvs::copyResultToHost");
     if (current_k_ == 0 || current_batch_ == 0) {
         throw std::runtime_error("zcgvs: copyResultToHost called before search");
     }
