@@ -144,7 +144,7 @@ def test_descriptors_keep_their_buffers_alive(capi):
 @pytest.mark.parametrize("n,dtype,int8_mode,batch,k", [
     (10_000_000, 2, 1, 256, 100),   # per-vector int8 MFMA path
     (1_000_000, 0, 0, 64, 10),      # float32 VALU path
-    (123_457, 1, 0, 3, 10),         # ragged tail block
+    (123_457, 1, 0, 3, 40),         # ragged tail block
 ])
 def test_phase_rows_cover_the_corpus_once(capi, n, dtype, int8_mode, batch, k):
     kw = dict(n=n, dim=768 if dtype == 2 else 384, dtype=dtype, batch=batch, k=k)
@@ -154,6 +154,18 @@ def test_phase_rows_cover_the_corpus_once(capi, n, dtype, int8_mode, batch, k):
     assert len(rows) >= 2
     assert sum(rows) == n  # the phases partition the corpus
     assert all(r > 0 for r in rows)
+
+
+@pytest.mark.parametrize("n,dtype,int8_mode,batch,k", [
+    (123_457, 1, 0, 3, 10),         # float16, three queries
+    (1_000_000, 0, 0, 1, 32),       # float32, the widest selection
+    (10_000_000, 2, 1, 4, 20),      # per-vector int8 below the MFMA batch
+])
+def test_small_batches_scan_in_one_pass(capi, n, dtype, int8_mode, batch, k):
+    kw = dict(n=n, dim=768 if dtype == 2 else 384, dtype=dtype, batch=batch, k=k)
+    if int8_mode:
+        kw.update(int8_mode=1, row_scales=1 << 24)
+    assert capi.search_phase_rows(_desc(capi, **kw)) == [n]
 
 
 @pytest.mark.parametrize("with_roctx", [False, True])

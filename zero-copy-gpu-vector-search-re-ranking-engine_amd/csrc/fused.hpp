@@ -136,6 +136,23 @@ int mfmaBinaryBlockRows(const ScanArgs& scan);
 int launchMfmaBinaryScan(const ScanArgs& scan, const PhaseArgs& phase, const EmitArgs& emit,
                          int workgroups, hipStream_t stream);
 
+// Single-pass scan (single_pass.hip) for at most kSinglePassQueries queries and a selection of at
+// most a few dozen keys: each of `workgroups` workgroups writes its exact top-`width` of every
+// query to its candidate segment seg[((s * batch + q) << seg_log2) + j], j < seg_count[s * batch
+// + q], for the per-query merge. Nothing overflows.
+constexpr int kSinglePassQueries = 4;
+constexpr long long kSinglePassMergeKeys = 12288;  // candidate keys the merge gathers in LDS (topk.hip)
+struct SinglePassArgs {
+    int width = 0;
+    int workgroups = 0;
+    std::uint64_t* seg = nullptr;
+    std::uint32_t* seg_count = nullptr;
+    int seg_log2 = 0;
+};
+int singlePassWorkgroups();
+bool singlePassSupported(const ScanArgs& scan, int width);
+int launchSinglePass(const ScanArgs& scan, const SinglePassArgs& args, hipStream_t stream);
+
 // Exact device fallback (recover.hip): the top-`width` of every query whose flag is set (every
 // query with `force`) over the whole corpus, written sorted to out_keys [batch, width] and, when
 // out_index is set, as (index, score) pairs [batch, width]. The scan arguments are the VALU

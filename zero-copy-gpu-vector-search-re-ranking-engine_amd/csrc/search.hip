@@ -74,6 +74,7 @@ struct Plan {
     bool direct_scales = false;  // MFMA path without a mask: only the tail tile's scales are copied
     bool lex_sorted = false;     // hybrid with postings ascending by document: sliced BM25 stage
     bool recover = false;        // threshold phases ran: the exact fallback follows them
+    bool single_pass = false;    // a few queries, small width: one scan launch and one merge
     int width = 0;  // keys selected by the scan stage
     int block_rows = 64;
     int workgroups = 1;
@@ -332,6 +333,40 @@ Plan makePlan(const zcgvs_search_desc& d) {
             if (s2 > scratch) {
                 return fail(ZCGVS_ERR_RUNTIME, "zcgvs: rescore scratch sizing");
             }
+        }
+        plan.total = layout.total;
+        return plan;
+    }
+
+    // A few queries with a small selection and no MFMA scan: one launch streams the corpus once
+    // and keeps each workgroup's exact top-width (single_pass.hip), so neither threshold phases
+    // nor the fallback run. (Not with the test flags, which exercise the phased scan's fallback.)
+    if (!plan.use_mfma && !plan.use_mfma_float && !plan.use_mfma_binary &&
+        (d.flags & (ZCGVS_SEARCH_FORCE_EXACT_PASS | ZCGVS_SEARCH_TEST_TINY_SEGMENTS)) == 0) {
+        ScanArgs single = probe;
+        single.row_scales = plan.per_vector ? d.corpus.row_scales : nullptr;
+        single.mask = d.mask;
+        plan.single_pass = singlePassSupported(single, plan.width);
+    }
+    if (plan.single_pass) {
+        plan.workgroups = singlePassWorkgroups();
+        plan.segments = plan.workgroups;
+        plan.block_rows = 1;
+        plan.seg_log2 = ceilLog2(plan.width);
+        PhaseArgs whole;
+        whole.items = n;
+        whole.block_rows = 1;
+        whole.dense = 0;
+        plan.phases.push_back(whole);
+        if (plan.hybrid) {
+            plan.lex = layout.add(static_cast<std::size_t>(batch) * n * 4);
+            plan.lexmax = layout.add(static_cast<std::size_t>(batch) * 4);
+        }
+        plan.seg = layout.add((static_cast<std::size_t>(plan.segments) * batch << plan.seg_log2) * 8);
+        plan.segcnt = layout.add(static_cast<std::size_t>(plan.segments) * batch * 4);
+        plan.keys = layout.add(static_cast<std::size_t>(batch) * plan.width * 8);
+        if (plan.rescore) {
+            plan.rescored = layout.add(static_cast<std::size_t>(batch) * plan.width * 8);
         }
         plan.total = layout.total;
         return plan;
@@ -674,67 +709,102 @@ int searchTopk(const zcgvs_search_desc* desc, void* d_workspace, std::size_t wor
         }
         ZCGVS_LAUNCH_CHECK("merge mask");
     }
-    const ScanArgs scan = scanArgsOf(d, plan, ws);
-    if ((plan.use_mfma && !mfmaSupported(scan)) || (plan.use_mfma_float && !mfmaFloatSupported(scan)) ||
-        (plan.use_mfma_binary && !mfmaBinarySupported(scan))) {
-        return setError(ZCGVS_ERR_INVALID_ARGUMENT, "zcgvs: corpus or queries are not 16-byte aligned");
-    }
-    EmitArgs emit;
-    emit.tau = at<std::uint64_t>(ws, plan.tau);
-    emit.dense = at<std::uint64_t>(ws, plan.dense);
-    emit.dense_stride = plan.dense_stride;
-    emit.seg = plan.phases.size() > 1 ? at<std::uint64_t>(ws, plan.seg) : nullptr;
-    emit.seg_count = plan.phases.size() > 1 ? at<std::uint32_t>(ws, plan.segcnt) : nullptr;
-    emit.seg_log2 = plan.seg_log2;
     std::uint64_t* keys = at<std::uint64_t>(ws, plan.keys);
-    std::uint64_t* tau = at<std::uint64_t>(ws, plan.tau);
     std::uint32_t* overflow = at<std::uint32_t>(ws, plan.overflow);
-
-    if (phases_out != nullptr) {
-        *phases_out = static_cast<int>(plan.phases.size());
-    }
-    for (std::size_t p = 0; p < plan.phases.size(); ++p) {
-        const PhaseArgs& phase = plan.phases[p];
-        const bool timed = events != nullptr && static_cast<int>(p) < max_phases;
+    if (plan.single_pass) {
+        if (phases_out != nullptr) {
+            *phases_out = 1;
+        }
+        const bool timed = events != nullptr && max_phases > 0;
         if (timed) {
-            ZCGVS_HIP_RETURN(hipEventRecord(reinterpret_cast<hipEvent_t>(events[2 * p]), s));
+            ZCGVS_HIP_RETURN(hipEventRecord(reinterpret_cast<hipEvent_t>(events[0]), s));
         }
-        if (plan.use_mfma) {
-            status = launchMfmaScan(scan, phase, emit, plan.workgroups, s);
-        } else if (plan.use_mfma_float) {
-            status = launchMfmaFloatScan(scan, phase, emit, plan.workgroups, s);
-        } else if (plan.use_mfma_binary) {
-            status = launchMfmaBinaryScan(scan, phase, emit, plan.workgroups, s);
-        } else {
-            status = launchValuScan(scan, phase, emit, plan.workgroups, s);
-        }
+        SinglePassArgs single;
+        single.width = plan.width;
+        single.workgroups = plan.workgroups;
+        single.seg = at<std::uint64_t>(ws, plan.seg);
+        single.seg_count = at<std::uint32_t>(ws, plan.segcnt);
+        single.seg_log2 = plan.seg_log2;
+        status = launchSinglePass(recoverArgsOf(d, plan, ws), single, s);
         if (status != ZCGVS_OK) {
             return status;
         }
         if (timed) {
-            ZCGVS_HIP_RETURN(hipEventRecord(reinterpret_cast<hipEvent_t>(events[2 * p + 1]), s));
+            ZCGVS_HIP_RETURN(hipEventRecord(reinterpret_cast<hipEvent_t>(events[1]), s));
         }
         MergeInputs in;
-        if (p == 0) {
-            in.dense = emit.dense;
-            in.n_dense = phase.items * phase.block_rows;
-            in.dense_stride = plan.dense_stride;
-            in.reset_overflow = true;
-        } else {
-            in.prev = keys;
-            in.k_prev = plan.width;
-            in.seg = emit.seg;
-            in.seg_count = emit.seg_count;
-            in.n_seg = plan.segments;
-            in.seg_log2 = plan.seg_log2;
-        }
-        const bool last = p + 1 == plan.phases.size();
-        const bool write_out = last && !plan.rescore;
-        status = launchSelectMerge(in, plan.width, batch, keys, tau, overflow,
-                                   write_out ? d_out_indices : nullptr,
-                                   write_out ? d_out_values : nullptr, s);
+        in.seg = single.seg;
+        in.seg_count = single.seg_count;
+        in.n_seg = plan.segments;
+        in.seg_log2 = plan.seg_log2;
+        in.reset_overflow = true;  // (segments hold at most width keys: the flags end cleared)
+        status = launchSelectMerge(in, plan.width, batch, keys, nullptr, overflow,
+                                   plan.rescore ? nullptr : d_out_indices,
+                                   plan.rescore ? nullptr : d_out_values, s);
         if (status != ZCGVS_OK) {
             return status;
+        }
+    } else {
+        const ScanArgs scan = scanArgsOf(d, plan, ws);
+        if ((plan.use_mfma && !mfmaSupported(scan)) || (plan.use_mfma_float && !mfmaFloatSupported(scan)) ||
+            (plan.use_mfma_binary && !mfmaBinarySupported(scan))) {
+            return setError(ZCGVS_ERR_INVALID_ARGUMENT, "zcgvs: corpus or queries are not 16-byte aligned");
+        }
+        EmitArgs emit;
+        emit.tau = at<std::uint64_t>(ws, plan.tau);
+        emit.dense = at<std::uint64_t>(ws, plan.dense);
+        emit.dense_stride = plan.dense_stride;
+        emit.seg = plan.phases.size() > 1 ? at<std::uint64_t>(ws, plan.seg) : nullptr;
+        emit.seg_count = plan.phases.size() > 1 ? at<std::uint32_t>(ws, plan.segcnt) : nullptr;
+        emit.seg_log2 = plan.seg_log2;
+        std::uint64_t* tau = at<std::uint64_t>(ws, plan.tau);
+
+        if (phases_out != nullptr) {
+            *phases_out = static_cast<int>(plan.phases.size());
+        }
+        for (std::size_t p = 0; p < plan.phases.size(); ++p) {
+            const PhaseArgs& phase = plan.phases[p];
+            const bool timed = events != nullptr && static_cast<int>(p) < max_phases;
+            if (timed) {
+                ZCGVS_HIP_RETURN(hipEventRecord(reinterpret_cast<hipEvent_t>(events[2 * p]), s));
+            }
+            if (plan.use_mfma) {
+                status = launchMfmaScan(scan, phase, emit, plan.workgroups, s);
+            } else if (plan.use_mfma_float) {
+                status = launchMfmaFloatScan(scan, phase, emit, plan.workgroups, s);
+            } else if (plan.use_mfma_binary) {
+                status = launchMfmaBinaryScan(scan, phase, emit, plan.workgroups, s);
+            } else {
+                status = launchValuScan(scan, phase, emit, plan.workgroups, s);
+            }
+            if (status != ZCGVS_OK) {
+                return status;
+            }
+            if (timed) {
+                ZCGVS_HIP_RETURN(hipEventRecord(reinterpret_cast<hipEvent_t>(events[2 * p + 1]), s));
+            }
+            MergeInputs in;
+            if (p == 0) {
+                in.dense = emit.dense;
+                in.n_dense = phase.items * phase.block_rows;
+                in.dense_stride = plan.dense_stride;
+                in.reset_overflow = true;
+            } else {
+                in.prev = keys;
+                in.k_prev = plan.width;
+                in.seg = emit.seg;
+                in.seg_count = emit.seg_count;
+                in.n_seg = plan.segments;
+                in.seg_log2 = plan.seg_log2;
+            }
+            const bool last = p + 1 == plan.phases.size();
+            const bool write_out = last && !plan.rescore;
+            status = launchSelectMerge(in, plan.width, batch, keys, tau, overflow,
+                                       write_out ? d_out_indices : nullptr,
+                                       write_out ? d_out_values : nullptr, s);
+            if (status != ZCGVS_OK) {
+                return status;
+            }
         }
     }
 
