@@ -5,9 +5,10 @@
 //
 // Two streaming kernels over buffers far larger than the last-level cache: a read that folds
 // every 16-byte chunk into a per-thread xor (one word per workgroup is written, so the loads
-// cannot be dropped) and a copy. Both use nontemporal 16-byte accesses, four in flight per
-// thread per iteration, and a grid-stride loop; each is launched at a few grid sizes and the
-// best timed launch counts.
+// cannot be dropped) and a copy. Both use nontemporal 16-byte accesses, eight in flight per
+// thread per iteration, in two access orders (each workgroup reading contiguous 32 KiB spans,
+// or each thread's loads spread over the grid); each order is launched at a few grid sizes and
+// the best timed launch counts.
 #include <hip/hip_runtime.h>
 
 #include <algorithm>
@@ -21,26 +22,43 @@ namespace {
 typedef unsigned int u32x4v __attribute__((ext_vector_type(4)));
 
 constexpr int kProbeThreads = 256;
-constexpr int kProbeUnroll = 4;
+constexpr int kProbeUnroll = 8;
 
+// Chunk index of load u of this thread in span `span`: with kBlocked, a workgroup's kProbeUnroll
+// loads cover one contiguous span of kProbeUnroll * kProbeThreads chunks (each wavefront reads
+// 1 KiB runs of one 32 KiB span); otherwise the loads of one thread stride the whole grid apart.
+template <bool kBlocked>
+__device__ inline std::size_t probeIndex(std::size_t span, int u) {
+    if (kBlocked) {
+        return (span * gridDim.x + blockIdx.x) * (kProbeUnroll * kProbeThreads) +
+               static_cast<std::size_t>(u) * kProbeThreads + threadIdx.x;
+    }
+    return span * (static_cast<std::size_t>(gridDim.x) * kProbeThreads * kProbeUnroll) +
+           static_cast<std::size_t>(u) * gridDim.x * kProbeThreads +
+           static_cast<std::size_t>(blockIdx.x) * kProbeThreads + threadIdx.x;
+}
+
+template <bool kBlocked>
 __global__ __launch_bounds__(kProbeThreads) void probeReadKernel(const u32x4v* __restrict__ src,
                                                                  std::size_t chunks,
                                                                  std::uint32_t* __restrict__ sink) {
-    const std::size_t stride = static_cast<std::size_t>(gridDim.x) * kProbeThreads;
-    std::size_t i = static_cast<std::size_t>(blockIdx.x) * kProbeThreads + threadIdx.x;
+    // every span is whole: the grid reads spans [0, spans) of kProbeUnroll * grid threads chunks
+    const std::size_t per_span = static_cast<std::size_t>(gridDim.x) * kProbeThreads * kProbeUnroll;
+    const std::size_t spans = chunks / per_span;
     u32x4v acc = {0u, 0u, 0u, 0u};
-    for (; i + (kProbeUnroll - 1) * stride < chunks; i += kProbeUnroll * stride) {
+    for (std::size_t span = 0; span < spans; ++span) {
         u32x4v v[kProbeUnroll];
 #pragma unroll
         for (int u = 0; u < kProbeUnroll; ++u) {
-            v[u] = __builtin_nontemporal_load(src + i + u * stride);
+            v[u] = __builtin_nontemporal_load(src + probeIndex<kBlocked>(span, u));
         }
 #pragma unroll
         for (int u = 0; u < kProbeUnroll; ++u) {
             acc ^= v[u];
         }
     }
-    for (; i < chunks; i += stride) {
+    for (std::size_t i = spans * per_span + static_cast<std::size_t>(blockIdx.x) * kProbeThreads + threadIdx.x;
+         i < chunks; i += static_cast<std::size_t>(gridDim.x) * kProbeThreads) {
         acc ^= __builtin_nontemporal_load(src + i);
     }
     std::uint32_t word = acc.x ^ acc.y ^ acc.z ^ acc.w;
@@ -62,23 +80,25 @@ __global__ __launch_bounds__(kProbeThreads) void probeReadKernel(const u32x4v* _
     }
 }
 
+template <bool kBlocked>
 __global__ __launch_bounds__(kProbeThreads) void probeCopyKernel(const u32x4v* __restrict__ src,
                                                                  u32x4v* __restrict__ dst,
                                                                  std::size_t chunks) {
-    const std::size_t stride = static_cast<std::size_t>(gridDim.x) * kProbeThreads;
-    std::size_t i = static_cast<std::size_t>(blockIdx.x) * kProbeThreads + threadIdx.x;
-    for (; i + (kProbeUnroll - 1) * stride < chunks; i += kProbeUnroll * stride) {
+    const std::size_t per_span = static_cast<std::size_t>(gridDim.x) * kProbeThreads * kProbeUnroll;
+    const std::size_t spans = chunks / per_span;
+    for (std::size_t span = 0; span < spans; ++span) {
         u32x4v v[kProbeUnroll];
 #pragma unroll
         for (int u = 0; u < kProbeUnroll; ++u) {
-            v[u] = __builtin_nontemporal_load(src + i + u * stride);
+            v[u] = __builtin_nontemporal_load(src + probeIndex<kBlocked>(span, u));
         }
 #pragma unroll
         for (int u = 0; u < kProbeUnroll; ++u) {
-            __builtin_nontemporal_store(v[u], dst + i + u * stride);
+            __builtin_nontemporal_store(v[u], dst + probeIndex<kBlocked>(span, u));
         }
     }
-    for (; i < chunks; i += stride) {
+    for (std::size_t i = spans * per_span + static_cast<std::size_t>(blockIdx.x) * kProbeThreads + threadIdx.x;
+         i < chunks; i += static_cast<std::size_t>(gridDim.x) * kProbeThreads) {
         __builtin_nontemporal_store(__builtin_nontemporal_load(src + i), dst + i);
     }
 }
@@ -150,30 +170,41 @@ int zcgvs_measure_hbm_bandwidth(std::size_t bytes, int iterations, double* read_
     ZCGVS_LAUNCH_CHECK("probe fill");
     double best_read = 0.0;
     double best_copy = 0.0;
-    for (int g : grids) {
+    // one timed launch of `launch` per iteration after a warm-up; the best rate counts
+    auto timeBest = [&](auto&& launch, double bytes_moved, double* best) -> int {
         for (int it = 0; it <= iterations; ++it) {  // the first launch of each shape is a warm-up
             ZCGVS_HIP_RETURN(hipEventRecord(r.begin, r.stream));
-            probeReadKernel<<<g, kProbeThreads, 0, r.stream>>>(src, chunks, static_cast<std::uint32_t*>(r.sink));
-            ZCGVS_LAUNCH_CHECK("probe read");
+            launch();
+            ZCGVS_LAUNCH_CHECK("bandwidth probe");
             ZCGVS_HIP_RETURN(hipEventRecord(r.end, r.stream));
             ZCGVS_HIP_RETURN(hipEventSynchronize(r.end));
             float ms = 0.0f;
             ZCGVS_HIP_RETURN(hipEventElapsedTime(&ms, r.begin, r.end));
             if (it > 0 && ms > 0.0f) {
-                best_read = std::max(best_read, static_cast<double>(used) / (ms * 1e-3) / 1e9);
+                *best = std::max(*best, bytes_moved / (ms * 1e-3) / 1e9);
             }
         }
-        for (int it = 0; it <= iterations; ++it) {
-            ZCGVS_HIP_RETURN(hipEventRecord(r.begin, r.stream));
-            probeCopyKernel<<<g, kProbeThreads, 0, r.stream>>>(src, dst, chunks);
-            ZCGVS_LAUNCH_CHECK("probe copy");
-            ZCGVS_HIP_RETURN(hipEventRecord(r.end, r.stream));
-            ZCGVS_HIP_RETURN(hipEventSynchronize(r.end));
-            float ms = 0.0f;
-            ZCGVS_HIP_RETURN(hipEventElapsedTime(&ms, r.begin, r.end));
-            if (it > 0 && ms > 0.0f) {
-                best_copy = std::max(best_copy, 2.0 * static_cast<double>(used) / (ms * 1e-3) / 1e9);
-            }
+        return ZCGVS_OK;
+    };
+    auto* sink = static_cast<std::uint32_t*>(r.sink);
+    const double once = static_cast<double>(used);
+    for (int g : grids) {
+        int status = timeBest([&] { probeReadKernel<false><<<g, kProbeThreads, 0, r.stream>>>(src, chunks, sink); },
+                              once, &best_read);
+        if (status == ZCGVS_OK) {
+            status = timeBest([&] { probeReadKernel<true><<<g, kProbeThreads, 0, r.stream>>>(src, chunks, sink); },
+                              once, &best_read);
+        }
+        if (status == ZCGVS_OK) {
+            status = timeBest([&] { probeCopyKernel<false><<<g, kProbeThreads, 0, r.stream>>>(src, dst, chunks); },
+                              2.0 * once, &best_copy);
+        }
+        if (status == ZCGVS_OK) {
+            status = timeBest([&] { probeCopyKernel<true><<<g, kProbeThreads, 0, r.stream>>>(src, dst, chunks); },
+                              2.0 * once, &best_copy);
+        }
+        if (status != ZCGVS_OK) {
+            return status;
         }
     }
     *read_gbs = best_read;

@@ -4,8 +4,13 @@
 //   1. query preparation: sign packing for a binary corpus (searcher.cpp:215-218), per-row int8
 //      quantization for the per-vector int8 mode;
 //   2. optional BM25 scores and their per-query maximum (hybrid, searcher.cpp:235-259);
-//   3. phased scan-and-filter (fused.hpp) with a per-query merge after every phase; the scan
-//      selects `width` = rescore_candidates (rescore on) or k keys per query;
+//   3. the scan selects `width` = rescore_candidates (rescore on) or k keys per query, either
+//      - in one pass (single_pass.hip: at most 4 queries, width <= 32, no MFMA scan applies):
+//        per-workgroup exact top-width lists, then one merge; or
+//      - in phases (fused.hpp): a dense sample, then threshold phases that emit only keys above
+//        the running threshold, with a per-query merge after every phase, followed by the exact
+//        fallback (recover.hip) for any query whose candidate segments overflowed, so the result
+//        is exact for every input;
 //   4. optional exact gather rescore of those candidates and a final top-k, whose keys carry the
 //      corpus id, which subsumes the reference's remap (searcher.cpp:261-278).
 //
