@@ -181,6 +181,8 @@ def measured_traffic(workload, kernel):
 def scan_kernel_name(w):
     if w["kind"] == "i8i8" and w["batch"] >= 8:
         return f"mfmaScanKernel<{w['dim'] // 32}, false>"
+    if w["kind"] == "f32" and w["batch"] >= 32 and w["dim"] in (256, 384):
+        return f"mfmaSplitScanKernel<{w['dim']}, false>"
     if w["kind"] in ("f32", "f16", "hybrid") and w["batch"] >= 4 and w["dim"] in (128, 256, 384, 512):
         kind = 0 if w["kind"] == "f32" else 1
         lexical = "true" if w["kind"] == "hybrid" else "false"

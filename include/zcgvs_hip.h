@@ -305,7 +305,10 @@ size_t zcgvs_search_workspace_bytes(const zcgvs_search_desc* desc);
  * threshold in bounded per-workgroup buffers, and a query whose buffers overflowed (a corpus whose
  * best rows crowd into a few blocks) is recomputed on the device, in the same call and stream,
  * by an exact fallback that selects over recomputed scores (one workgroup per such query, a few
- * corpus reads). zcgvs_search_overflow_flags tells which queries took that path. */
+ * corpus reads). zcgvs_search_overflow_flags tells which queries took that path. A search of at
+ * most four queries selecting at most 32 keys each (k, or rescore_candidates with a rescore store)
+ * that no matrix-core scan takes reads the corpus in a single pass whose per-workgroup lists are
+ * exact; it never overflows. */
 int zcgvs_search_topk(const zcgvs_search_desc* desc, void* d_workspace, size_t workspace_bytes,
                       int* d_out_indices, float* d_out_values, zcgvs_stream_t stream);
 

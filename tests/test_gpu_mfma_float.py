@@ -1,10 +1,12 @@
 """Batched float32 / float16 searches (the matrix-core scan) against the CPU oracle.
 
 Batches of 4 or more queries over float32 or float16 rows of 128, 256, 384 or 512 dims take the
-MFMA scan; these cases cover every such row size, partial query groups (17), a batch over two
-launches (130), a partial last tile (n not a multiple of the tile rows), k = 1 and k = 100, both
-metrics, and query magnitudes far from 1 (the float16 path rescales each query by a power of two
-before splitting it). Ids must match the oracle's except at near-ties within the float32
+MFMA scan; launches of 32 to 128 queries over float32 rows of 256 or 384 dims take its bf16
+three-part split form. These cases cover every such row size, partial query groups (17, 33, 40),
+a batch over two launches (130: a split launch of 128 and a float32 launch of 2), a partial last
+tile (n not a multiple of the tile rows), k = 1 and k = 100, both metrics, query magnitudes far
+from 1 (the float16 path rescales each query by a power of two before splitting it), and rows
+whose components span thirty binary orders of magnitude (every part of the bf16 split matters). Ids must match the oracle's except at near-ties within the float32
 tolerance, and every score must be within it."""
 
 import numpy as np
@@ -33,6 +35,9 @@ CASES = [
     ("f32", 100_003, 384, 64, 100, 1, 1.0),
     ("f32", 100_003, 384, 130, 10, 0, 1.0),
     ("f32", 60_013, 512, 33, 1, 0, 1.0),
+    ("f32", 60_013, 256, 32, 10, 0, 1.0),
+    ("f32", 100_003, 384, 40, 10, 1, 1000.0),
+    ("f32", 100_003, 384, 48, 10, 0, 1e-3),
     ("f16", 60_013, 128, 17, 10, 0, 1.0),
     ("f16", 60_013, 256, 17, 10, 1, 1.0),
     ("f16", 100_003, 384, 4, 10, 0, 1.0),
@@ -80,3 +85,18 @@ def test_batched_float_scan_ties(gpu):
                 members = idx[b][classes == c]
                 lowest = c + 1000 * np.arange(len(members))
                 assert np.array_equal(members, lowest), f"{kind} query {b}: class {c} ids {members}"
+
+
+@pytest.mark.parametrize("dim,batch", [(256, 64), (384, 96)])
+def test_split_scan_wide_dynamic_range(gpu, dim, batch):
+    """Rows and queries whose components are scaled by 2^-30 .. 2^0 (per component): the bf16
+    split must carry the low parts of every value, or the scores miss the float32 tolerance."""
+    capi = gpu
+    n, k = 80_021, 20
+    rng = np.random.default_rng(dim + batch)
+    corpus = normalized(n, dim, 300 + dim) * np.exp2(rng.integers(-30, 1, size=(n, dim))).astype(np.float32)
+    queries = normalized(batch, dim, 400 + dim) * np.exp2(rng.integers(-30, 1, size=(batch, dim))).astype(np.float32)
+    corpus, queries = corpus.astype(np.float32), queries.astype(np.float32)
+    idx, val = search(capi, corpus, capi.F32, queries, k, 1)
+    ref = oracle.scores_f32(corpus, queries, 1)
+    assert_topk_equivalent(idx, val, ref, k, float_tolerance(queries, corpus, 1))

@@ -129,6 +129,13 @@ int mfmaFloatBlockRows(const ScanArgs& scan);
 int launchMfmaFloatScan(const ScanArgs& scan, const PhaseArgs& phase, const EmitArgs& emit,
                         int workgroups, hipStream_t stream);
 
+// The float32 scan on the bf16 matrix cores (fused_mfma_split.hip): three-part bf16 splits of
+// rows and queries, for launches of 32 to 128 queries over rows of 256 or 384 dims (32-row
+// tiles, as the float MFMA scan uses at those sizes); launchMfmaFloatScan hands it those launches.
+bool mfmaSplitSupported(const ScanArgs& scan, int queries_in_launch);
+int launchMfmaSplitScan(const ScanArgs& scan, const PhaseArgs& phase, const EmitArgs& emit, int workgroups,
+                        int q0, int count, hipStream_t stream);
+
 // The binary (Hamming) MFMA scan (batches of at least 4 queries, no mask or lexical scores,
 // dim 512 or 1024).
 bool mfmaBinarySupported(const ScanArgs& scan);

@@ -365,6 +365,17 @@ int launchQueries(const ScanArgs& scan, const PhaseArgs& phase, const EmitArgs& 
     const int per_launch = kLex ? kLexQueries : kQueriesPerLaunch;
     for (int q0 = 0; q0 < scan.batch; q0 += per_launch) {
         const int count = std::min(per_launch, scan.batch - q0);
+        if (kKind == ZCGVS_DTYPE_F32 && !kLex && mfmaSplitSupported(scan, count)) {
+            // float32 rows against 32 or more queries: the bf16 three-part split scan, whose
+            // 32-row tiles and emission are this kernel's
+            static_assert(kKind != ZCGVS_DTYPE_F32 || kDim < 256 || kDim > 384 || FloatTile<kKind, kDim>::kRows == 32,
+                          "the split scan uses 32-row tiles");
+            const int status = launchMfmaSplitScan(scan, phase, emit, static_cast<int>(grid.x), q0, count, stream);
+            if (status != ZCGVS_OK) {
+                return status;
+            }
+            continue;
+        }
         if (phase.dense) {
             mfmaFloatScanKernel<kKind, kDim, true, kLex><<<grid, kThreads, 0, stream>>>(scan, phase, emit, q0, count);
         } else {
