@@ -191,7 +191,7 @@ def scan_kernel_name(w):
         # up to 32 queries per launch: the streaming kernel; more: the shared-tile kernel
         name = "mfmaBinaryStreamKernel" if w["batch"] <= 32 else "mfmaBinaryScanKernel"
         return f"{name}<{w['dim'] // 32}, false>"
-    if w["batch"] <= 4 and w.get("candidates", w["k"]) <= 32:
+    if w["batch"] <= 4:
         return "singlePassScanKernel"
     return "valuScanKernel"
 

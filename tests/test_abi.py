@@ -144,7 +144,7 @@ def test_descriptors_keep_their_buffers_alive(capi):
 @pytest.mark.parametrize("n,dtype,int8_mode,batch,k", [
     (10_000_000, 2, 1, 256, 100),   # per-vector int8 MFMA path
     (1_000_000, 0, 0, 64, 10),      # float32 VALU path
-    (123_457, 1, 0, 3, 40),         # ragged tail block
+    (123_457, 1, 0, 5, 40),         # ragged tail block
 ])
 def test_phase_rows_cover_the_corpus_once(capi, n, dtype, int8_mode, batch, k):
     kw = dict(n=n, dim=768 if dtype == 2 else 384, dtype=dtype, batch=batch, k=k)
@@ -158,8 +158,9 @@ def test_phase_rows_cover_the_corpus_once(capi, n, dtype, int8_mode, batch, k):
 
 @pytest.mark.parametrize("n,dtype,int8_mode,batch,k", [
     (123_457, 1, 0, 3, 10),         # float16, three queries
-    (1_000_000, 0, 0, 1, 32),       # float32, the widest selection
-    (10_000_000, 2, 1, 4, 20),      # per-vector int8 below the MFMA batch
+    (1_000_000, 0, 0, 1, 32),       # float32
+    (10_000_000, 2, 1, 4, 100),     # per-vector int8 below the MFMA batch, merged in groups
+    (50_000_000, 3, 0, 1, 1000),    # binary, the widest selection the merges take
 ])
 def test_small_batches_scan_in_one_pass(capi, n, dtype, int8_mode, batch, k):
     kw = dict(n=n, dim=768 if dtype == 2 else 384, dtype=dtype, batch=batch, k=k)

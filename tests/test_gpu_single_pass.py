@@ -1,14 +1,16 @@
 """The single-pass scan of the fused search (single_pass.hip) against the oracle.
 
-A search of at most four queries whose selection (k, or the rescore candidates C) is at most 32
-and that no MFMA scan takes is one streaming launch plus one merge: every workgroup keeps its
-exact top-width per query in LDS and the merge selects the global top-width from those lists.
+A search of at most four queries that no MFMA scan takes is one streaming launch plus one merge
+(two for wide selections: groups of workgroup lists first): every workgroup keeps its exact
+top-width per query (k, or the rescore candidates C, up to 1024) in LDS and the merges select the
+global top-width from those lists.
 Each case checks that this path ran (one phase over the whole corpus) and that the result is the
 oracle's top-k: bit for bit for the integer kinds (Hamming, per-vector int8) and for exactly
 representable scores, to the float32 summation tolerance otherwise. The corpora include the
 ones that stress the per-workgroup lists: ascending scores (every row beats the running
 threshold, so the lists compact at every check), all-equal scores (lowest indices across
-workgroup boundaries), fewer rows than workgroups, and masks that leave fewer live rows than k."""
+workgroup boundaries), fewer rows than workgroups, masks that leave fewer live rows than k, and
+selections of 100 to 1024 keys, which compact their lists repeatedly and merge in groups."""
 
 from __future__ import annotations
 
@@ -245,16 +247,102 @@ def test_integer_kinds_match_the_phased_scan(gpu):
 
 
 def test_selection_limits(gpu):
-    """k = 32 with four queries is the widest single pass; k = 33, five queries, and the test
-    flags take the phased scan. (A dimension the MFMA float scan does not take, which would take
-    four unmasked queries of 128 to 512 dimensions.)"""
+    """Four queries and k = 1024 is the widest single pass; five queries and the test flags take
+    the phased scan. (A dimension the MFMA float scan does not take, which would take four
+    unmasked queries of 128 to 512 dimensions.)"""
     capi = gpu
     n, dim = 50_000, 64
     d_corpus = capi.DeviceArray.from_host(normalized(n, dim, 201))
     d_q = capi.DeviceArray.from_host(normalized(5, dim, 202))
     store = capi.store_desc(d_corpus, n, dim, capi.F32)
     assert capi.search_phase_rows(capi.search_desc(store, d_q, 4, 32)) == [n]
-    assert capi.search_phase_rows(capi.search_desc(store, d_q, 1, 33)) != [n]
+    assert capi.search_phase_rows(capi.search_desc(store, d_q, 4, 1024)) == [n]
     assert capi.search_phase_rows(capi.search_desc(store, d_q, 5, 10)) != [n]
     for flag in (capi.SEARCH_FORCE_EXACT_PASS, capi.SEARCH_TEST_TINY_SEGMENTS):
         assert capi.search_phase_rows(capi.search_desc(store, d_q, 1, 10, flags=flag)) != [n]
+
+
+@pytest.mark.parametrize("batch,k,masked", [(1, 100, False), (2, 333, True), (4, 1024, False)])
+def test_wide_selections_float32(gpu, batch, k, masked):
+    # (96 dimensions: the MFMA float scan, which takes four unmasked queries of 128 to 512
+    # dimensions, does not take them)
+    capi = gpu
+    n, dim = 400_009, 96
+    corpus, queries = normalized(n, dim, 211), normalized(batch, dim, 212)
+    mask = (np.random.default_rng(213).random(n) > 0.5).astype(np.uint8) if masked else None
+    desc = capi.search_desc(capi.store_desc(capi.DeviceArray.from_host(corpus), n, dim, capi.F32),
+                            capi.DeviceArray.from_host(queries), batch, k, oracle.L2 if masked else oracle.DOT,
+                            mask=capi.DeviceArray.from_host(mask) if masked else None)
+    idx, val = _single(capi, desc, n)
+    metric = oracle.L2 if masked else oracle.DOT
+    ref = oracle.scores_f32(corpus, queries, metric, mask)
+    assert_topk_equivalent(idx, val, ref, k, float_tolerance(queries, corpus, metric))
+
+
+def test_wide_selection_int8_per_vector_bit_exact(gpu):
+    capi = gpu
+    n, dim, batch, k = 500_000, 768, 1, 100
+    codes, scales = oracle.quantize_rows_i8(normalized(n, dim, 221))
+    queries = normalized(batch, dim, 222)
+    desc = capi.search_desc(capi.store_desc(capi.DeviceArray.from_host(codes), n, dim, capi.I8, 1.0,
+                                            capi.DeviceArray.from_host(scales)),
+                            capi.DeviceArray.from_host(queries), batch, k, int8_mode=capi.INT8_PER_VECTOR)
+    idx, val = _single(capi, desc, n)
+    qcodes, qscales = oracle.quantize_rows_i8(queries)
+    assert_topk_equivalent(idx, val, oracle.scores_i8i8(codes, scales, qcodes, qscales), k)
+
+
+def test_wide_binary_with_ties_and_rescore(gpu):
+    """Hamming top-1000 over 64 repeated sign patterns (the top-1000 ends inside a tie of
+    thousands of rows: lowest indices, bit for bit), then the float16 rescore of those 1000."""
+    capi = gpu
+    n, dim, batch, k, c = 300_000, 1024, 1, 10, 1000
+    base = normalized(64, dim, 231)
+    rows = base[np.random.default_rng(232).integers(0, 64, n)] + 1e-3 * normalized(n, dim, 233)
+    words, half = oracle.pack_binary(rows), oracle.f32_to_f16(rows)
+    queries = normalized(batch, dim, 234)
+    d_words, d_q = capi.DeviceArray.from_host(words), capi.DeviceArray.from_host(queries)
+    stage1 = capi.search_desc(capi.store_desc(d_words, n, dim, capi.BINARY), d_q, batch, c)
+    cand, cand_val = _single(capi, stage1, n)
+    assert_topk_equivalent(cand, cand_val, oracle.scores_hamming(words, oracle.pack_binary(queries), dim), c)
+    full = capi.search_desc(capi.store_desc(d_words, n, dim, capi.BINARY), d_q, batch, k,
+                            rescore=capi.store_desc(capi.DeviceArray.from_host(half), n, dim, capi.F16),
+                            rescore_candidates=c)
+    idx, val = _single(capi, full, n)
+    decoded = half.astype(np.float32)
+    rescored = oracle.rescore(decoded, queries, cand)
+    local, ref_val = oracle.topk(rescored, k)
+    tol = float_tolerance(queries, decoded[cand[0]], 0)
+    for r in range(k):
+        g, e = int(idx[0, r]), int(cand[0, local[0, r]])
+        assert g in set(cand[0].tolist())
+        if g != e:
+            pos = int(np.flatnonzero(cand[0] == g)[0])
+            assert abs(float(rescored[0, pos]) - float(ref_val[0, r])) <= tol[0, pos] + tol[0, local[0, r]]
+
+
+@pytest.mark.parametrize("ascending", [True, False])
+def test_wide_monotone_scores(gpu, ascending):
+    """Ascending scores append every row to every list: with k = 1000 each list compacts many
+    times and the merges see full groups."""
+    capi = gpu
+    n, dim, k = 600_000, 64, 1000
+    corpus, query = _ramp(n, dim, ascending)
+    desc = capi.search_desc(capi.store_desc(capi.DeviceArray.from_host(corpus), n, dim, capi.F32),
+                            capi.DeviceArray.from_host(query), 1, k, oracle.DOT)
+    idx, val = _single(capi, desc, n)
+    expected = list(range(n - 1, n - 1 - k, -1)) if ascending else list(range(k))
+    assert idx[0].tolist() == expected
+    assert_topk_equivalent(idx, val, oracle.scores_f32(corpus, query, oracle.DOT), k)
+
+
+def test_wide_selection_small_corpus(gpu):
+    """1,500 rows and k = 1,000: most workgroups hold a handful of rows, the groups' merges see
+    mostly empty segments."""
+    capi = gpu
+    n, dim, k = 1_500, 128, 1_000
+    corpus, queries = normalized(n, dim, 241), normalized(3, dim, 242)
+    desc = capi.search_desc(capi.store_desc(capi.DeviceArray.from_host(corpus), n, dim, capi.F32),
+                            capi.DeviceArray.from_host(queries), 3, k)
+    idx, val = _single(capi, desc, n)
+    assert_topk_equivalent(idx, val, oracle.scores_f32(corpus, queries), k, float_tolerance(queries, corpus, 0))

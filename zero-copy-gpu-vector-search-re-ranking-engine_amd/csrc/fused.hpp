@@ -144,19 +144,32 @@ int launchMfmaBinaryScan(const ScanArgs& scan, const PhaseArgs& phase, const Emi
                          int workgroups, hipStream_t stream);
 
 // Single-pass scan (single_pass.hip) for at most kSinglePassQueries queries and a selection of at
-// most a few dozen keys: each of `workgroups` workgroups writes its exact top-`width` of every
-// query to its candidate segment seg[((s * batch + q) << seg_log2) + j], j < seg_count[s * batch
-// + q], for the per-query merge. Nothing overflows.
+// most kMaxK keys: each of `workgroups` workgroups writes its exact top-`width` of every query to
+// a candidate segment. Workgroup b is segment s = b / groups of merge query q * groups + b %
+// groups, i.e. seg[((s * batch * groups + q * groups + b % groups) << seg_log2) + j], j <
+// seg_count[s * batch * groups + q * groups + b % groups], so one selectMerge over the batch *
+// groups merge queries (workgroups / groups segments each) takes every group's top-width, and
+// with groups > 1 merges of up to 8 neighbouring group results at a time finish. Nothing
+// overflows.
 constexpr int kSinglePassQueries = 4;
 constexpr long long kSinglePassMergeKeys = 12288;  // candidate keys the merge gathers in LDS (topk.hip)
 struct SinglePassArgs {
     int width = 0;
     int workgroups = 0;
+    int cap = 0;     // LDS list keys per query (singlePassShape)
+    int groups = 1;  // merge groups (singlePassShape)
     std::uint64_t* seg = nullptr;
     std::uint32_t* seg_count = nullptr;
     int seg_log2 = 0;
 };
-int singlePassWorkgroups();
+struct SinglePassShape {
+    bool supported = false;
+    int workgroups = 0;
+    int cap = 0;
+    int groups = 1;
+    int seg_log2 = 0;
+};
+SinglePassShape singlePassShape(const ScanArgs& scan, int width);
 bool singlePassSupported(const ScanArgs& scan, int width);
 int launchSinglePass(const ScanArgs& scan, const SinglePassArgs& args, hipStream_t stream);
 

@@ -5,8 +5,8 @@
 //      quantization for the per-vector int8 mode;
 //   2. optional BM25 scores and their per-query maximum (hybrid, searcher.cpp:235-259);
 //   3. the scan selects `width` = rescore_candidates (rescore on) or k keys per query, either
-//      - in one pass (single_pass.hip: at most 4 queries, width <= 32, no MFMA scan applies):
-//        per-workgroup exact top-width lists, then one merge; or
+//      - in one pass (single_pass.hip: at most 4 queries, no MFMA scan applies): per-workgroup
+//        exact top-width lists, then one merge (two for wide selections); or
 //      - in phases (fused.hpp): a dense sample, then threshold phases that emit only keys above
 //        the running threshold, with a per-query merge after every phase, followed by the exact
 //        fallback (recover.hip) for any query whose candidate segments overflowed, so the result
@@ -79,7 +79,9 @@ struct Plan {
     bool direct_scales = false;  // MFMA path without a mask: only the tail tile's scales are copied
     bool lex_sorted = false;     // hybrid with postings ascending by document: sliced BM25 stage
     bool recover = false;        // threshold phases ran: the exact fallback follows them
-    bool single_pass = false;    // a few queries, small width: one scan launch and one merge
+    bool single_pass = false;    // a few queries: one scan launch and one or two merges
+    int sp_cap = 0;              // single pass: LDS list keys per query
+    int sp_groups = 1;           // single pass: merge groups (a second merge when above 1)
     int width = 0;  // keys selected by the scan stage
     int block_rows = 64;
     int workgroups = 1;
@@ -92,7 +94,7 @@ struct Plan {
     std::size_t mscales = 0;  // MFMA path: row scales padded to whole tiles, NaN = masked/padding
     std::size_t qbits = 0, qi8 = 0, qscale = 0, lex = 0, lexmax = 0, dense = 0, seg = 0,
                 segcnt = 0, keys = 0, tau = 0, overflow = 0, rescored = 0, scores = 0, lexmat = 0,
-                topk_a = 0, topk_b = 0, topk_c = 0, topk_d = 0, cand_idx = 0, cand_val = 0,
+                topk_a = 0, topk_b = 0, topk_c = 0, topk_d = 0, cand_idx = 0, cand_val = 0, sp_level = 0,
                 local_idx = 0, rescore_val = 0, lexmax_m = 0, lexbounds = 0;
     std::size_t total = 0;
 };
@@ -343,21 +345,25 @@ Plan makePlan(const zcgvs_search_desc& d) {
         return plan;
     }
 
-    // A few queries with a small selection and no MFMA scan: one launch streams the corpus once
-    // and keeps each workgroup's exact top-width (single_pass.hip), so neither threshold phases
-    // nor the fallback run. (Not with the test flags, which exercise the phased scan's fallback.)
+    // A few queries and no MFMA scan: one launch streams the corpus once and keeps each
+    // workgroup's exact top-width (single_pass.hip), so neither threshold phases nor the fallback
+    // run. (Not with the test flags, which exercise the phased scan's fallback.)
+    SinglePassShape single_shape;
     if (!plan.use_mfma && !plan.use_mfma_float && !plan.use_mfma_binary &&
         (d.flags & (ZCGVS_SEARCH_FORCE_EXACT_PASS | ZCGVS_SEARCH_TEST_TINY_SEGMENTS)) == 0) {
         ScanArgs single = probe;
         single.row_scales = plan.per_vector ? d.corpus.row_scales : nullptr;
         single.mask = d.mask;
-        plan.single_pass = singlePassSupported(single, plan.width);
+        single_shape = singlePassShape(single, plan.width);
+        plan.single_pass = single_shape.supported;
     }
     if (plan.single_pass) {
-        plan.workgroups = singlePassWorkgroups();
+        plan.workgroups = single_shape.workgroups;
         plan.segments = plan.workgroups;
         plan.block_rows = 1;
-        plan.seg_log2 = ceilLog2(plan.width);
+        plan.seg_log2 = single_shape.seg_log2;
+        plan.sp_cap = single_shape.cap;
+        plan.sp_groups = single_shape.groups;
         PhaseArgs whole;
         whole.items = n;
         whole.block_rows = 1;
@@ -369,6 +375,10 @@ Plan makePlan(const zcgvs_search_desc& d) {
         }
         plan.seg = layout.add((static_cast<std::size_t>(plan.segments) * batch << plan.seg_log2) * 8);
         plan.segcnt = layout.add(static_cast<std::size_t>(plan.segments) * batch * 4);
+        if (plan.sp_groups > 1) {
+            // two buffers of every (query, group) result, merged 8 groups at a time in turn
+            plan.sp_level = layout.add(2 * static_cast<std::size_t>(batch) * plan.sp_groups * plan.width * 8);
+        }
         plan.keys = layout.add(static_cast<std::size_t>(batch) * plan.width * 8);
         if (plan.rescore) {
             plan.rescored = layout.add(static_cast<std::size_t>(batch) * plan.width * 8);
@@ -727,6 +737,8 @@ int searchTopk(const zcgvs_search_desc* desc, void* d_workspace, std::size_t wor
         SinglePassArgs single;
         single.width = plan.width;
         single.workgroups = plan.workgroups;
+        single.cap = plan.sp_cap;
+        single.groups = plan.sp_groups;
         single.seg = at<std::uint64_t>(ws, plan.seg);
         single.seg_count = at<std::uint32_t>(ws, plan.segcnt);
         single.seg_log2 = plan.seg_log2;
@@ -740,8 +752,40 @@ int searchTopk(const zcgvs_search_desc* desc, void* d_workspace, std::size_t wor
         MergeInputs in;
         in.seg = single.seg;
         in.seg_count = single.seg_count;
-        in.n_seg = plan.segments;
+        in.n_seg = plan.segments / plan.sp_groups;
         in.seg_log2 = plan.seg_log2;
+        if (plan.sp_groups > 1) {
+            // Every (query, group) pair's top-width, then the results of up to 8 neighbouring
+            // groups at a time (contiguous in the buffer: pair (q, g) at (q * groups + g) * width)
+            // until one remains per query; each merge gathers at most 8192 keys in LDS.
+            std::uint64_t* level[2] = {at<std::uint64_t>(ws, plan.sp_level),
+                                       at<std::uint64_t>(ws, plan.sp_level) +
+                                           static_cast<std::size_t>(batch) * plan.sp_groups * plan.width};
+            status = launchSelectMerge(in, plan.width, batch * plan.sp_groups, level[0], nullptr, nullptr, nullptr,
+                                       nullptr, s);
+            if (status != ZCGVS_OK) {
+                return status;
+            }
+            int groups = plan.sp_groups;
+            int cur = 0;
+            while (true) {
+                const int fold = std::min(8, groups);
+                in = MergeInputs{};
+                in.dense = level[cur];
+                in.n_dense = static_cast<long long>(fold) * plan.width;
+                in.dense_stride = in.n_dense;
+                groups /= fold;
+                if (groups == 1) {
+                    break;  // the last merge, below, writes the keys and the result
+                }
+                status = launchSelectMerge(in, plan.width, batch * groups, level[cur ^ 1], nullptr, nullptr, nullptr,
+                                           nullptr, s);
+                if (status != ZCGVS_OK) {
+                    return status;
+                }
+                cur ^= 1;
+            }
+        }
         in.reset_overflow = true;  // (segments hold at most width keys: the flags end cleared)
         status = launchSelectMerge(in, plan.width, batch, keys, nullptr, overflow,
                                    plan.rescore ? nullptr : d_out_indices,

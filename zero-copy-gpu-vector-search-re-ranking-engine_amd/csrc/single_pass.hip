@@ -1,7 +1,7 @@
-// Single-pass scan for a few queries and a small selection (zcgvs_search_topk with batch <= 4 and
-// k or rescore candidates <= a few dozen): one scan launch plus one merge, instead of the phased
-// scan's sample, threshold phases and merges between them, whose launches dominate a
-// single-query search of a corpus the HBM streams in a hundred microseconds.
+// Single-pass scan for a few queries (zcgvs_search_topk with batch <= 4 and k or rescore
+// candidates up to 1024): one scan launch plus one or two merges, instead of the phased scan's
+// sample, threshold phases and merges between them, whose launches dominate a single-query search
+// of a corpus the HBM streams in a hundred microseconds.
 //
 // Each workgroup (1024 threads, one per compute unit) streams every W-th step of 1024 / L rows
 // (W workgroups, L lanes per row) and keeps, per query, every key above its own running
@@ -10,12 +10,16 @@
 // the list (select.hpp) and raises the threshold to the smallest of them, so the list is exact:
 // it always holds the workgroup's true top-`width`. At the end each workgroup writes its
 // top-`width` to its candidate segment, and the per-query merge (topk.hip) selects the global
-// top-`width` from the segments. Nothing can overflow, so no fallback pass follows.
+// top-`width` from the segments; for wide selections groups of workgroups are merged first. A
+// list holds max(1024, 4 * width) keys (less when four queries share the LDS), so compactions
+// are rare. Nothing can overflow, so no fallback pass follows.
 //
 // Rows are read and scored as the VALU scan and the exact fallback read them (the same lane
 // groups of L lanes and up to 8 16-byte chunks per lane, scan_core.hpp), so scores equal theirs
 // bit for bit.
 #include <hip/hip_runtime.h>
+
+#include <algorithm>
 
 #include "common.hpp"
 #include "fused.hpp"
@@ -29,8 +33,8 @@ namespace {
 constexpr int kSpThreads = 1024;
 constexpr int kSpChunksPerLane = 8;  // with 8 lanes at least: the VALU scan's row layout
 constexpr int kSpMinLanes = 8;
-constexpr int kSpCap = 1024;  // LDS keys per query (one per thread for the compaction)
-constexpr int kSpWidthLimit = 32;
+constexpr int kSpListKeys = 12288;  // LDS keys of all queries' lists together (96 KB)
+constexpr int kSpMinCap = 1024;     // keys per query list at least
 constexpr int kKindI8I8 = 4;
 constexpr std::size_t kSpQueryLds = 32 * 1024;
 
@@ -53,11 +57,11 @@ __device__ inline void ldsBarrier() {
     asm volatile("" ::: "memory");
 }
 
-template <int kKind, int L>
+template <int kKind, int L, int kSets>
 __global__ __launch_bounds__(kSpThreads) void singlePassScanKernel(ScanArgs scan, SinglePassArgs args,
                                                                    int chunks) {
     extern __shared__ std::uint32_t lds_query[];
-    __shared__ std::uint64_t lds_keys[kSinglePassQueries][kSpCap];
+    __shared__ std::uint64_t lds_keys[kSpListKeys];  // query q's list at q * cap
     __shared__ std::uint32_t lds_count[kSinglePassQueries];
     __shared__ std::uint64_t lds_tau[kSinglePassQueries];
     __shared__ std::uint32_t lds_hist[kSelectBins];
@@ -122,9 +126,11 @@ __global__ __launch_bounds__(kSpThreads) void singlePassScanKernel(ScanArgs scan
     }
     __syncthreads();
 
+    const int cap = args.cap;  // keys per query list (width + at least one check's appends)
     // Keeps the `width` best keys of query q's list (every thread calls it; q is uniform) and
     // sets the list's threshold to the smallest of them.
     auto compact = [&](int q) __attribute__((always_inline)) {
+        std::uint64_t* list = lds_keys + q * cap;
         const std::uint32_t count = lds_count[q];
         if (count <= static_cast<std::uint32_t>(width)) {
             return;  // (uniform: read after a barrier)
@@ -147,8 +153,8 @@ __global__ __launch_bounds__(kSpThreads) void singlePassScanKernel(ScanArgs scan
             const std::uint32_t bits = lds_state.bits;
             const std::uint64_t prefix = lds_state.prefix;
             const int shift = 64 - static_cast<int>(bits) - digit;
-            if (static_cast<std::uint32_t>(t) < count) {
-                const std::uint64_t key = lds_keys[q][t];
+            for (std::uint32_t i = static_cast<std::uint32_t>(t); i < count; i += kSpThreads) {
+                const std::uint64_t key = list[i];
                 if (bits == 0u || (key >> (64 - bits)) == prefix) {
                     atomicAdd(&lds_hist[(key >> shift) & ((1u << digit) - 1u)], 1u);
                 }
@@ -158,19 +164,43 @@ __global__ __launch_bounds__(kSpThreads) void singlePassScanKernel(ScanArgs scan
         }
         __syncthreads();
         const std::uint64_t cut = selectThreshold(lds_state);
-        const std::uint64_t mine = static_cast<std::uint32_t>(t) < count ? lds_keys[q][t] : 0ull;
-        __syncthreads();
+        // In place, 1024 keys a round: a kept key moves to a position no later than its own, and
+        // every key of a round is read before any of the round's moves, so nothing unread is
+        // overwritten. lds_state.count is the number of keys kept so far.
         if (t == 0) {
-            lds_count[q] = 0u;
+            lds_state.count = 0u;
         }
-        __syncthreads();
-        const bool keep = mine != 0ull && mine >= cut;
-        if (keep) {
-            const std::uint32_t slot = atomicAdd(&lds_count[q], 1u);
-            lds_keys[q][slot] = mine;
+        std::uint64_t lo = ~0ull;
+        for (std::uint32_t base = 0; base < count; base += kSpThreads) {
+            const std::uint32_t i = base + static_cast<std::uint32_t>(t);
+            const std::uint64_t key = i < count ? list[i] : 0ull;
+            const bool keep = key != 0ull && key >= cut;
+            __syncthreads();  // the round's reads (and the last round's count) before its moves
+            const std::uint64_t mask = __builtin_amdgcn_ballot_w64(keep);
+            const std::uint32_t before = __builtin_amdgcn_mbcnt_hi(static_cast<std::uint32_t>(mask >> 32),
+                                                                   __builtin_amdgcn_mbcnt_lo(static_cast<std::uint32_t>(mask), 0u));
+            if ((t & (kWave - 1)) == 0) {
+                lds_scan[t / kWave] = static_cast<std::uint32_t>(__builtin_popcountll(mask));
+            }
+            __syncthreads();
+            std::uint32_t offset = lds_state.count;
+            for (int w = 0; w < t / kWave; ++w) {
+                offset += lds_scan[w];
+            }
+            if (keep) {
+                list[offset + before] = key;
+                lo = min(lo, key);
+            }
+            __syncthreads();  // every wavefront has read lds_state.count and lds_scan
+            if (t == kSpThreads - 1) {
+                std::uint32_t round = 0u;
+                for (int w = 0; w < kSpThreads / kWave; ++w) {
+                    round += lds_scan[w];
+                }
+                lds_state.count += round;
+            }
         }
         // the new threshold: the smallest kept key (exactly the width-th best so far)
-        std::uint64_t lo = keep ? mine : ~0ull;
         lo = waveReduce64(lo, [](std::uint64_t a, std::uint64_t b) { return min(a, b); });
         if ((t & (kWave - 1)) == 0) {
             lds_wave_lo[t / kWave] = lo;
@@ -182,17 +212,24 @@ __global__ __launch_bounds__(kSpThreads) void singlePassScanKernel(ScanArgs scan
                 all = min(all, lds_wave_lo[w]);
             }
             lds_tau[q] = all;
+            lds_count[q] = lds_state.count;
         }
         __syncthreads();
     };
 
     const int lane = t & (kWave - 1);
     const int group = lane % L;
-    constexpr int kRowsPerStep = kSpThreads / L;
+    // A step: kSets row sets of kSpThreads / L consecutive rows; a lane reads kPerRow chunks of
+    // its row in every set (several sets for short rows, so each lane keeps up to
+    // kSpChunksPerLane chunks in flight).
+    constexpr int kGroupsPerSet = kSpThreads / L;
+    constexpr int kRowsPerStep = kGroupsPerSet * kSets;
     constexpr int kPer = kSpChunksPerLane;
-    // steps between capacity checks: every list takes at most kRowsPerStep keys per step
-    constexpr int kCheckEvery = (kSpCap - kSpWidthLimit) / kRowsPerStep;
-    static_assert(kCheckEvery >= 1, "an LDS list holds at least one step of keys beyond the width");
+    constexpr int kPerRow = kPer / kSets;
+    static_assert(kPerRow * kSets == kPer, "row sets split the lane's chunks evenly");
+    // steps between capacity checks: every list takes at most kRowsPerStep keys per step (the
+    // host makes cap - width at least one step's rows)
+    const int check_every = (cap - width) / kRowsPerStep;
     const std::size_t row_bytes = static_cast<std::size_t>(chunks) * 16;
     const std::uint8_t* corpus = static_cast<const std::uint8_t*>(scan.corpus);
     const bool l2 = scan.metric == ZCGVS_METRIC_L2;
@@ -202,115 +239,124 @@ __global__ __launch_bounds__(kSpThreads) void singlePassScanKernel(ScanArgs scan
     const long long stride = static_cast<long long>(gridDim.x) * kRowsPerStep;
     const long long end = n;
 
-    // this lane's chunks of its row in the step starting at `base` (rows past the corpus and
+    // this lane's chunks of its rows in the step starting at `base` (rows past the corpus and
     // masked rows are not read)
     auto loadStep = [&](long long base, uint4 (&raw)[kPer]) __attribute__((always_inline)) {
-        const long long row = base + t / L;
-        const long long r = row < end ? row : end - 1;
-        const bool skip = row >= end || (scan.mask != nullptr && scan.mask[r] == 0);
 #pragma unroll
-        for (int i = 0; i < kPer; ++i) {
-            const int c = group + i * L;
-            raw[i] = make_uint4(0u, 0u, 0u, 0u);
-            if (!skip && c < chunks) {
-                raw[i] = loadChunkStreaming(corpus + static_cast<std::size_t>(r) * row_bytes + static_cast<std::size_t>(c) * 16);
+        for (int set = 0; set < kSets; ++set) {
+            const long long row = base + set * kGroupsPerSet + t / L;
+            const long long r = row < end ? row : end - 1;
+            const bool skip = row >= end || (scan.mask != nullptr && scan.mask[r] == 0);
+#pragma unroll
+            for (int i = 0; i < kPerRow; ++i) {
+                const int c = group + i * L;
+                uint4& chunk = raw[set * kPerRow + i];
+                chunk = make_uint4(0u, 0u, 0u, 0u);
+                if (!skip && c < chunks) {
+                    chunk = loadChunkStreaming(corpus + static_cast<std::size_t>(r) * row_bytes + static_cast<std::size_t>(c) * 16);
+                }
             }
         }
     };
     // scores of the step's rows against every query, keys above each list's threshold appended
-    auto scoreStep = [&](long long base, const uint4 (&raw)[kPer]) __attribute__((always_inline)) {
-        const long long row = base + t / L;
-        const bool valid = row < end;
-        const long long r = valid ? row : end - 1;
-        const bool masked = scan.mask != nullptr && scan.mask[r] == 0;
-        float row_scale = 1.0f;
-        if constexpr (kKind == kKindI8I8) {
-            row_scale = masked ? 0.0f : scan.row_scales[r];
-        }
+    auto scoreStep = [&](long long base, const uint4 (&raw_step)[kPer]) __attribute__((always_inline)) {
 #pragma unroll
-        for (int q = 0; q < kSinglePassQueries; ++q) {
-            if (q >= q_count) {
-                break;
+        for (int set = 0; set < kSets; ++set) {
+            const uint4* raw = raw_step + set * kPerRow;
+            const long long row = base + set * kGroupsPerSet + t / L;
+            const bool valid = row < end;
+            const long long r = valid ? row : end - 1;
+            const bool masked = scan.mask != nullptr && scan.mask[r] == 0;
+            float row_scale = 1.0f;
+            if constexpr (kKind == kKindI8I8) {
+                row_scale = masked ? 0.0f : scan.row_scales[r];
             }
-            const std::uint32_t* staged = lds_query + q * words;
-            float score;
-            if constexpr (kKind == ZCGVS_DTYPE_BINARY || kKind == kKindI8I8) {
-                int acc = 0;
 #pragma unroll
-                for (int i = 0; i < kPer; ++i) {
-                    const int c = group + i * L;
-                    if (c < chunks) {
-                        const uint4 qw = *reinterpret_cast<const uint4*>(staged + 4 * c);
-                        if constexpr (kKind == ZCGVS_DTYPE_BINARY) {
-                            acc += __popc(raw[i].x ^ qw.x) + __popc(raw[i].y ^ qw.y) + __popc(raw[i].z ^ qw.z) +
-                                   __popc(raw[i].w ^ qw.w);
-                        } else {
-                            acc = __builtin_amdgcn_sdot4(static_cast<int>(raw[i].x), static_cast<int>(qw.x), acc, false);
-                            acc = __builtin_amdgcn_sdot4(static_cast<int>(raw[i].y), static_cast<int>(qw.y), acc, false);
-                            acc = __builtin_amdgcn_sdot4(static_cast<int>(raw[i].z), static_cast<int>(qw.z), acc, false);
-                            acc = __builtin_amdgcn_sdot4(static_cast<int>(raw[i].w), static_cast<int>(qw.w), acc, false);
+            for (int q = 0; q < kSinglePassQueries; ++q) {
+                if (q >= q_count) {
+                    break;
+                }
+                const std::uint32_t* staged = lds_query + q * words;
+                float score;
+                if constexpr (kKind == ZCGVS_DTYPE_BINARY || kKind == kKindI8I8) {
+                    int acc = 0;
+#pragma unroll
+                    for (int i = 0; i < kPerRow; ++i) {
+                        const int c = group + i * L;
+                        if (c < chunks) {
+                            const uint4 qw = *reinterpret_cast<const uint4*>(staged + 4 * c);
+                            if constexpr (kKind == ZCGVS_DTYPE_BINARY) {
+                                acc += __popc(raw[i].x ^ qw.x) + __popc(raw[i].y ^ qw.y) + __popc(raw[i].z ^ qw.z) +
+                                       __popc(raw[i].w ^ qw.w);
+                            } else {
+                                acc = __builtin_amdgcn_sdot4(static_cast<int>(raw[i].x), static_cast<int>(qw.x), acc, false);
+                                acc = __builtin_amdgcn_sdot4(static_cast<int>(raw[i].y), static_cast<int>(qw.y), acc, false);
+                                acc = __builtin_amdgcn_sdot4(static_cast<int>(raw[i].z), static_cast<int>(qw.z), acc, false);
+                                acc = __builtin_amdgcn_sdot4(static_cast<int>(raw[i].w), static_cast<int>(qw.w), acc, false);
+                            }
                         }
                     }
-                }
-                const int total = groupSum<L>(acc);
-                if constexpr (kKind == ZCGVS_DTYPE_BINARY) {
-                    score = static_cast<float>(dim - 2 * total) / static_cast<float>(dim);
+                    const int total = groupSum<L>(acc);
+                    if constexpr (kKind == ZCGVS_DTYPE_BINARY) {
+                        score = static_cast<float>(dim - 2 * total) / static_cast<float>(dim);
+                    } else {
+                        const float combined = qscale[q] * row_scale;
+                        score = static_cast<float>(total) * combined;
+                    }
                 } else {
-                    const float combined = qscale[q] * row_scale;
-                    score = static_cast<float>(total) * combined;
-                }
-            } else {
-                using Traits = ChunkTraits<kKind>;
-                constexpr int E = Traits::kElems;
-                const float* fstaged = reinterpret_cast<const float*>(staged);
-                float acc = 0.0f;
+                    using Traits = ChunkTraits<kKind>;
+                    constexpr int E = Traits::kElems;
+                    const float* fstaged = reinterpret_cast<const float*>(staged);
+                    float acc = 0.0f;
 #pragma unroll
-                for (int i = 0; i < kPer; ++i) {
-                    const int c = group + i * L;
-                    if (c < chunks) {
-                        float v[E];
-                        Traits::decode(raw[i], scan.scale, v);
-                        const float* qv = fstaged + c * E;
-                        if (l2) {
+                    for (int i = 0; i < kPerRow; ++i) {
+                        const int c = group + i * L;
+                        if (c < chunks) {
+                            float v[E];
+                            Traits::decode(raw[i], scan.scale, v);
+                            const float* qv = fstaged + c * E;
+                            if (l2) {
 #pragma unroll
-                            for (int e = 0; e < E; ++e) {
-                                const float d = qv[e] - v[e];
-                                acc = fmaf(d, d, acc);
-                            }
-                        } else {
+                                for (int e = 0; e < E; ++e) {
+                                    const float d = qv[e] - v[e];
+                                    acc = fmaf(d, d, acc);
+                                }
+                            } else {
 #pragma unroll
-                            for (int e = 0; e < E; ++e) {
-                                acc = fmaf(qv[e], v[e], acc);
+                                for (int e = 0; e < E; ++e) {
+                                    acc = fmaf(qv[e], v[e], acc);
+                                }
                             }
                         }
                     }
+                    const float total = groupSum<L>(acc);
+                    score = l2 ? -total : total;
                 }
-                const float total = groupSum<L>(acc);
-                score = l2 ? -total : total;
-            }
-            if (valid && group == 0) {
-                float value = masked ? kMaskedScore : score;
-                if (scan.lexical != nullptr) {
-                    const float lex = scan.lexical[static_cast<std::size_t>(q) * n + row];
-                    value = fuseHybrid(value, lex, scan.dense_weight, inverse[q]);
-                }
-                const std::uint64_t key = makeKey(value, static_cast<std::uint32_t>(row));
-                if (key > lds_tau[q]) {
-                    const std::uint32_t slot = atomicAdd(&lds_count[q], 1u);
-                    if (slot < static_cast<std::uint32_t>(kSpCap)) {  // (always: checked between steps)
-                        lds_keys[q][slot] = key;
+                if (valid && group == 0) {
+                    float value = masked ? kMaskedScore : score;
+                    if (scan.lexical != nullptr) {
+                        const float lex = scan.lexical[static_cast<std::size_t>(q) * n + row];
+                        value = fuseHybrid(value, lex, scan.dense_weight, inverse[q]);
+                    }
+                    const std::uint64_t key = makeKey(value, static_cast<std::uint32_t>(row));
+                    if (key > lds_tau[q]) {
+                        const std::uint32_t slot = atomicAdd(&lds_count[q], 1u);
+                        if (slot < static_cast<std::uint32_t>(cap)) {  // (always: checked between steps)
+                            lds_keys[q * cap + slot] = key;
+                        }
                     }
                 }
             }
         }
     };
-    // Every kCheckEvery steps: the lists' counts after every wavefront's appends, read between two
+
+    // Every check_every steps: the lists' counts after every wavefront's appends, read between two
     // LDS-only barriers (so the next step's loads stay in flight, and no wavefront appends again
     // before all have read the same counts), and a compaction of any list that the next
-    // kCheckEvery steps could overflow.
+    // check_every steps could overflow.
     int step = 0;
     auto check = [&]() __attribute__((always_inline)) {
-        if (++step < kCheckEvery) {
+        if (++step < check_every) {
             return;
         }
         step = 0;
@@ -323,7 +369,7 @@ __global__ __launch_bounds__(kSpThreads) void singlePassScanKernel(ScanArgs scan
         ldsBarrier();
 #pragma unroll
         for (int q = 0; q < kSinglePassQueries; ++q) {
-            if (counts[q] > static_cast<std::uint32_t>(kSpCap - kCheckEvery * kRowsPerStep)) {
+            if (counts[q] > static_cast<std::uint32_t>(cap - check_every * kRowsPerStep)) {
                 compact(q);
             }
         }
@@ -340,70 +386,137 @@ __global__ __launch_bounds__(kSpThreads) void singlePassScanKernel(ScanArgs scan
         compact(q);
     }
     __syncthreads();
-    // this workgroup's top-`width` of every query -> its candidate segment
+    // This workgroup's top-`width` of every query -> its candidate segment. With G merge groups
+    // workgroup b belongs to group g = b % G as its segment s = b / G, and the list of query q
+    // goes to the segment of (s, q * G + g) in a layout of q_count * G merge queries, so the first
+    // merge treats every (query, group) pair as a query of its own.
+    const int groups = args.groups;
+    const int g = static_cast<int>(blockIdx.x) % groups;
+    const std::size_t s_index = blockIdx.x / groups;
     for (int q = 0; q < q_count; ++q) {
         const std::uint32_t count = min(lds_count[q], static_cast<std::uint32_t>(width));
-        const std::size_t seg_row = (static_cast<std::size_t>(blockIdx.x) * q_count + q) << args.seg_log2;
+        const std::size_t merge_q = static_cast<std::size_t>(q) * groups + g;
+        const std::size_t slot = s_index * static_cast<std::size_t>(q_count * groups) + merge_q;
         for (std::uint32_t i = static_cast<std::uint32_t>(t); i < count; i += kSpThreads) {
-            args.seg[seg_row + i] = lds_keys[q][i];
+            args.seg[(slot << args.seg_log2) + i] = lds_keys[q * cap + i];
         }
         if (t == 0) {
-            args.seg_count[static_cast<std::size_t>(blockIdx.x) * q_count + q] = count;
+            args.seg_count[slot] = count;
         }
     }
 }
 
-template <int kKind>
-int launchKind(int lanes, int workgroups, std::size_t shared, const ScanArgs& scan, const SinglePassArgs& args,
-               int chunks, hipStream_t stream) {
-    const dim3 grid(static_cast<unsigned>(workgroups));
-    switch (lanes) {
-        case 8: singlePassScanKernel<kKind, 8><<<grid, kSpThreads, shared, stream>>>(scan, args, chunks); break;
-        case 16: singlePassScanKernel<kKind, 16><<<grid, kSpThreads, shared, stream>>>(scan, args, chunks); break;
-        case 32: singlePassScanKernel<kKind, 32><<<grid, kSpThreads, shared, stream>>>(scan, args, chunks); break;
-        default: singlePassScanKernel<kKind, 64><<<grid, kSpThreads, shared, stream>>>(scan, args, chunks); break;
+// Lanes per row and row sets per step for rows of `chunks` 16-byte chunks: the VALU scan's lane
+// count (at least 8 lanes, at most 8 chunks a lane); rows that leave a lane's 8 chunks mostly
+// unused (at most 4 chunks a lane) take several rows per step, up to L sets.
+struct SpLayout {
+    int lanes = 0;
+    int sets = 1;
+};
+
+SpLayout spLayout(int chunks) {
+    SpLayout layout;
+    layout.lanes = lanesPerRow(chunks, kSpChunksPerLane, kSpMinLanes);
+    int per_row = 1;
+    while (per_row * layout.lanes < chunks) {
+        per_row *= 2;
     }
+    layout.sets = std::min(kSpChunksPerLane / per_row, layout.lanes);
+    return layout;
+}
+
+template <int kKind, int L, int kSets>
+int launchSets(int workgroups, std::size_t shared, const ScanArgs& scan, const SinglePassArgs& args, int chunks,
+               hipStream_t stream) {
+    singlePassScanKernel<kKind, L, kSets><<<dim3(static_cast<unsigned>(workgroups)), kSpThreads, shared, stream>>>(
+        scan, args, chunks);
     ZCGVS_LAUNCH_CHECK("single-pass scan");
     return ZCGVS_OK;
 }
 
+template <int kKind>
+int launchKind(const SpLayout& layout, int workgroups, std::size_t shared, const ScanArgs& scan,
+               const SinglePassArgs& args, int chunks, hipStream_t stream) {
+    switch (layout.lanes * 16 + layout.sets) {
+        case 1 * 16 + 1: return launchSets<kKind, 1, 1>(workgroups, shared, scan, args, chunks, stream);
+        case 2 * 16 + 2: return launchSets<kKind, 2, 2>(workgroups, shared, scan, args, chunks, stream);
+        case 4 * 16 + 4: return launchSets<kKind, 4, 4>(workgroups, shared, scan, args, chunks, stream);
+        case 8 * 16 + 8: return launchSets<kKind, 8, 8>(workgroups, shared, scan, args, chunks, stream);
+        case 8 * 16 + 4: return launchSets<kKind, 8, 4>(workgroups, shared, scan, args, chunks, stream);
+        case 8 * 16 + 2: return launchSets<kKind, 8, 2>(workgroups, shared, scan, args, chunks, stream);
+        case 8 * 16 + 1: return launchSets<kKind, 8, 1>(workgroups, shared, scan, args, chunks, stream);
+        case 16 * 16 + 1: return launchSets<kKind, 16, 1>(workgroups, shared, scan, args, chunks, stream);
+        case 32 * 16 + 1: return launchSets<kKind, 32, 1>(workgroups, shared, scan, args, chunks, stream);
+        case 64 * 16 + 1: return launchSets<kKind, 64, 1>(workgroups, shared, scan, args, chunks, stream);
+        default: return setError(ZCGVS_ERR_RUNTIME, "zcgvs single-pass scan: no kernel for this row layout");
+    }
+}
+
 }  // namespace
 
-int singlePassWorkgroups() { return deviceComputeUnits(); }
-
-bool singlePassSupported(const ScanArgs& scan, int width) {
-    if (scan.batch < 1 || scan.batch > kSinglePassQueries || width < 1 || width > kSpWidthLimit) {
-        return false;
-    }
-    // the merge gathers every workgroup's top-`width` in LDS
-    if (static_cast<long long>(singlePassWorkgroups()) * width > kSinglePassMergeKeys) {
-        return false;
+SinglePassShape singlePassShape(const ScanArgs& scan, int width) {
+    SinglePassShape shape;
+    if (scan.batch < 1 || scan.batch > kSinglePassQueries || width < 1 || width > kMaxK) {
+        return shape;
     }
     const std::size_t bytes = rowBytes(scan.dtype, scan.dim);
     if (bytes % 16 != 0 || !aligned16(scan.corpus)) {
-        return false;
+        return shape;
     }
     const int chunks = static_cast<int>(bytes / 16);
-    const int lanes = lanesPerRow(chunks, kSpChunksPerLane, kSpMinLanes);
+    const SpLayout layout = spLayout(chunks);
     const std::size_t staged = static_cast<std::size_t>(scan.batch) * chunks * spWordsPerChunk(spKindOf(scan)) * 4;
-    return (chunks + lanes - 1) / lanes <= kSpChunksPerLane && staged <= kSpQueryLds;
+    if ((chunks + layout.lanes - 1) / layout.lanes > kSpChunksPerLane || staged > kSpQueryLds) {
+        return shape;
+    }
+    // A list holds its width best keys plus at least one check's appends (rows per step); four
+    // times the width, or two steps' rows beyond it, keeps compactions rare.
+    const int rows_per_step = kSpThreads / layout.lanes * layout.sets;
+    const int cap = std::min(kSpListKeys / scan.batch,
+                             std::max({kSpMinCap, (4 * width + 63) / 64 * 64, width + 2 * rows_per_step}));
+    if (cap - width < rows_per_step) {
+        return shape;
+    }
+    // Merge groups: one merge of every workgroup's list when the lists fit its LDS gather,
+    // otherwise groups of workgroups merged first (each group's lists in LDS, at most 8192 keys)
+    // and their results merged after.
+    const int units = deviceComputeUnits();
+    int groups = 1;
+    while (static_cast<long long>(units / groups) * width > (groups == 1 ? kSinglePassMergeKeys : 8192) &&
+           groups < units) {
+        groups *= 2;
+    }
+    shape.supported = true;
+    shape.groups = groups;
+    shape.workgroups = std::max(groups, units / groups * groups);
+    shape.cap = cap;
+    int log2 = 0;
+    while ((1 << log2) < width) {
+        ++log2;
+    }
+    shape.seg_log2 = log2;
+    return shape;
 }
 
+bool singlePassSupported(const ScanArgs& scan, int width) { return singlePassShape(scan, width).supported; }
+
 int launchSinglePass(const ScanArgs& scan, const SinglePassArgs& args, hipStream_t stream) {
-    if (!singlePassSupported(scan, args.width)) {
+    const SinglePassShape shape = singlePassShape(scan, args.width);
+    if (!shape.supported || args.cap != shape.cap || args.groups != shape.groups ||
+        args.workgroups % args.groups != 0) {
         return setError(ZCGVS_ERR_RUNTIME, "zcgvs single-pass scan: shape not supported");
     }
     const int chunks = static_cast<int>(rowBytes(scan.dtype, scan.dim) / 16);
-    const int lanes = lanesPerRow(chunks, kSpChunksPerLane, kSpMinLanes);
+    const SpLayout layout = spLayout(chunks);
     const int kind = spKindOf(scan);
     const std::size_t shared = static_cast<std::size_t>(scan.batch) * chunks * spWordsPerChunk(kind) * 4;
     const int workgroups = args.workgroups;
     switch (kind) {
-        case ZCGVS_DTYPE_F16: return launchKind<ZCGVS_DTYPE_F16>(lanes, workgroups, shared, scan, args, chunks, stream);
-        case ZCGVS_DTYPE_I8: return launchKind<ZCGVS_DTYPE_I8>(lanes, workgroups, shared, scan, args, chunks, stream);
-        case ZCGVS_DTYPE_BINARY: return launchKind<ZCGVS_DTYPE_BINARY>(lanes, workgroups, shared, scan, args, chunks, stream);
-        case kKindI8I8: return launchKind<kKindI8I8>(lanes, workgroups, shared, scan, args, chunks, stream);
-        default: return launchKind<ZCGVS_DTYPE_F32>(lanes, workgroups, shared, scan, args, chunks, stream);
+        case ZCGVS_DTYPE_F16: return launchKind<ZCGVS_DTYPE_F16>(layout, workgroups, shared, scan, args, chunks, stream);
+        case ZCGVS_DTYPE_I8: return launchKind<ZCGVS_DTYPE_I8>(layout, workgroups, shared, scan, args, chunks, stream);
+        case ZCGVS_DTYPE_BINARY: return launchKind<ZCGVS_DTYPE_BINARY>(layout, workgroups, shared, scan, args, chunks, stream);
+        case kKindI8I8: return launchKind<kKindI8I8>(layout, workgroups, shared, scan, args, chunks, stream);
+        default: return launchKind<ZCGVS_DTYPE_F32>(layout, workgroups, shared, scan, args, chunks, stream);
     }
 }
 
