@@ -57,6 +57,16 @@ inline long long phaseItems(long long blocks, long long stride, long long skip) 
     return multiples - (multiples + skip - 1) / skip;
 }
 
+// A score floor for the keys above a threshold key `tau`: keys order by their score's ordered bits
+// first, so key > tau needs score >= keyScore(tau). The floor holds only when tau is a real key
+// whose score is not NaN (NaN scores rank lowest and fail every comparison); *gated is false
+// otherwise and every score must then be keyed and compared.
+__device__ __forceinline__ float keyFloor(std::uint64_t tau, bool* gated) {
+    const float score = keyScore(tau);
+    *gated = tau != 0ull && score == score;
+    return score;
+}
+
 // Appends `key` to query q's segment of this workgroup (lds_count: this workgroup's per-query
 // counts for the launch's query range, indexed by q - q_offset).
 __device__ __forceinline__ void appendCandidate(const EmitArgs& emit, std::uint32_t* lds_count,

@@ -180,8 +180,11 @@ void mfmaFloatScanKernel(ScanArgs scan, PhaseArgs phase, EmitArgs emit, int q_of
         }
     }
     std::uint64_t tau = 0ull;
+    bool gated = false;  // tau_floor applies (every key above tau scores at least tau_floor)
+    float tau_floor = 0.0f;
     if constexpr (!kDense) {
         tau = emit.tau[q];
+        tau_floor = keyFloor(tau, &gated);
     }
     float inverse = 0.0f;  // 1 / (the query's largest lexical score), 0 when none is positive
     if constexpr (kLex) {
@@ -327,23 +330,29 @@ void mfmaFloatScanKernel(ScanArgs scan, PhaseArgs phase, EmitArgs emit, int q_of
         }
         if (wave_active) {
             const long long row0 = phaseBlock(item, phase.stride, phase.skip) * kRows;
+            const int valid_rows = static_cast<int>(min(static_cast<long long>(kRows), doc_count - row0));
+            const std::uint32_t row_base = static_cast<std::uint32_t>(row0);
             for (int block = first_block; block < kRowBlocks; block += waves_per_group) {
                 const v4f score = multiply(ring[slot], block);
                 if (q_valid) {
 #pragma unroll
                     for (int i = 0; i < 4; ++i) {
                         const int local = block * 16 + 4 * h + i;
-                        const long long row = row0 + local;
                         float value = score[i];
                         if constexpr (kLex) {
                             value = fuseHybrid(value, lex_ring[slot][qlocal][local], scan.dense_weight, inverse);
                         }
-                        const std::uint64_t key =
-                            row < doc_count ? makeKey(value, static_cast<std::uint32_t>(row)) : 0ull;
                         if constexpr (kDense) {
+                            const std::uint64_t key =
+                                local < valid_rows ? makeKey(value, row_base + static_cast<std::uint32_t>(local)) : 0ull;
                             emit.dense[static_cast<std::size_t>(q) * emit.dense_stride + item * kRows + local] = key;
-                        } else if (key > tau) {
-                            appendCandidate(emit, lds_count, q, q_offset, scan.batch, key);
+                        } else if (!gated || value >= tau_floor) {
+                            // (almost every row of a threshold phase fails the score test above)
+                            const std::uint64_t key =
+                                local < valid_rows ? makeKey(value, row_base + static_cast<std::uint32_t>(local)) : 0ull;
+                            if (key > tau) {
+                                appendCandidate(emit, lds_count, q, q_offset, scan.batch, key);
+                            }
                         }
                     }
                 }
