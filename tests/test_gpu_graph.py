@@ -25,10 +25,29 @@ def _f16_desc(capi, n, dim, batch, k, seed):
     return capi.search_desc(store, capi.DeviceArray.from_host(queries), batch, k)
 
 
+def _f32_desc(capi, n, dim, batch, k, seed):
+    corpus = normalized(n, dim, seed)
+    queries = normalized(batch, dim, seed + 1)
+    store = capi.store_desc(capi.DeviceArray.from_host(corpus), n, dim, capi.F32)
+    return capi.search_desc(store, capi.DeviceArray.from_host(queries), batch, k)
+
+
+def _binary_rescore_desc(capi, n, dim, batch, k, seed):
+    rows = normalized(n, dim, seed)
+    words, half = oracle.pack_binary(rows), oracle.f32_to_f16(rows)
+    queries = normalized(batch, dim, seed + 1)
+    return capi.search_desc(capi.store_desc(capi.DeviceArray.from_host(words), n, dim, capi.BINARY),
+                            capi.DeviceArray.from_host(queries), batch, k,
+                            rescore=capi.store_desc(capi.DeviceArray.from_host(half), n, dim, capi.F16),
+                            rescore_candidates=1000)
+
+
 @pytest.mark.parametrize("make,n,dim,batch,k", [
     (_int8_desc, 200_000, 768, 64, 100),   # MFMA scan, several threshold phases
-    (_f16_desc, 150_000, 384, 1, 10),      # VALU scan, one query
+    (_f16_desc, 150_000, 384, 1, 10),      # single pass, one query
     (_f16_desc, 150_000, 384, 16, 10),     # fp16 MFMA scan
+    (_f32_desc, 200_000, 384, 64, 10),     # fp32 bf16-split MFMA scan
+    (_binary_rescore_desc, 200_000, 1024, 1, 10),  # single pass of 1000 keys, group merges, rescore
 ])
 def test_graph_replays_match_direct_calls(gpu, make, n, dim, batch, k):
     capi = gpu

@@ -49,12 +49,14 @@ def test_static_scratch_size(gpu):
     assert gpu.library().zcgvs_static_scratch_bytes() == 64 << 20
 
 
-@pytest.mark.parametrize("case", ["int8", "float32"])
+@pytest.mark.parametrize("case", ["int8", "float32", "float32-few"])
 def test_noalloc_matches_the_workspace_entry_point(gpu, case):
     capi = gpu
     build = _int8_case if case == "int8" else _float_case
-    # two calls in a row, the second smaller: the array keeps the first call's contents
-    for n, batch, seed in ((300_000, 48, 11), (70_001, 9, 21)):
+    # two calls in a row, the second smaller: the array keeps the first call's contents (the
+    # few-query case takes the single pass)
+    sizes = ((300_000, 3, 31), (70_001, 1, 41)) if case == "float32-few" else ((300_000, 48, 11), (70_001, 9, 21))
+    for n, batch, seed in sizes:
         desc, ref, _keep = build(capi, n, batch, seed)
         assert capi.search_workspace_bytes(desc) <= 64 << 20
         (exp_idx, exp_val, flags), (got_idx, got_val) = _pair(capi, desc)
