@@ -336,7 +336,8 @@ int zcgvs_search_topk_profiled(const zcgvs_search_desc* desc, void* d_workspace,
 
 /* Corpus rows each scan phase of the fused pipeline visits for `desc` (rows[p] for p <
  * max_phases; the phase count in *phases; 0 phases when the pipeline materializes the score
- * matrix instead). Host only; used to price the scan launches. No reference counterpart. */
+ * matrix instead; one phase of doc_count rows for the single pass). Host only; used to price the
+ * scan launches. No reference counterpart. */
 int zcgvs_search_phase_rows(const zcgvs_search_desc* desc, long long* rows, int max_phases,
                             int* phases);
 
