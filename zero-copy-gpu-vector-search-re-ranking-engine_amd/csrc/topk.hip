@@ -215,6 +215,7 @@ __device__ __forceinline__ void forEachCandidate(const MergeInputs& in, int q, i
 // and dense keys are copied as they lie (zero keys are skipped later), and segment j of
 // segment s goes to offset[s] + j, from the exclusive scan of the segment counts.
 constexpr std::uint32_t kSelectLdsKeys = 12288;
+static_assert(kMaxK <= kSelectBins, "the ranks of a selection reuse the histogram");
 
 __global__ __launch_bounds__(kMergeThreads) void selectMergeKernel(
     MergeInputs in, int k, int batch, std::uint64_t* __restrict__ out_keys,
@@ -244,6 +245,20 @@ __global__ __launch_bounds__(kMergeThreads) void selectMergeKernel(
         lds_state.count = 0u;
     }
     __syncthreads();
+    const std::uint32_t k_prev = in.prev != nullptr ? static_cast<std::uint32_t>(in.k_prev) : 0u;
+    const std::uint32_t n_dense = in.dense != nullptr ? static_cast<std::uint32_t>(in.n_dense) : 0u;
+    // Count, smallest and largest non-zero key of what this thread gathers (then reduced over
+    // the block), so the radix passes can start below the bits every key shares.
+    std::uint32_t own_count = 0u;
+    std::uint64_t own_lo = ~0ull;
+    std::uint64_t own_hi = 0ull;
+    auto note = [&](std::uint64_t key) {
+        if (key != 0ull) {
+            ++own_count;
+            own_lo = min(own_lo, key);
+            own_hi = max(own_hi, key);
+        }
+    };
     std::uint32_t seg_total = 0u;
     if (in.n_seg > 0) {  // (uniform: a kernel argument)
         const std::uint32_t cap = 1u << in.seg_log2;
@@ -271,8 +286,6 @@ __global__ __launch_bounds__(kMergeThreads) void selectMergeKernel(
             }
         }
     }
-    const std::uint32_t k_prev = in.prev != nullptr ? static_cast<std::uint32_t>(in.k_prev) : 0u;
-    const std::uint32_t n_dense = in.dense != nullptr ? static_cast<std::uint32_t>(in.n_dense) : 0u;
     const std::uint64_t gathered = static_cast<std::uint64_t>(k_prev) + n_dense + seg_total;
     const bool in_lds = gathered <= kSelectLdsKeys;
     __syncthreads();
@@ -281,19 +294,23 @@ __global__ __launch_bounds__(kMergeThreads) void selectMergeKernel(
         if (k_prev > 0u) {
             const std::uint64_t* prev = in.prev + static_cast<std::size_t>(q) * in.k_prev;
             for (std::uint32_t i = t; i < k_prev; i += blockDim.x) {
-                lds_cand[i] = prev[i];
+                const std::uint64_t key = prev[i];
+                lds_cand[i] = key;
+                note(key);
             }
         }
         if (n_dense > 0u) {
             const std::uint64_t* dense = in.dense + static_cast<std::size_t>(q) * in.dense_stride;
 #pragma unroll 8
             for (std::uint32_t i = t; i < n_dense; i += blockDim.x) {
-                lds_cand[k_prev + i] = dense[i];
+                const std::uint64_t key = dense[i];
+                lds_cand[k_prev + i] = key;
+                note(key);
             }
         }
         if (in.seg != nullptr) {
-            // Candidate i of the compacted list lives in the last segment whose offset is <= i
-            // (empty segments share their successor's offset), at position i - offset there.
+            // Candidate i of the compacted list lives in the last segment whose offset is
+            // <= i (empty segments share their successor's offset), at position i - offset.
             const std::uint32_t base = k_prev + n_dense;
 #pragma unroll 4
             for (std::uint32_t i = t; i < seg_total; i += blockDim.x) {
@@ -308,11 +325,14 @@ __global__ __launch_bounds__(kMergeThreads) void selectMergeKernel(
                     }
                 }
                 const std::uint32_t j = i - lds_offset[lo];
-                lds_cand[base + i] = in.seg[((static_cast<std::size_t>(lo) * batch + q) << in.seg_log2) + j];
+                const std::uint64_t key = in.seg[((static_cast<std::size_t>(lo) * batch + q) << in.seg_log2) + j];
+                lds_cand[base + i] = key;
+                note(key);
             }
         }
+    } else {
+        forEachCandidate(in, q, batch, lds_seg, note);
     }
-    __syncthreads();
 
     auto forEachKey = [&](auto&& f) {
         if (in_lds) {
@@ -328,45 +348,38 @@ __global__ __launch_bounds__(kMergeThreads) void selectMergeKernel(
         }
     };
 
-    // Count, smallest and largest valid key: per-thread values, wavefront reductions, one LDS
-    // slot per wavefront (a block-wide atomic on one word would serialize 1024 updates).
+    // Count, smallest and largest valid key: wavefront reductions, one LDS slot per wavefront,
+    // then wavefront 0 reduces the slots (a block-wide atomic on one word would serialize 1024
+    // updates).
     {
-        std::uint32_t mine = 0u;
-        std::uint64_t lo = ~0ull;
-        std::uint64_t hi = 0ull;
-        forEachKey([&](std::uint64_t key) {
-            ++mine;
-            lo = min(lo, key);
-            hi = max(hi, key);
-        });
-        mine = static_cast<std::uint32_t>(
-            waveReduce64(mine, [](std::uint64_t a, std::uint64_t b) { return a + b; }));
-        lo = waveReduce64(lo, [](std::uint64_t a, std::uint64_t b) { return min(a, b); });
-        hi = waveReduce64(hi, [](std::uint64_t a, std::uint64_t b) { return max(a, b); });
+        const std::uint64_t count = waveReduce64(own_count, [](std::uint64_t a, std::uint64_t b) { return a + b; });
+        const std::uint64_t lo = waveReduce64(own_lo, [](std::uint64_t a, std::uint64_t b) { return min(a, b); });
+        const std::uint64_t hi = waveReduce64(own_hi, [](std::uint64_t a, std::uint64_t b) { return max(a, b); });
         if ((t & (kWave - 1)) == 0) {
-            lds_wave_count[t / kWave] = mine;
+            lds_wave_count[t / kWave] = static_cast<std::uint32_t>(count);
             lds_wave_lo[t / kWave] = lo;
             lds_wave_hi[t / kWave] = hi;
         }
     }
-    __syncthreads();
-    if (t == 0) {
-        std::uint32_t count = 0u;
-        std::uint64_t lo = ~0ull;
-        std::uint64_t hi = 0ull;
-        for (int w = 0; w < kMergeThreads / kWave; ++w) {
-            count += lds_wave_count[w];
-            lo = min(lo, lds_wave_lo[w]);
-            hi = max(hi, lds_wave_hi[w]);
-        }
-        lds_valid = count;
-        lds_state.done = count <= static_cast<std::uint32_t>(k) ? 1u : 0u;
-        if (count > static_cast<std::uint32_t>(k)) {
-            // The keys (unique, at least two) share their top `common` bits: the radix passes
-            // start below them, so the first digit already separates the keys.
-            const int common = __clzll(hi ^ lo);
-            lds_state.prefix = common == 0 ? 0ull : (hi >> (64 - common));
-            lds_state.bits = static_cast<std::uint32_t>(common);
+    __syncthreads();  // (also: the gathered keys are in LDS)
+    if (t < kWave) {
+        constexpr int kSlots = kMergeThreads / kWave;
+        std::uint64_t count = t < kSlots ? lds_wave_count[t] : 0ull;
+        std::uint64_t lo = t < kSlots ? lds_wave_lo[t] : ~0ull;
+        std::uint64_t hi = t < kSlots ? lds_wave_hi[t] : 0ull;
+        count = waveReduce64(count, [](std::uint64_t a, std::uint64_t b) { return a + b; });
+        lo = waveReduce64(lo, [](std::uint64_t a, std::uint64_t b) { return min(a, b); });
+        hi = waveReduce64(hi, [](std::uint64_t a, std::uint64_t b) { return max(a, b); });
+        if (t == 0) {
+            lds_valid = static_cast<std::uint32_t>(count);
+            lds_state.done = count <= static_cast<std::uint64_t>(k) ? 1u : 0u;
+            if (count > static_cast<std::uint64_t>(k)) {
+                // The keys (unique, at least two) share their top `common` bits: the radix
+                // passes start below them, so the first digit already separates the keys.
+                const int common = __clzll(hi ^ lo);
+                lds_state.prefix = common == 0 ? 0ull : (hi >> (64 - common));
+                lds_state.bits = static_cast<std::uint32_t>(common);
+            }
         }
     }
     __syncthreads();
@@ -429,15 +442,42 @@ __global__ __launch_bounds__(kMergeThreads) void selectMergeKernel(
                                     static_cast<std::uint32_t>(k));
     std::uint64_t* dst = out_keys + static_cast<std::size_t>(q) * k;
     if (out_index != nullptr) {
-        // the search's result: every key at its rank
-        forEachRanked(lds_keys, taken, [&](std::uint32_t rank, std::uint64_t key) {
+        // The search's result: every key at its rank, the number of selected keys above it. The
+        // comparisons of one key are split over `parts` threads whose counts meet in LDS (the
+        // histogram, free after the passes), so a short list takes one round of comparisons.
+        std::uint32_t* rank_of = lds_hist;
+        for (std::uint32_t i = static_cast<std::uint32_t>(t); i < taken; i += blockDim.x) {
+            rank_of[i] = 0u;
+        }
+        __syncthreads();
+        if (taken > 0u) {
+            const std::uint32_t parts = max(1u, static_cast<std::uint32_t>(kMergeThreads) / taken);
+            const std::uint32_t per = (taken + parts - 1u) / parts;
+            for (std::uint32_t u = static_cast<std::uint32_t>(t); u < taken * parts; u += blockDim.x) {
+                const std::uint32_t i = u / parts;
+                const std::uint32_t j0 = (u - i * parts) * per;
+                const std::uint32_t j1 = min(taken, j0 + per);
+                const std::uint64_t key = lds_keys[i];
+                std::uint32_t above = 0u;
+                for (std::uint32_t j = j0; j < j1; ++j) {
+                    above += lds_keys[j] > key ? 1u : 0u;
+                }
+                if (above != 0u) {
+                    atomicAdd(&rank_of[i], above);
+                }
+            }
+        }
+        __syncthreads();
+        for (std::uint32_t i = static_cast<std::uint32_t>(t); i < taken; i += blockDim.x) {
+            const std::uint32_t rank = rank_of[i];
+            const std::uint64_t key = lds_keys[i];
             dst[rank] = key;
             const std::size_t o = static_cast<std::size_t>(q) * k + rank;
             writeHit(key, &out_index[o], &out_score[o]);
             if (threshold != nullptr && rank == static_cast<std::uint32_t>(k) - 1u) {
                 threshold[q] = key;
             }
-        });
+        }
     } else {
         // Between phases only the set and its smallest key (the threshold) matter: the keys stay
         // in collection order.
@@ -452,11 +492,12 @@ __global__ __launch_bounds__(kMergeThreads) void selectMergeKernel(
             lds_wave_lo[t / kWave] = lo;
         }
         __syncthreads();
-        if (t == 0 && threshold != nullptr && taken >= static_cast<std::uint32_t>(k)) {
-            for (int w = 0; w < kMergeThreads / kWave; ++w) {
-                lo = min(lo, lds_wave_lo[w]);
+        if (t < kWave) {  // wavefront 0 reduces the per-wavefront minima
+            std::uint64_t v = t < kMergeThreads / kWave ? lds_wave_lo[t] : ~0ull;
+            v = waveReduce64(v, [](std::uint64_t a, std::uint64_t b) { return min(a, b); });
+            if (t == 0 && threshold != nullptr && taken >= static_cast<std::uint32_t>(k)) {
+                threshold[q] = v;
             }
-            threshold[q] = lo;
         }
     }
     for (int i = static_cast<int>(taken) + t; i < k; i += blockDim.x) {
