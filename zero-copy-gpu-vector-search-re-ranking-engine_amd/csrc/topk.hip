@@ -217,6 +217,45 @@ __device__ __forceinline__ void forEachCandidate(const MergeInputs& in, int q, i
 constexpr std::uint32_t kSelectLdsKeys = 12288;
 static_assert(kMaxK <= kSelectBins, "the ranks of a selection reuse the histogram");
 
+// Visits elements 0..n-1 (n uniform) with the block's threads, kBatch per thread per round:
+// `load(i)` for each of a thread's elements of the round first (an index past n is clamped to
+// n - 1, so every load reads inside the source), then `use(i, value)` for those below n.
+// Keeping the loads of a round apart from their uses lets them all be in flight at once.
+template <int kBatch, typename Load, typename Use>
+__device__ __forceinline__ void gatherRoundsOf(std::uint32_t n, Load& load, Use& use) {
+    const std::uint32_t t = threadIdx.x;
+    for (std::uint32_t r0 = 0; r0 < n; r0 += kBatch * blockDim.x) {
+        std::uint64_t value[kBatch];
+#pragma unroll
+        for (int b = 0; b < kBatch; ++b) {
+            value[b] = load(min(r0 + b * blockDim.x + t, n - 1u));
+        }
+#pragma unroll
+        for (int b = 0; b < kBatch; ++b) {
+            const std::uint32_t i = r0 + b * blockDim.x + t;
+            if (i < n) {
+                use(i, value[b]);
+            }
+        }
+    }
+}
+
+// The batch is the smallest of 1, 2, 4 or 8 that covers n in one round (8 beyond), so no thread
+// loads more clamped duplicates than needed.
+template <typename Load, typename Use>
+__device__ __forceinline__ void gatherRounds(std::uint32_t n, Load&& load, Use&& use) {
+    const std::uint32_t threads = blockDim.x;
+    if (n <= threads) {
+        gatherRoundsOf<1>(n, load, use);
+    } else if (n <= 2u * threads) {
+        gatherRoundsOf<2>(n, load, use);
+    } else if (n <= 4u * threads) {
+        gatherRoundsOf<4>(n, load, use);
+    } else {
+        gatherRoundsOf<8>(n, load, use);
+    }
+}
+
 __global__ __launch_bounds__(kMergeThreads) void selectMergeKernel(
     MergeInputs in, int k, int batch, std::uint64_t* __restrict__ out_keys,
     std::uint64_t* __restrict__ threshold, std::uint32_t* __restrict__ overflow,
@@ -291,44 +330,51 @@ __global__ __launch_bounds__(kMergeThreads) void selectMergeKernel(
     __syncthreads();
 
     if (in_lds) {
+        // Each thread handles up to eight keys at a time: their sources are found first (a
+        // segment search in LDS for segment keys) and all their loads are issued before any
+        // result is used, so the loads of one round are in flight together.
         if (k_prev > 0u) {
             const std::uint64_t* prev = in.prev + static_cast<std::size_t>(q) * in.k_prev;
-            for (std::uint32_t i = t; i < k_prev; i += blockDim.x) {
-                const std::uint64_t key = prev[i];
-                lds_cand[i] = key;
-                note(key);
-            }
+            gatherRounds(k_prev, [&](std::uint32_t i) { return prev[i]; },
+                         [&](std::uint32_t i, std::uint64_t key) {
+                             lds_cand[i] = key;
+                             note(key);
+                         });
         }
         if (n_dense > 0u) {
             const std::uint64_t* dense = in.dense + static_cast<std::size_t>(q) * in.dense_stride;
-#pragma unroll 8
-            for (std::uint32_t i = t; i < n_dense; i += blockDim.x) {
-                const std::uint64_t key = dense[i];
-                lds_cand[k_prev + i] = key;
-                note(key);
-            }
+            gatherRounds(n_dense, [&](std::uint32_t i) { return dense[i]; },
+                         [&](std::uint32_t i, std::uint64_t key) {
+                             lds_cand[k_prev + i] = key;
+                             note(key);
+                         });
         }
-        if (in.seg != nullptr) {
+        if (in.seg != nullptr && seg_total > 0u) {
             // Candidate i of the compacted list lives in the last segment whose offset is
             // <= i (empty segments share their successor's offset), at position i - offset.
+            // The search takes ceil(log2(n_seg)) halving steps for every key (a step after
+            // convergence keeps the segment), so the steps of a thread's keys run side by side.
             const std::uint32_t base = k_prev + n_dense;
-#pragma unroll 4
-            for (std::uint32_t i = t; i < seg_total; i += blockDim.x) {
-                int lo = 0;
-                int hi = in.n_seg - 1;
-                while (lo < hi) {
-                    const int mid = (lo + hi + 1) >> 1;
-                    if (lds_offset[mid] <= i) {
-                        lo = mid;
-                    } else {
-                        hi = mid - 1;
-                    }
-                }
-                const std::uint32_t j = i - lds_offset[lo];
-                const std::uint64_t key = in.seg[((static_cast<std::size_t>(lo) * batch + q) << in.seg_log2) + j];
-                lds_cand[base + i] = key;
-                note(key);
-            }
+            const int steps = in.n_seg > 1 ? 32 - __clz(static_cast<std::uint32_t>(in.n_seg - 1)) : 0;
+            gatherRounds(seg_total,
+                         [&](std::uint32_t i) {
+                             int lo = 0;
+                             int hi = in.n_seg - 1;
+                             for (int step = 0; step < steps; ++step) {
+                                 const int mid = (lo + hi + 1) >> 1;
+                                 if (lds_offset[mid] <= i) {
+                                     lo = mid;
+                                 } else {
+                                     hi = mid - 1;
+                                 }
+                             }
+                             const std::uint32_t j = i - lds_offset[lo];
+                             return in.seg[((static_cast<std::size_t>(lo) * batch + q) << in.seg_log2) + j];
+                         },
+                         [&](std::uint32_t i, std::uint64_t key) {
+                             lds_cand[base + i] = key;
+                             note(key);
+                         });
         }
     } else {
         forEachCandidate(in, q, batch, lds_seg, note);
