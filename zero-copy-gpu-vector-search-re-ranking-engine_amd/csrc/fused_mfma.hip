@@ -11,10 +11,13 @@
 // Skew. Of the two wavefronts of a SIMD (chosen at start-up from the hardware SIMD id) one leads
 // and one lags: after the tile barrier the leader multiplies tile t and then filters it, while
 // the lagger first filters tile t - 1 and then multiplies tile t. So each wavefront's VALU filter
-// work runs while the other keeps the SIMD's matrix core busy. A filter that passes owes an exact
-// pass; that pass runs right after the next barrier, before that step's tile copies are issued
-// (its keys go to an LDS staging buffer, so in the loop global stores, which would queue behind
-// the copies in the vmcnt order, happen only when that buffer is full).
+// work runs while the other keeps the SIMD's matrix core busy. The two roles run separate loops,
+// so a value one role keeps across the barrier takes no register in the other's multiply. A
+// filter that passes owes an exact pass, which reuses the row scales the filter read (up to
+// d = 768); the lagger runs it right after its filter, the leader right after the next barrier,
+// both before that step's tile copies are issued (its keys go to an LDS staging buffer, so in
+// the loop global stores, which would queue behind the copies in the vmcnt order, happen only
+// when that buffer is full).
 //
 // Candidate staging. A query's candidates in a workgroup come from exactly two lanes (its two
 // row halves), so each lane owns a candidate segment (segment 2 * workgroup + half) and counts
@@ -234,6 +237,9 @@ void mfmaScanKernel(ScanArgs scan, PhaseArgs phase, EmitArgs emit, int q_offset,
     // (reads, then per k-step two MFMAs and the reads kAhead steps further on) so an MFMA never
     // waits on an LDS read issued just before it.
     constexpr int kAhead = kKSteps < 3 ? kKSteps : 3;
+    // The exact pass reuses the row scales the filter read (no second LDS round trip) up to
+    // d = 768; at d = 1024 the 32 registers they take would not fit beside the query operands.
+    constexpr bool kCacheScales = kKSteps <= 24;
     auto multiply = [&](const std::uint8_t* tile, v16i& acc0, v16i& acc1) {
         const std::uint8_t* lane_tile[kPeriod];
 #pragma unroll
@@ -332,7 +338,11 @@ void mfmaScanKernel(ScanArgs scan, PhaseArgs phase, EmitArgs emit, int q_offset,
         // this product order and the exact score's, so every exact candidate's slot is set).
         // A masked or padding row (NaN scale) never passes here; such rows can qualify only
         // against a -FLT_MAX threshold, and then every slot is examined.
-        auto filter = [&](const v16i& acc0, const v16i& acc1, const float* scales) -> std::uint32_t {
+        auto filter = [&](const v16i& acc0, const v16i& acc1, const float* scales, float4 (&gs)[8]) -> std::uint32_t {
+#pragma unroll
+            for (int grp = 0; grp < 8; ++grp) {
+                gs[grp] = *reinterpret_cast<const float4*>(scales + (grp / 4) * 32 + 8 * (grp % 4) + 4 * half);
+            }
             if (examine_all) {
                 return 0xFFFFFFFFu;
             }
@@ -344,7 +354,7 @@ void mfmaScanKernel(ScanArgs scan, PhaseArgs phase, EmitArgs emit, int q_offset,
             for (int mb = 0; mb < 2; ++mb) {
 #pragma unroll
                 for (int g = 0; g < 4; ++g) {
-                    const float4 rs = *reinterpret_cast<const float4*>(scales + mb * 32 + 8 * g + 4 * half);
+                    const float4 rs = gs[4 * mb + g];
                     const float rsv[4] = {rs.x, rs.y, rs.z, rs.w};
                     float p[4];
 #pragma unroll
@@ -365,7 +375,7 @@ void mfmaScanKernel(ScanArgs scan, PhaseArgs phase, EmitArgs emit, int q_offset,
             for (int grp = 0; grp < 8; ++grp) {
                 if (__any(group_best[grp] >= relaxed_floor)) {
                     // the group's products again (same operations, same values)
-                    const float4 rs = *reinterpret_cast<const float4*>(scales + (grp / 4) * 32 + 8 * (grp % 4) + 4 * half);
+                    const float4 rs = gs[grp];
                     const float rsv[4] = {rs.x, rs.y, rs.z, rs.w};
 #pragma unroll
                     for (int j = 0; j < 4; ++j) {
@@ -409,8 +419,8 @@ void mfmaScanKernel(ScanArgs scan, PhaseArgs phase, EmitArgs emit, int q_offset,
         // Exact scores and keys of the value slots `passing` marks (slot 4 grp + j: row block
         // grp / 4, rows 32 (grp / 4) + 8 (grp % 4) + 4 half + j); keys above the threshold are
         // appended. A group's four row scales come in one LDS read.
-        auto exact = [&](const v16i& acc0, const v16i& acc1, const float* scales, long long row0,
-                         std::uint32_t passing) {
+        auto exact = [&](const v16i& acc0, const v16i& acc1, const float4 (&gs)[8], const float* scales,
+                         long long row0, std::uint32_t passing) {
             // Tile-relative rows in 32 bits; the empty asm keeps the compiler from hoisting the
             // per-row constants out of the scan loop into registers.
             int hb = 4 * half;
@@ -421,7 +431,7 @@ void mfmaScanKernel(ScanArgs scan, PhaseArgs phase, EmitArgs emit, int q_offset,
             for (int grp = 0; grp < 8; ++grp) {
                 if ((passing >> (4 * grp)) & 0xFu) {
                     const int rl0 = (grp / 4) * 32 + 8 * (grp % 4) + hb;
-                    const float4 rs4 = *reinterpret_cast<const float4*>(scales + rl0);
+                    const float4 rs4 = kCacheScales ? gs[grp] : *reinterpret_cast<const float4*>(scales + rl0);
                     const float rsv[4] = {rs4.x, rs4.y, rs4.z, rs4.w};
 #pragma unroll
                     for (int j = 0; j < 4; ++j) {
@@ -442,38 +452,60 @@ void mfmaScanKernel(ScanArgs scan, PhaseArgs phase, EmitArgs emit, int q_offset,
 
         v16i acc0 = {};
         v16i acc1 = {};
+        float4 gs[8];             // row scales of the tile in (acc0, acc1), as the filter read them
         long long acc_row0 = -1;  // first row of the tile in (acc0, acc1); -1 = none yet
         int acc_sslot = 0;
-        std::uint32_t owed = 0u;  // slots of the tile in (acc0, acc1) that owe an exact pass
-        for (; item < phase.items; item += stride_items) {
-            arrive(item);
-            if (wave_active && !lead && acc_row0 >= 0) {
-                owed = filter(acc0, acc1, scale_ring[acc_sslot]);
+        if (lead) {
+            // Leader: multiply tile t and filter it; the exact pass it owes runs after the next
+            // barrier, before that step's tile copies are issued.
+            std::uint32_t owed = 0u;
+            for (; item < phase.items; item += stride_items) {
+                arrive(item);
+                if (owed != 0u) {
+                    exact(acc0, acc1, gs, scale_ring[acc_sslot], acc_row0, owed);
+                }
+                owed = 0u;
+                // (issuing the refill before the pending exact pass measured slower: the pass's
+                // direct stores then queue behind the copies in the vmcnt order)
+                refill(item, slot, sslot);
+                if (wave_active) {
+                    multiply(ring[slot], acc0, acc1);
+                    acc_row0 = phaseBlock(item, phase.stride, phase.skip) * kRows;
+                    acc_sslot = sslot;
+                    owed = filter(acc0, acc1, scale_ring[sslot], gs);
+                }
+                slot = slot + 1 == kDepth ? 0 : slot + 1;
+                sslot = sslot + 1 == kScaleDepth ? 0 : sslot + 1;
             }
             if (owed != 0u) {
-                exact(acc0, acc1, scale_ring[acc_sslot], acc_row0, owed);
+                exact(acc0, acc1, gs, scale_ring[acc_sslot], acc_row0, owed);
             }
-            owed = 0u;
-            // (issuing the refill before the pending exact pass measured slower: the pass's
-            // direct stores then queue behind the copies in the vmcnt order)
-            refill(item, slot, sslot);
-            if (wave_active) {
-                multiply(ring[slot], acc0, acc1);
-                acc_row0 = phaseBlock(item, phase.stride, phase.skip) * kRows;
-                acc_sslot = sslot;
-                if (lead) {
-                    owed = filter(acc0, acc1, scale_ring[sslot]);
+        } else {
+            // Lagger: filter tile t - 1 and run its exact pass, then multiply tile t.
+            for (; item < phase.items; item += stride_items) {
+                arrive(item);
+                if (wave_active && acc_row0 >= 0) {
+                    const std::uint32_t owed = filter(acc0, acc1, scale_ring[acc_sslot], gs);
+                    if (owed != 0u) {
+                        exact(acc0, acc1, gs, scale_ring[acc_sslot], acc_row0, owed);
+                    }
+                }
+                refill(item, slot, sslot);
+                if (wave_active) {
+                    multiply(ring[slot], acc0, acc1);
+                    acc_row0 = phaseBlock(item, phase.stride, phase.skip) * kRows;
+                    acc_sslot = sslot;
+                }
+                slot = slot + 1 == kDepth ? 0 : slot + 1;
+                sslot = sslot + 1 == kScaleDepth ? 0 : sslot + 1;
+            }
+            // the last tile
+            if (wave_active && acc_row0 >= 0) {
+                const std::uint32_t owed = filter(acc0, acc1, scale_ring[acc_sslot], gs);
+                if (owed != 0u) {
+                    exact(acc0, acc1, gs, scale_ring[acc_sslot], acc_row0, owed);
                 }
             }
-            slot = slot + 1 == kDepth ? 0 : slot + 1;
-            sslot = sslot + 1 == kScaleDepth ? 0 : sslot + 1;
-        }
-        // the last tile
-        if (wave_active && !lead && acc_row0 >= 0) {
-            owed = filter(acc0, acc1, scale_ring[acc_sslot]);
-        }
-        if (owed != 0u) {
-            exact(acc0, acc1, scale_ring[acc_sslot], acc_row0, owed);
         }
 
         // write the parked candidates of this wavefront, then every lane's count
