@@ -512,10 +512,17 @@ void mfmaBinaryStreamKernel(ScanArgs scan, PhaseArgs phase, EmitArgs emit, int q
         v4i a[2];
         a[0] = spreadWord(stepWord<kLaneChunks>(cur[0], 0), 0);
         a[1] = spreadWord(stepWord<kLaneChunks>(cur[1], 0), 0);
+        // the B operands of step t + 1 are read from LDS during step t
+        v4i b0 = qlds[0][0][lane];
+        v4i b1 = qlds[0][1][lane];
 #pragma unroll
         for (int t = 0; t < kSteps; ++t) {
-            const v4i b0 = qlds[t][0][lane];
-            const v4i b1 = qlds[t][1][lane];
+            v4i nb0 = b0;
+            v4i nb1 = b1;
+            if (t + 1 < kSteps) {
+                nb0 = qlds[t + 1][0][lane];
+                nb1 = qlds[t + 1][1][lane];
+            }
             acc[0][0] = __builtin_amdgcn_mfma_i32_16x16x64_i8(a[0], b0, acc[0][0], 0, 0, 0);
             acc[0][1] = __builtin_amdgcn_mfma_i32_16x16x64_i8(a[0], b1, acc[0][1], 0, 0, 0);
             acc[1][0] = __builtin_amdgcn_mfma_i32_16x16x64_i8(a[1], b0, acc[1][0], 0, 0, 0);
@@ -524,6 +531,8 @@ void mfmaBinaryStreamKernel(ScanArgs scan, PhaseArgs phase, EmitArgs emit, int q
                 a[0] = spreadWord(stepWord<kLaneChunks>(cur[0], t + 1), (t + 1) % 2);
                 a[1] = spreadWord(stepWord<kLaneChunks>(cur[1], t + 1), (t + 1) % 2);
             }
+            b0 = nb0;
+            b1 = nb1;
             // step by step: the compiler would otherwise hoist every step's B reads up front
             __builtin_amdgcn_sched_barrier(0);
         }
