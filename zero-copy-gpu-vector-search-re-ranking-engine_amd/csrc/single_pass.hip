@@ -7,7 +7,8 @@
 // (W workgroups, L lanes per row) and keeps, per query, every key above its own running
 // threshold in an LDS list. When a list could
 // overflow before the next check, the workgroup selects its `width` best keys by radix passes over
-// the list (select.hpp) and raises the threshold to the smallest of them, so the list is exact:
+// the list (select.hpp), or by ranking every key when the list holds at most 256, and raises the
+// threshold to the smallest of them, so the list is exact:
 // it always holds the workgroup's true top-`width`. At the end each workgroup writes its
 // top-`width` to its candidate segment, and the per-query merge (topk.hip) selects the global
 // top-`width` from the segments; for wide selections groups of workgroups are merged first. A
@@ -35,6 +36,7 @@ constexpr int kSpChunksPerLane = 8;  // with 8 lanes at least: the VALU scan's r
 constexpr int kSpMinLanes = 8;
 constexpr int kSpListKeys = 12288;  // LDS keys of all queries' lists together (96 KB)
 constexpr int kSpMinCap = 1024;     // keys per query list at least
+constexpr int kSpRankKeys = 256;    // lists up to this long are compacted by ranking, not radix passes
 constexpr int kKindI8I8 = 4;
 constexpr std::size_t kSpQueryLds = 32 * 1024;
 
@@ -134,6 +136,50 @@ __global__ __launch_bounds__(kSpThreads) void singlePassScanKernel(ScanArgs scan
         const std::uint32_t count = lds_count[q];
         if (count <= static_cast<std::uint32_t>(width)) {
             return;  // (uniform: read after a barrier)
+        }
+        if (count <= static_cast<std::uint32_t>(kSpRankKeys)) {
+            // A short list: every key's rank (the number of keys above it, all keys unique) from
+            // `parts` threads per key whose counts meet in LDS, then the best `width` move to
+            // their ranks. Four barriers instead of the radix passes' dozens.
+            std::uint32_t* rank_of = lds_hist;
+            for (std::uint32_t i = static_cast<std::uint32_t>(t); i < count; i += kSpThreads) {
+                rank_of[i] = 0u;
+            }
+            __syncthreads();
+            const std::uint32_t parts = static_cast<std::uint32_t>(kSpThreads) / count;
+            const std::uint32_t per = (count + parts - 1u) / parts;
+            if (static_cast<std::uint32_t>(t) < count * parts) {
+                const std::uint32_t i = static_cast<std::uint32_t>(t) / parts;
+                const std::uint32_t j0 = (static_cast<std::uint32_t>(t) - i * parts) * per;
+                const std::uint32_t j1 = min(count, j0 + per);
+                const std::uint64_t key = list[i];
+                std::uint32_t above = 0u;
+                for (std::uint32_t j = j0; j < j1; ++j) {
+                    above += list[j] > key ? 1u : 0u;
+                }
+                if (above != 0u) {
+                    atomicAdd(&rank_of[i], above);
+                }
+            }
+            __syncthreads();
+            std::uint64_t key = 0ull;
+            std::uint32_t rank = ~0u;
+            if (static_cast<std::uint32_t>(t) < count) {
+                key = list[t];
+                rank = rank_of[t];
+            }
+            __syncthreads();  // every key read before any moves
+            if (rank < static_cast<std::uint32_t>(width)) {
+                list[rank] = key;
+                if (rank == static_cast<std::uint32_t>(width) - 1u) {
+                    lds_tau[q] = key;
+                }
+            }
+            if (t == 0) {
+                lds_count[q] = static_cast<std::uint32_t>(width);
+            }
+            __syncthreads();
+            return;
         }
         if (t == 0) {
             lds_state.prefix = 0ull;
