@@ -787,9 +787,17 @@ int searchTopk(const zcgvs_search_desc* desc, void* d_workspace, std::size_t wor
             }
         }
         in.reset_overflow = true;  // (segments hold at most width keys: the flags end cleared)
-        status = launchSelectMerge(in, plan.width, batch, keys, nullptr, overflow,
-                                   plan.rescore ? nullptr : d_out_indices,
-                                   plan.rescore ? nullptr : d_out_values, s);
+        if (plan.sp_groups == 1 && plan.width <= kSortedMergeMaxK && in.n_seg <= kSortedMergeMaxSegments) {
+            // each workgroup's list is sorted (single_pass.hip): the merge reads at most width
+            // segments past their first key
+            status = launchSortedSegmentMerge(in, plan.width, batch, keys, overflow,
+                                              plan.rescore ? nullptr : d_out_indices,
+                                              plan.rescore ? nullptr : d_out_values, s);
+        } else {
+            status = launchSelectMerge(in, plan.width, batch, keys, nullptr, overflow,
+                                       plan.rescore ? nullptr : d_out_indices,
+                                       plan.rescore ? nullptr : d_out_values, s);
+        }
         if (status != ZCGVS_OK) {
             return status;
         }

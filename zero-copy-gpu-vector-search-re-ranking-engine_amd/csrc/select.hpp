@@ -171,4 +171,13 @@ int launchSelectMerge(const MergeInputs& in, int k, int batch, std::uint64_t* ou
                       std::uint64_t* threshold, std::uint32_t* overflow, int* out_index,
                       float* out_score, hipStream_t stream);
 
+// The same selection (segments only, no threshold) for candidate segments that each hold at most
+// k keys sorted descending, as the single-pass scan writes them: the k-th best segment head bounds
+// the result from below, so only the segments whose head reaches it (at most k) are read past
+// their first key. For k <= kSortedMergeMaxK and n_seg <= kSortedMergeMaxSegments.
+constexpr int kSortedMergeMaxK = 32;
+constexpr int kSortedMergeMaxSegments = 1024;
+int launchSortedSegmentMerge(const MergeInputs& in, int k, int batch, std::uint64_t* out_keys,
+                             std::uint32_t* overflow, int* out_index, float* out_score, hipStream_t stream);
+
 }  // namespace zcgvs_hip

@@ -10,8 +10,10 @@
 // the list (select.hpp), or by ranking every key when the list holds at most 256, and raises the
 // threshold to the smallest of them, so the list is exact:
 // it always holds the workgroup's true top-`width`. At the end each workgroup writes its
-// top-`width` to its candidate segment, and the per-query merge (topk.hip) selects the global
-// top-`width` from the segments; for wide selections groups of workgroups are merged first. A
+// top-`width` to its candidate segment (sorted descending when width <= 256), and the per-query
+// merge (topk.hip) selects the global top-`width` from the segments: for width <= 32 from the
+// segments whose first key reaches the width-th best first key, for wide selections after
+// merging groups of workgroups first. A
 // list holds max(1024, 4 * width) keys (less when four queries share the LDS), so compactions
 // are rare. Nothing can overflow, so no fallback pass follows.
 //
@@ -129,6 +131,51 @@ __global__ __launch_bounds__(kSpThreads) void singlePassScanKernel(ScanArgs scan
     __syncthreads();
 
     const int cap = args.cap;  // keys per query list (width + at least one check's appends)
+    // Keeps the best min(count, width) of query q's `count` list keys (2 <= count <= kSpRankKeys),
+    // sorted descending at the front of the list: every key's rank (the number of keys above it;
+    // all keys are unique) from `parts` threads per key whose counts meet in LDS, then the kept
+    // keys move to their ranks. Four barriers instead of the radix passes' dozens.
+    auto rankKeep = [&](int q, std::uint32_t count) __attribute__((always_inline)) {
+        std::uint64_t* list = lds_keys + q * cap;
+        std::uint32_t* rank_of = lds_hist;
+        for (std::uint32_t i = static_cast<std::uint32_t>(t); i < count; i += kSpThreads) {
+            rank_of[i] = 0u;
+        }
+        __syncthreads();
+        const std::uint32_t parts = static_cast<std::uint32_t>(kSpThreads) / count;
+        const std::uint32_t per = (count + parts - 1u) / parts;
+        if (static_cast<std::uint32_t>(t) < count * parts) {
+            const std::uint32_t i = static_cast<std::uint32_t>(t) / parts;
+            const std::uint32_t j0 = (static_cast<std::uint32_t>(t) - i * parts) * per;
+            const std::uint32_t j1 = min(count, j0 + per);
+            const std::uint64_t key = list[i];
+            std::uint32_t above = 0u;
+            for (std::uint32_t j = j0; j < j1; ++j) {
+                above += list[j] > key ? 1u : 0u;
+            }
+            if (above != 0u) {
+                atomicAdd(&rank_of[i], above);
+            }
+        }
+        __syncthreads();
+        std::uint64_t key = 0ull;
+        std::uint32_t rank = ~0u;
+        if (static_cast<std::uint32_t>(t) < count) {
+            key = list[t];
+            rank = rank_of[t];
+        }
+        __syncthreads();  // every key read before any moves
+        if (rank < static_cast<std::uint32_t>(width)) {
+            list[rank] = key;
+            if (rank == static_cast<std::uint32_t>(width) - 1u) {
+                lds_tau[q] = key;
+            }
+        }
+        if (t == 0) {
+            lds_count[q] = min(count, static_cast<std::uint32_t>(width));
+        }
+        __syncthreads();
+    };
     // Keeps the `width` best keys of query q's list (every thread calls it; q is uniform) and
     // sets the list's threshold to the smallest of them.
     auto compact = [&](int q) __attribute__((always_inline)) {
@@ -138,47 +185,7 @@ __global__ __launch_bounds__(kSpThreads) void singlePassScanKernel(ScanArgs scan
             return;  // (uniform: read after a barrier)
         }
         if (count <= static_cast<std::uint32_t>(kSpRankKeys)) {
-            // A short list: every key's rank (the number of keys above it, all keys unique) from
-            // `parts` threads per key whose counts meet in LDS, then the best `width` move to
-            // their ranks. Four barriers instead of the radix passes' dozens.
-            std::uint32_t* rank_of = lds_hist;
-            for (std::uint32_t i = static_cast<std::uint32_t>(t); i < count; i += kSpThreads) {
-                rank_of[i] = 0u;
-            }
-            __syncthreads();
-            const std::uint32_t parts = static_cast<std::uint32_t>(kSpThreads) / count;
-            const std::uint32_t per = (count + parts - 1u) / parts;
-            if (static_cast<std::uint32_t>(t) < count * parts) {
-                const std::uint32_t i = static_cast<std::uint32_t>(t) / parts;
-                const std::uint32_t j0 = (static_cast<std::uint32_t>(t) - i * parts) * per;
-                const std::uint32_t j1 = min(count, j0 + per);
-                const std::uint64_t key = list[i];
-                std::uint32_t above = 0u;
-                for (std::uint32_t j = j0; j < j1; ++j) {
-                    above += list[j] > key ? 1u : 0u;
-                }
-                if (above != 0u) {
-                    atomicAdd(&rank_of[i], above);
-                }
-            }
-            __syncthreads();
-            std::uint64_t key = 0ull;
-            std::uint32_t rank = ~0u;
-            if (static_cast<std::uint32_t>(t) < count) {
-                key = list[t];
-                rank = rank_of[t];
-            }
-            __syncthreads();  // every key read before any moves
-            if (rank < static_cast<std::uint32_t>(width)) {
-                list[rank] = key;
-                if (rank == static_cast<std::uint32_t>(width) - 1u) {
-                    lds_tau[q] = key;
-                }
-            }
-            if (t == 0) {
-                lds_count[q] = static_cast<std::uint32_t>(width);
-            }
-            __syncthreads();
+            rankKeep(q, count);
             return;
         }
         if (t == 0) {
@@ -428,8 +435,16 @@ __global__ __launch_bounds__(kSpThreads) void singlePassScanKernel(ScanArgs scan
         check();
     }
     __syncthreads();
+    // The final lists: each workgroup's top-`width`, sorted descending when width <= kSpRankKeys
+    // (the merge of narrow selections relies on it).
     for (int q = 0; q < q_count; ++q) {
+        const std::uint32_t before = lds_count[q];
         compact(q);
+        const bool ranked = before > static_cast<std::uint32_t>(width) && before <= static_cast<std::uint32_t>(kSpRankKeys);
+        const std::uint32_t count = lds_count[q];  // (uniform: compact ends with a barrier)
+        if (width <= kSpRankKeys && !ranked && count >= 2u) {
+            rankKeep(q, count);  // a list compact left as it was, or compacted by radix passes
+        }
     }
     __syncthreads();
     // This workgroup's top-`width` of every query -> its candidate segment. With G merge groups

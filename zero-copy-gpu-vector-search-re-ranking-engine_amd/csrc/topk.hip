@@ -563,6 +563,105 @@ __global__ __launch_bounds__(kMergeThreads) void selectMergeKernel(
     }
 }
 
+// ---- merge of sorted segments (one block per query) ---------------------------------------------
+
+constexpr int kSortedMergeThreads = 256;
+
+// Every segment s holds c_s <= k keys in descending order. With T the k-th largest non-zero
+// segment head (or every key when fewer than k heads are non-zero), the k best keys are all at
+// least T (k heads are), and each lies in a segment whose head is at least T: at most k segments
+// of at most k keys, ranked by comparison.
+__global__ __launch_bounds__(kSortedMergeThreads) void sortedSegmentMergeKernel(
+    MergeInputs in, int k, int batch, std::uint64_t* __restrict__ out_keys, std::uint32_t* __restrict__ overflow,
+    int* __restrict__ out_index, float* __restrict__ out_score) {
+    __shared__ std::uint64_t lds_head[kSortedMergeMaxSegments];
+    __shared__ std::uint32_t lds_count[kSortedMergeMaxSegments];
+    __shared__ int lds_segs[kSortedMergeMaxK];
+    __shared__ std::uint64_t lds_pick[kSortedMergeMaxK * kSortedMergeMaxK];
+    __shared__ std::uint64_t lds_cut;
+    __shared__ std::uint32_t lds_nsegs;
+    __shared__ std::uint32_t lds_taken;
+
+    const int q = blockIdx.x;
+    const int t = threadIdx.x;
+    const int n_seg = in.n_seg;
+    const std::uint32_t cap = 1u << in.seg_log2;
+    auto segment = [&](int s) { return in.seg + ((static_cast<std::size_t>(s) * batch + q) << in.seg_log2); };
+    for (int s = t; s < n_seg; s += kSortedMergeThreads) {
+        // both loads at once: the first slot is read whatever the count (an empty segment's slot
+        // holds a stale key, which the count then discards)
+        const std::uint32_t c = min(in.seg_count[static_cast<std::size_t>(s) * batch + q], cap);
+        const std::uint64_t first = segment(s)[0];
+        lds_count[s] = c;
+        lds_head[s] = c > 0u ? first : 0ull;
+    }
+    if (t == 0) {
+        lds_cut = 1ull;  // fewer than k non-zero heads: every non-zero key
+        lds_nsegs = 0u;
+        lds_taken = 0u;
+    }
+    __syncthreads();
+    for (int s = t; s < n_seg; s += kSortedMergeThreads) {
+        const std::uint64_t head = lds_head[s];
+        if (head != 0ull) {
+            int above = 0;
+            for (int j = 0; j < n_seg; ++j) {
+                above += lds_head[j] > head ? 1 : 0;
+            }
+            if (above == k - 1) {
+                lds_cut = head;
+            }
+        }
+    }
+    __syncthreads();
+    const std::uint64_t cut = lds_cut;
+    for (int s = t; s < n_seg; s += kSortedMergeThreads) {
+        if (lds_head[s] >= cut) {  // (a zero head never reaches cut >= 1)
+            lds_segs[atomicAdd(&lds_nsegs, 1u)] = s;  // at most k segments
+        }
+    }
+    __syncthreads();
+    const int nsegs = static_cast<int>(lds_nsegs);
+    for (int i = t; i < nsegs * k; i += kSortedMergeThreads) {
+        const int s = lds_segs[i / k];
+        const int j = i - (i / k) * k;
+        if (static_cast<std::uint32_t>(j) < lds_count[s]) {
+            const std::uint64_t key = segment(s)[j];
+            if (key >= cut) {
+                lds_pick[atomicAdd(&lds_taken, 1u)] = key;  // at most k * k keys
+            }
+        }
+    }
+    __syncthreads();
+    const int picked = static_cast<int>(lds_taken);
+    const int taken = min(picked, k);
+    std::uint64_t* dst = out_keys + static_cast<std::size_t>(q) * k;
+    for (int i = t; i < picked; i += kSortedMergeThreads) {
+        const std::uint64_t key = lds_pick[i];
+        int rank = 0;
+        for (int j = 0; j < picked; ++j) {
+            rank += lds_pick[j] > key ? 1 : 0;  // keys are unique
+        }
+        if (rank < k) {
+            dst[rank] = key;
+            if (out_index != nullptr) {
+                const std::size_t o = static_cast<std::size_t>(q) * k + rank;
+                writeHit(key, &out_index[o], &out_score[o]);
+            }
+        }
+    }
+    for (int i = taken + t; i < k; i += kSortedMergeThreads) {
+        dst[i] = 0ull;
+        if (out_index != nullptr) {
+            const std::size_t o = static_cast<std::size_t>(q) * k + i;
+            writeHit(0ull, &out_index[o], &out_score[o]);
+        }
+    }
+    if (t == 0 && overflow != nullptr && in.reset_overflow) {
+        overflow[q] = 0u;  // (no segment holds more than its k keys)
+    }
+}
+
 int topkScratchElements(int doc_count, int k) {
     if (doc_count <= 0 || k <= 0) {
         return 0;
@@ -583,6 +682,18 @@ int launchSelectMerge(const MergeInputs& in, int k, int batch, std::uint64_t* ou
     selectMergeKernel<<<batch, kMergeThreads, 0, stream>>>(in, k, batch, out_keys, threshold,
                                                             overflow, out_index, out_score);
     ZCGVS_LAUNCH_CHECK("select merge");
+    return ZCGVS_OK;
+}
+
+int launchSortedSegmentMerge(const MergeInputs& in, int k, int batch, std::uint64_t* out_keys,
+                             std::uint32_t* overflow, int* out_index, float* out_score, hipStream_t stream) {
+    if (k < 1 || k > kSortedMergeMaxK || in.n_seg < 1 || in.n_seg > kSortedMergeMaxSegments || in.seg == nullptr ||
+        in.prev != nullptr || in.dense != nullptr || (1 << in.seg_log2) < k) {
+        return setError(ZCGVS_ERR_RUNTIME, "zcgvs select: sorted-segment merge does not take this shape");
+    }
+    sortedSegmentMergeKernel<<<batch, kSortedMergeThreads, 0, stream>>>(in, k, batch, out_keys, overflow,
+                                                                        out_index, out_score);
+    ZCGVS_LAUNCH_CHECK("sorted-segment merge");
     return ZCGVS_OK;
 }
 
