@@ -80,6 +80,54 @@ __global__ __launch_bounds__(kSpThreads) void singlePassScanKernel(ScanArgs scan
     const long long n = scan.doc_count;
     const int words = chunks * spWordsPerChunk(kKind);
 
+    const int cap = args.cap;  // keys per query list (width + at least one check's appends)
+    const int lane = t & (kWave - 1);
+    const int group = lane % L;
+    // A step: kSets row sets of kSpThreads / L consecutive rows; a lane reads kPerRow chunks of
+    // its row in every set (several sets for short rows, so each lane keeps up to
+    // kSpChunksPerLane chunks in flight).
+    constexpr int kGroupsPerSet = kSpThreads / L;
+    constexpr int kRowsPerStep = kGroupsPerSet * kSets;
+    constexpr int kPer = kSpChunksPerLane;
+    constexpr int kPerRow = kPer / kSets;
+    static_assert(kPerRow * kSets == kPer, "row sets split the lane's chunks evenly");
+    // steps between capacity checks: every list takes at most kRowsPerStep keys per step (the
+    // host makes cap - width at least one step's rows)
+    const int check_every = (cap - width) / kRowsPerStep;
+    const std::size_t row_bytes = static_cast<std::size_t>(chunks) * 16;
+    const std::uint8_t* corpus = static_cast<const std::uint8_t*>(scan.corpus);
+    const bool l2 = scan.metric == ZCGVS_METRIC_L2;
+    // Steps interleave over the workgroups (workgroup b takes steps b, b + W, ...), so the
+    // workgroups stream neighbouring rows at any moment.
+    const long long begin = static_cast<long long>(blockIdx.x) * kRowsPerStep;
+    const long long stride = static_cast<long long>(gridDim.x) * kRowsPerStep;
+    const long long end = n;
+
+    // this lane's chunks of its rows in the step starting at `base` (rows past the corpus and
+    // masked rows are not read)
+    auto loadStep = [&](long long base, uint4 (&raw)[kPer]) __attribute__((always_inline)) {
+#pragma unroll
+        for (int set = 0; set < kSets; ++set) {
+            const long long row = base + set * kGroupsPerSet + t / L;
+            const long long r = row < end ? row : end - 1;
+            const bool skip = row >= end || (scan.mask != nullptr && scan.mask[r] == 0);
+#pragma unroll
+            for (int i = 0; i < kPerRow; ++i) {
+                const int c = group + i * L;
+                uint4& chunk = raw[set * kPerRow + i];
+                chunk = make_uint4(0u, 0u, 0u, 0u);
+                if (!skip && c < chunks) {
+                    chunk = loadChunkStreaming(corpus + static_cast<std::size_t>(r) * row_bytes + static_cast<std::size_t>(c) * 16);
+                }
+            }
+        }
+    };
+    // The first step's loads go out before the queries are staged, so the two round trips overlap.
+    uint4 raw[kPer];
+    if (begin < end) {
+        loadStep(begin, raw);
+    }
+
     // ---- the queries, staged as the VALU scan stages them ----
     for (int q = 0; q < q_count; ++q) {
         std::uint32_t* staged = lds_query + q * words;
@@ -130,7 +178,6 @@ __global__ __launch_bounds__(kSpThreads) void singlePassScanKernel(ScanArgs scan
     }
     __syncthreads();
 
-    const int cap = args.cap;  // keys per query list (width + at least one check's appends)
     // Keeps the best min(count, width) of query q's `count` list keys (2 <= count <= kSpRankKeys),
     // sorted descending at the front of the list: every key's rank (the number of keys above it;
     // all keys are unique) from `parts` threads per key whose counts meet in LDS, then the kept
@@ -270,47 +317,6 @@ __global__ __launch_bounds__(kSpThreads) void singlePassScanKernel(ScanArgs scan
         __syncthreads();
     };
 
-    const int lane = t & (kWave - 1);
-    const int group = lane % L;
-    // A step: kSets row sets of kSpThreads / L consecutive rows; a lane reads kPerRow chunks of
-    // its row in every set (several sets for short rows, so each lane keeps up to
-    // kSpChunksPerLane chunks in flight).
-    constexpr int kGroupsPerSet = kSpThreads / L;
-    constexpr int kRowsPerStep = kGroupsPerSet * kSets;
-    constexpr int kPer = kSpChunksPerLane;
-    constexpr int kPerRow = kPer / kSets;
-    static_assert(kPerRow * kSets == kPer, "row sets split the lane's chunks evenly");
-    // steps between capacity checks: every list takes at most kRowsPerStep keys per step (the
-    // host makes cap - width at least one step's rows)
-    const int check_every = (cap - width) / kRowsPerStep;
-    const std::size_t row_bytes = static_cast<std::size_t>(chunks) * 16;
-    const std::uint8_t* corpus = static_cast<const std::uint8_t*>(scan.corpus);
-    const bool l2 = scan.metric == ZCGVS_METRIC_L2;
-    // Steps interleave over the workgroups (workgroup b takes steps b, b + W, ...), so the
-    // workgroups stream neighbouring rows at any moment.
-    const long long begin = static_cast<long long>(blockIdx.x) * kRowsPerStep;
-    const long long stride = static_cast<long long>(gridDim.x) * kRowsPerStep;
-    const long long end = n;
-
-    // this lane's chunks of its rows in the step starting at `base` (rows past the corpus and
-    // masked rows are not read)
-    auto loadStep = [&](long long base, uint4 (&raw)[kPer]) __attribute__((always_inline)) {
-#pragma unroll
-        for (int set = 0; set < kSets; ++set) {
-            const long long row = base + set * kGroupsPerSet + t / L;
-            const long long r = row < end ? row : end - 1;
-            const bool skip = row >= end || (scan.mask != nullptr && scan.mask[r] == 0);
-#pragma unroll
-            for (int i = 0; i < kPerRow; ++i) {
-                const int c = group + i * L;
-                uint4& chunk = raw[set * kPerRow + i];
-                chunk = make_uint4(0u, 0u, 0u, 0u);
-                if (!skip && c < chunks) {
-                    chunk = loadChunkStreaming(corpus + static_cast<std::size_t>(r) * row_bytes + static_cast<std::size_t>(c) * 16);
-                }
-            }
-        }
-    };
     // scores of the step's rows against every query, keys above each list's threshold appended
     auto scoreStep = [&](long long base, const uint4 (&raw_step)[kPer]) __attribute__((always_inline)) {
 #pragma unroll
@@ -428,11 +434,12 @@ __global__ __launch_bounds__(kSpThreads) void singlePassScanKernel(ScanArgs scan
         }
     };
 
-    uint4 raw[kPer];
     for (long long base = begin; base < end; base += stride) {
-        loadStep(base, raw);
         scoreStep(base, raw);
         check();
+        if (base + stride < end) {
+            loadStep(base + stride, raw);
+        }
     }
     __syncthreads();
     // The final lists: each workgroup's top-`width`, sorted descending when width <= kSpRankKeys
