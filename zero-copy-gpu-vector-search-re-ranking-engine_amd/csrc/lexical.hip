@@ -11,7 +11,7 @@
 //
 // The fused search's default needs no atomics in global memory and no separate clearing or
 // maximum pass. With every term's postings ascending by document, bm25BoundsKernel finds where
-// each query term's postings cross every 1024-document boundary (one binary search per thread,
+// each query term's postings cross every 2048-document boundary (one binary search per thread,
 // all at once), and bm25SweepKernel, one workgroup per (query, slice), loads its slice of every
 // term's postings, adds them into an LDS accumulator slot by slot in slot order (the same
 // per-document order), then writes the slice, zeros included, and folds its maximum into the
@@ -30,7 +30,9 @@ namespace {
 constexpr int kPostingThreads = 256;
 constexpr int kReduceThreads = 256;
 constexpr int kSweepThreads = 256;
-constexpr int kSweepDocs = 1024;              // documents per sweep workgroup
+// documents per sweep workgroup (measured on the 1M-document hybrid search: 2048 takes the BM25
+// stage 9 us below 1024 with half the bound searches; 4096 is slower)
+constexpr int kSweepDocs = 2048;
 constexpr int kSweepPerThread = kSweepDocs / kSweepThreads;  // postings per thread per slot
 // slots whose postings are loaded together: two keep the sweep at about 40 registers, so more
 // (query, slice) workgroups are resident to hide each other's load latency (measured: 8 slots
@@ -118,9 +120,10 @@ __global__ void bm25BoundsKernel(const std::int64_t* __restrict__ offsets, const
 // BM25 scores of documents [blockIdx.x * kSweepDocs, + kSweepDocs) for query blockIdx.y from the
 // postings between the slice bounds; writes every score of the slice and raises lexical_max[q]
 // (zeroed beforehand) to the slice's max(0, max score). A slot's postings inside one slice are
-// distinct documents, so there are at most kSweepDocs of them: thread t loads postings
-// begin + 4t .. + 3 with one 16-byte load of documents and one of weights (a range's last load
-// starts at end - 4, so no load leaves the range; ranges under 4 postings load them one by one),
+// distinct documents, so there are at most kSweepDocs of them: thread t loads the
+// kSweepPerThread = 8 postings from begin + 8t with two 16-byte loads of documents and two of
+// weights (a range's last thread starts at end - 8, so no load leaves the range; ranges under 8
+// postings load them one by one),
 // for kSweepSlotGroup slots at a time, before any is added, and the additions of one slot touch
 // distinct accumulator entries.
 //
@@ -219,9 +222,12 @@ __global__ __launch_bounds__(kSweepThreads) void bm25SweepKernel(
     float best = 0.0f;
     float* row = scores + static_cast<std::size_t>(q) * doc_count + d0;
     if (d1 - d0 == kSweepDocs && (reinterpret_cast<std::uintptr_t>(row) & 15u) == 0) {
-        const float4 value = reinterpret_cast<const float4*>(acc)[t];
-        reinterpret_cast<float4*>(row)[t] = value;
-        best = fmaxf(fmaxf(value.x, value.y), fmaxf(value.z, value.w));
+#pragma unroll
+        for (int i = t; i < kSweepDocs / 4; i += kSweepThreads) {
+            const float4 value = reinterpret_cast<const float4*>(acc)[i];
+            reinterpret_cast<float4*>(row)[i] = value;
+            best = fmaxf(best, fmaxf(fmaxf(value.x, value.y), fmaxf(value.z, value.w)));
+        }
     } else {
         for (int i = t; i < d1 - d0; i += kSweepThreads) {
             const float value = acc[i];
