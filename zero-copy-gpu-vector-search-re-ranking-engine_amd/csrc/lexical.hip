@@ -11,7 +11,7 @@
 //
 // The fused search's default needs no atomics in global memory and no separate clearing or
 // maximum pass. With every term's postings ascending by document, bm25BoundsKernel finds where
-// each query term's postings cross every 2048-document boundary (one binary search per thread,
+// each query term's postings cross every 4096-document boundary (one binary search per thread,
 // all at once), and bm25SweepKernel, one workgroup per (query, slice), loads its slice of every
 // term's postings, adds them into an LDS accumulator slot by slot in slot order (the same
 // per-document order), then writes the slice, zeros included, and folds its maximum into the
@@ -29,10 +29,11 @@ namespace {
 
 constexpr int kPostingThreads = 256;
 constexpr int kReduceThreads = 256;
-constexpr int kSweepThreads = 256;
-// documents per sweep workgroup (measured on the 1M-document hybrid search: 2048 takes the BM25
-// stage 9 us below 1024 with half the bound searches; 4096 is slower)
-constexpr int kSweepDocs = 2048;
+constexpr int kSweepThreads = 512;
+// documents per sweep workgroup (measured on the 1M-document hybrid search, BM25 stage: 1024
+// documents and 256 threads 114 us, 2048 and 256 threads 105 us, 4096 and 512 threads 100 us;
+// 4096 and 256, 8192 and 1024, or one slot per load group are slower)
+constexpr int kSweepDocs = 4096;
 constexpr int kSweepPerThread = kSweepDocs / kSweepThreads;  // postings per thread per slot
 // slots whose postings are loaded together: two keep the sweep at about 40 registers, so more
 // (query, slice) workgroups are resident to hide each other's load latency (measured: 8 slots
