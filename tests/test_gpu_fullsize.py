@@ -137,8 +137,8 @@ def test_one_million_hybrid_bm25_fp16(gpu):
     """The hybrid configuration at its stated size: N = 1,000,000 documents, vocabulary 30,000,
     Poisson(200) lengths, Zipf(1.1) tokens, 8 distinct Zipf terms per query, BM25 k1 = 1.2,
     b = 0.75, fp16 d = 384 cosine, fusion weight 0.5, batch 16, k = 10 - the sliced BM25 sweep over
-    sorted postings (about 977 slices, head terms with df near N) against the oracle's BM25,
-    maximum and fusion (src/cuda/lexical.cu:17-74, tests/cuda/test_lexical.cu:71-93), then the
+    sorted postings (245 slices of 4096 documents, head terms with df near N) against the oracle's
+    BM25, maximum and fusion (src/cuda/lexical.cu:17-74, tests/cuda/test_lexical.cu:71-93), then the
     same search with the postings scattered (the default, any order), bit-identical."""
     capi = gpu
     w = bench.WORKLOADS["hybrid-1m"]
