@@ -24,8 +24,11 @@
 // (each row value is split once per workgroup, not once per query group), the wavefronts meet at
 // an LDS-only barrier (the register loads of the next tile stay in flight), and every wavefront
 // reads its A fragments from the planes. The query parts take 144 of a wavefront's 256
-// registers at d = 384, so one tile (48 KB per workgroup) is all the registers hold in flight;
-// that, not the matrix core, sets the rate (about 2.9 us per tile, against 1.3 us of MFMA). Plane row r keeps its 16-byte chunk s (8 dims) at chunk
+// registers at d = 384, so one tile (48 KB per workgroup) is all the registers hold in flight. A
+// tile takes about 2.9 us against 1.3 us of MFMA work; its LDS traffic (288 KB of A fragments
+// read and 72 KB of planes written per 48 KB tile) is of the same order as the matrix core's
+// time, and a form with two tiles in flight (pairs of wavefronts splitting the dimensions,
+// single-buffered planes) was slower. Plane row r keeps its 16-byte chunk s (8 dims) at chunk
 // s ^ (r & 15) (rows are whole multiples of 256 bytes), so the 16 rows one ds_read_b128 quarter-
 // wave reads hit 16 distinct bank groups.
 //
