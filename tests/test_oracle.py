@@ -266,17 +266,48 @@ def test_bm25_accumulates_in_term_order():
     assert got[2] == np.float32(np.float32(np.float32(0.7) + np.float32(0.2)) + np.float32(0.4))
 
 
-def test_fuse_formula():
-    dense = RNG.uniform(-1, 1, 1000).astype(np.float32)
-    lexical = RNG.uniform(0, 7, 1000).astype(np.float32)
+def test_fuse_special_cases_and_bounds():
+    """zo_fuse (src/cuda/lexical.cu:67-74: w * dense + (1 - w) * lex * inv, inv = 1 / max when
+    max > 0, else 0) pinned by what the formula forces rather than by restating it:
+    w = 1 leaves the dense scores; w = 0 leaves lex * fl(1 / max), so the top lexical document
+    scores within an ulp of 1; max = 0 drops the lexical term; for any w in [0, 1] the result
+    is a convex combination of dense and lex / max (within rounding) and rises with lex."""
+    n = 4000
+    dense = RNG.uniform(-1, 1, n).astype(np.float32)
+    lexical = RNG.uniform(0, 7, n).astype(np.float32)
+    lexical[17] = np.float32(0.0)
     peak = oracle.max_positive(lexical)
     assert peak == lexical.max()
-    got = oracle.fuse(dense, lexical, peak, 0.6)
-    w = np.float32(0.6)
+    top = int(np.argmax(lexical))
     inverse = np.float32(1.0) / np.float32(peak)
-    expected = (w * dense + ((np.float32(1.0) - w) * lexical) * inverse).astype(np.float32)
-    assert np.array_equal(got, expected)
-    assert np.array_equal(oracle.fuse(dense, lexical, 0.0, 0.6), (w * dense).astype(np.float32))
+    # w = 1: the dense score itself (zero lexical weight)
+    assert np.array_equal(oracle.fuse(dense, lexical, peak, 1.0), dense)
+    # w = 0: the normalized lexical score, one rounding of lex * inverse
+    only_lexical = oracle.fuse(dense, lexical, peak, 0.0)
+    assert np.array_equal(only_lexical, (lexical * inverse).astype(np.float32))
+    assert abs(float(only_lexical[top]) - 1.0) <= float(np.spacing(np.float32(1.0)))
+    assert only_lexical[17] == 0.0 and float(only_lexical.min()) >= 0.0
+    # max = 0 (no positive lexical score): the lexical term vanishes
+    for w in (0.0, 0.25, 0.6):
+        assert np.array_equal(oracle.fuse(dense, lexical, 0.0, w), (np.float32(w) * dense).astype(np.float32))
+    # convexity: between dense and lex / max, within a few roundings of the operands' size
+    normalized_lex = lexical.astype(np.float64) / float(peak)
+    for w in RNG.uniform(0, 1, 12):
+        got = oracle.fuse(dense, lexical, peak, float(w)).astype(np.float64)
+        lo = np.minimum(dense, normalized_lex)
+        hi = np.maximum(dense, normalized_lex)
+        slack = 4 * np.spacing(np.maximum(np.abs(lo), np.abs(hi)).astype(np.float32)).astype(np.float64)
+        assert np.all(got >= lo - slack) and np.all(got <= hi + slack)
+        # monotone in lex at fixed dense: sort by lex with one dense value
+        same = np.full(n, dense[0], dtype=np.float32)
+        order = np.argsort(lexical, kind="stable")
+        ranked = oracle.fuse(same, lexical[order], peak, float(w))
+        assert np.all(np.diff(ranked.astype(np.float64)) >= 0)
+    # the weight is the dense share: w = 0.75 leans three to one towards dense
+    w = 0.75
+    mixed = oracle.fuse(dense, lexical, peak, w).astype(np.float64)
+    expected = w * dense.astype(np.float64) + (1 - w) * normalized_lex
+    assert np.all(np.abs(mixed - expected) <= 1e-6)
 
 
 def test_rescore_and_remap():
