@@ -49,6 +49,9 @@ WORKLOADS = {
     "int8-10m-sorted": dict(kind="i8i8", n=10_000_000, dim=768, batch=256, k=100, sort_rows=True,
                             name="per-vector int8 10M x 768 with rows sorted by their first coordinate, "
                                  "batch 256, k=100"),
+    "int8-10m-hot": dict(kind="i8i8", n=10_000_000, dim=768, batch=256, k=100, hot_queries=16, hot_blocks=4,
+                         name="per-vector int8 10M x 768 with 256 near-copies of each of 16 queries crowded "
+                              "into one workgroup's blocks, batch 256, k=100"),
     "f32-1m-b1": dict(kind="f32", n=1_000_000, dim=384, batch=1, k=10,
                       name="float32 1M x 384, batch 1, k=10"),
     "f16-1m-b1": dict(kind="f16", n=1_000_000, dim=384, batch=1, k=10,
@@ -69,6 +72,7 @@ WORKLOADS = {
 }
 LEXICAL_SEED = 7
 TERMS_SEED = 11
+HOT_SEED = 13
 
 
 def log(*args):
@@ -124,6 +128,30 @@ def build_inputs(capi, w):
     queries = capi.DeviceArray((batch, dim), np.float32)
     capi.generate_normalized(queries, batch, dim, QUERY_SEED, 0)
     capi.synchronize()
+    if w.get("hot_queries"):
+        # A corpus whose best rows crowd together: for each of the first hot_queries queries,
+        # hot_blocks 64-row blocks of near-copies of it (the query plus 2% noise per dimension, normalized),
+        # placed at blocks 1 + cu * m, so one workgroup of a scan with one workgroup per CU visits
+        # them all (and the sketch's every-32nd-block sample none): those queries' candidates
+        # overflow that workgroup's buffers and take the exact fallback.
+        cus = capi.device_info(0).compute_units
+        host_q = queries.to_host()
+        rng = np.random.default_rng(HOT_SEED)
+        hot = capi.DeviceArray((64, dim), np.float32)
+        block = 0
+        for b in range(w["hot_queries"]):
+            for _ in range(w["hot_blocks"]):
+                rows = host_q[b] + np.float32(0.02) * rng.standard_normal((64, dim)).astype(np.float32)
+                rows /= np.linalg.norm(rows, axis=1, keepdims=True)
+                rows = np.ascontiguousarray(rows, dtype=np.float32)
+                capi.call("zcgvs_memcpy_h2d", hot.ptr, rows.ctypes.data, rows.nbytes, None)
+                first = (1 + cus * block) * 64
+                capi.launch_quantize_rows_i8(hot, 64, dim, corpus.ptr + first * dim,
+                                             keep["scales"].ptr + first * 4)
+                capi.synchronize()
+                block += 1
+        hot.free()
+        keep["hot_rows"] = [(1 + cus * m) * 64 for m in range(block)]
     dtype = {"i8i8": capi.I8, "f32": capi.F32, "f16": capi.F16, "hybrid": capi.F16, "binary": capi.BINARY}[kind]
     store = capi.store_desc(corpus, n, dim, dtype, 1.0, keep.get("scales"))
     extra = {}
@@ -180,7 +208,7 @@ def measured_traffic(workload, kernel):
 
 def scan_kernel_name(w):
     if w["kind"] == "i8i8" and w["batch"] >= 8:
-        return f"mfmaScanKernel<{w['dim'] // 32}, false>"
+        return f"mfmaScanKernel<{w['dim'] // 32}, 0>"
     if w["kind"] == "f32" and w["batch"] >= 32 and w["dim"] in (256, 384):
         return f"mfmaSplitScanKernel<{w['dim']}, false>"
     if w["kind"] in ("f32", "f16", "hybrid") and w["batch"] >= 4 and w["dim"] in (128, 256, 384, 512):
@@ -461,7 +489,9 @@ def main(argv=None) -> int:
               flags.nbytes, None)
     capi.synchronize()
     if flags.any():
-        log(f"ERROR: {int(flags.sum())} queries report an incomplete result")
+        # information, not an error: flagged queries took the exact fallback inside the step (the
+        # parity check below still compares the sampled results with the oracle)
+        log(f"{int(flags.sum())} queries took the exact fallback")
     gpu_idx, gpu_val = out_idx.to_host(), out_val.to_host()
 
     batch = w["batch"]
@@ -524,7 +554,7 @@ def main(argv=None) -> int:
         if parity is not None:
             result["parity"] = parity
     print(json.dumps(result), flush=True)
-    return 3 if flags.any() else 0
+    return 0
 
 
 if __name__ == "__main__":

@@ -286,14 +286,19 @@ typedef struct zcgvs_search_desc {
  * ZCGVS_SEARCH_SORTED_POSTINGS is an invalid argument.
  * ZCGVS_SEARCH_FORCE_EXACT_PASS runs the exact device fallback (see zcgvs_search_topk) for every
  * query instead of only the ones whose candidate buffers overflowed; for tests and verification.
- * ZCGVS_SEARCH_TEST_TINY_SEGMENTS gives every candidate segment two slots, so that almost every
- * query overflows and takes the fallback through its overflow flag; for tests only. */
+ * ZCGVS_SEARCH_TEST_TINY_SEGMENTS gives every candidate segment of the first attempt two slots, so
+ * that almost every query overflows and takes the fallback through its overflow flag; for tests
+ * only.
+ * ZCGVS_SEARCH_TEST_HIGH_THRESHOLD sets the speculative threshold of a sketch-planned search (see
+ * zcgvs_search_topk) to the best sampled score, so that most queries find fewer than k candidates
+ * and take the fallback; for tests only (no effect on other plans). */
 enum zcgvs_search_flags {
     ZCGVS_SEARCH_MATERIALIZE = 1,
     ZCGVS_SEARCH_UNSORTED_POSTINGS = 2,
     ZCGVS_SEARCH_SORTED_POSTINGS = 4,
     ZCGVS_SEARCH_FORCE_EXACT_PASS = 8,
-    ZCGVS_SEARCH_TEST_TINY_SEGMENTS = 16
+    ZCGVS_SEARCH_TEST_TINY_SEGMENTS = 16,
+    ZCGVS_SEARCH_TEST_HIGH_THRESHOLD = 32
 };
 
 /* Bytes of device workspace zcgvs_search_topk needs for this descriptor (0 on error). */
@@ -302,13 +307,22 @@ size_t zcgvs_search_workspace_bytes(const zcgvs_search_desc* desc);
 /* Runs the fused pipeline. d_out_indices/d_out_values are [batch, k]. The workspace must be
  * zcgvs_search_workspace_bytes(desc) bytes; its contents need no initialization. Capture safe.
  * The result is the exact top-k for every input: the scan keeps only candidates above a sampled
- * threshold in bounded per-workgroup buffers, and a query whose buffers overflowed (a corpus whose
- * best rows crowd into a few blocks) is recomputed on the device, in the same call and stream,
- * by an exact fallback that selects over recomputed scores (one workgroup per such query, a few
- * corpus reads). zcgvs_search_overflow_flags tells which queries took that path. A search of at
- * most four queries selecting at most 32 keys each (k, or rescore_candidates with a rescore store)
- * that no matrix-core scan takes reads the corpus in a single pass whose per-workgroup lists are
- * exact; it never overflows. */
+ * threshold in bounded per-workgroup buffers. A per-vector int8 search on the matrix cores over a
+ * large corpus is sketch-planned: a first launch over every 32nd block records per row half of
+ * each workgroup the best score of each query, and one scan of the whole corpus keeps the keys
+ * at or above the j-th best of those scores (a threshold that is likely, not certain, to lie
+ * below the k-th best key); other searches run threshold phases whose thresholds are certain
+ * lower bounds. The search's last merge flags a query whose buffers overflowed (a corpus whose
+ * best rows crowd into a few blocks) or which found fewer than k keys above a speculative
+ * threshold; flagged queries are completed on the device, in the same call and stream, by the
+ * exact fallback: the int8 matrix-core scan runs once more over the whole corpus for just those
+ * queries with a threshold that is a certain lower bound and the batch's candidate buffers
+ * shared among them, and the selection is taken from that; for other scans, or when that rerun
+ * overflows too, one workgroup per query selects over recomputed scores (a few corpus reads).
+ * zcgvs_search_overflow_flags tells which queries took the fallback. A search of at most four
+ * queries selecting at most 1024 keys each (k, or rescore_candidates with a rescore store) that
+ * no matrix-core scan takes reads the corpus in a single pass whose per-workgroup lists are exact
+ * (selections above 32 keys merge groups of workgroups first); it never overflows. */
 int zcgvs_search_topk(const zcgvs_search_desc* desc, void* d_workspace, size_t workspace_bytes,
                       int* d_out_indices, float* d_out_values, zcgvs_stream_t stream);
 

@@ -141,8 +141,24 @@ def test_descriptors_keep_their_buffers_alive(capi):
     assert all(r() is None for r in refs)
 
 
+@pytest.mark.parametrize("n,batch,k,stride", [
+    (10_000_000, 256, 100, 32),     # the per-vector int8 10M x 768 configuration
+    (1_000_000, 256, 100, 8),       # a smaller corpus samples every 8th block (>= 4 per workgroup)
+    (1_000_003, 64, 100, 8),        # ragged tail block
+])
+def test_sketch_plan_samples_then_scans_everything(capi, n, batch, k, stride):
+    # A sketch-planned search (per-vector int8 on the matrix cores, large corpus): a sketch
+    # phase over every stride-th 64-row block, then one threshold scan of the whole corpus.
+    kw = dict(n=n, dim=768, dtype=2, batch=batch, k=k, int8_mode=1, row_scales=1 << 24)
+    rows = capi.search_phase_rows(_desc(capi, **kw))
+    blocks = (n + 63) // 64
+    sampled = (blocks + stride - 1) // stride
+    last_sampled = (blocks - 1) % stride == 0
+    assert rows == [sampled * 64 - ((blocks * 64 - n) if last_sampled else 0), n]
+
+
 @pytest.mark.parametrize("n,dtype,int8_mode,batch,k", [
-    (10_000_000, 2, 1, 256, 100),   # per-vector int8 MFMA path
+    (100_000, 2, 1, 256, 100),      # per-vector int8 MFMA path below the sketch plan's size
     (1_000_000, 0, 0, 64, 10),      # float32 VALU path
     (123_457, 1, 0, 5, 40),         # ragged tail block
 ])
@@ -185,3 +201,59 @@ def test_trace_ranges_compile_in_and_out(tmp_path, with_roctx):
     result = subprocess.run(["g++", "-std=c++17", "-fsyntax-only", f"-I{ROOT / 'include'}", *flags, str(source)],
                             capture_output=True, text=True)
     assert result.returncode == 0, result.stderr
+
+
+def test_name_helpers_follow_the_reference(tmp_path):
+    # metricFromName / scalarTypeFromName keep the reference's aliases and defaults
+    # (include/zcgvs/core/metric.hpp:26-34, scalar_type.hpp:56-67: unknown names fall back to
+    # cosine / float32); the *Strict variants reject unknown names instead.
+    import shutil
+    import subprocess
+    if shutil.which("g++") is None:
+        pytest.skip("no host C++ compiler")
+    source = tmp_path / "names.cpp"
+    source.write_text(r"""
+#include <cstdio>
+#include <stdexcept>
+#include "zcgvs/core/metric.hpp"
+#include "zcgvs/core/scalar_type.hpp"
+using namespace zcgvs;
+static int failures = 0;
+#define CHECK(x) do { if (!(x)) { std::printf("failed: %s\n", #x); ++failures; } } while (0)
+template <typename F> static bool throws(F f) { try { f(); } catch (const std::invalid_argument&) { return true; } return false; }
+int main() {
+    CHECK(metricFromName("dot") == Metric::DotProduct);
+    CHECK(metricFromName("dotproduct") == Metric::DotProduct);
+    CHECK(metricFromName("ip") == Metric::DotProduct);
+    CHECK(metricFromName("l2") == Metric::L2);
+    CHECK(metricFromName("euclidean") == Metric::L2);
+    CHECK(metricFromName("cosine") == Metric::Cosine);
+    CHECK(metricFromName("dot_product") == Metric::Cosine);
+    CHECK(metricFromName("") == Metric::Cosine);
+    CHECK(metricFromNameStrict("ip") == Metric::DotProduct);
+    CHECK(metricFromNameStrict("cosine") == Metric::Cosine);
+    CHECK(throws([] { metricFromNameStrict("cosin"); }));
+    CHECK(scalarTypeFromName("float16") == ScalarType::Float16);
+    CHECK(scalarTypeFromName("fp16") == ScalarType::Float16);
+    CHECK(scalarTypeFromName("half") == ScalarType::Float16);
+    CHECK(scalarTypeFromName("int8") == ScalarType::Int8);
+    CHECK(scalarTypeFromName("i8") == ScalarType::Int8);
+    CHECK(scalarTypeFromName("binary") == ScalarType::Binary);
+    CHECK(scalarTypeFromName("bin") == ScalarType::Binary);
+    CHECK(scalarTypeFromName("b1") == ScalarType::Binary);
+    CHECK(scalarTypeFromName("float32") == ScalarType::Float32);
+    CHECK(scalarTypeFromName("whatever") == ScalarType::Float32);
+    CHECK(scalarTypeFromNameStrict("f32") == ScalarType::Float32);
+    CHECK(scalarTypeFromNameStrict("b1") == ScalarType::Binary);
+    CHECK(throws([] { scalarTypeFromNameStrict("int4"); }));
+    CHECK(std::string(metricName(metricFromName("ip"))) == "dot");
+    CHECK(std::string(scalarName(scalarTypeFromName("half"))) == "float16");
+    return failures == 0 ? 0 : 1;
+}
+""")
+    exe = tmp_path / "names"
+    built = subprocess.run(["g++", "-std=c++17", f"-I{ROOT / 'include'}", str(source), "-o", str(exe)],
+                           capture_output=True, text=True)
+    assert built.returncode == 0, built.stderr
+    ran = subprocess.run([str(exe)], capture_output=True, text=True)
+    assert ran.returncode == 0, ran.stdout

@@ -83,6 +83,34 @@ def test_ten_million_sorted_rows_are_exact(gpu):
     assert_topk_equivalent(idx[sample], val[sample], ref, w["k"])
 
 
+def test_ten_million_crowded_rows_take_the_fallback(gpu):
+    """Near-copies of 16 queries crowded into the blocks of one workgroup (bench workload
+    int8-10m-hot): those queries' candidates overflow that workgroup's buffers, the merge flags
+    them, and the whole-GPU rerun completes them; every result is exact."""
+    w = bench.WORKLOADS["int8-10m-hot"]
+    desc, corpus, queries, keep = bench.build_inputs(gpu, w)
+    idx, val, flags = gpu.search(desc)
+    flagged = set(np.flatnonzero(flags).tolist())
+    print(f"queries through the exact fallback: {len(flagged)} of {w['batch']}", flush=True)
+    assert set(range(w["hot_queries"])) <= flagged, "the crowded queries should take the fallback"
+    _ranked(idx, val, w["n"])
+    codes = corpus.to_host()
+    scales = keep["scales"].to_host()
+    qcodes, qscales = oracle.quantize_rows_i8(queries.to_host())
+    for b in range(w["batch"]):
+        rows = idx[b]
+        exact = oracle.scores_i8i8(codes[rows], scales[rows], qcodes[b:b + 1], qscales[b:b + 1])[0]
+        assert np.array_equal(val[b], exact), f"query {b}: scores differ from the oracle's"
+    hot = set()
+    for first in keep["hot_rows"]:
+        hot.update(range(first, first + 64))
+    for b in range(w["hot_queries"]):
+        assert set(idx[b].tolist()) <= hot, f"query {b}: its near-copies should be its top-{w['k']}"
+    sample = [0, 7, 15, 16, 255]
+    ref = oracle.scores_i8i8(codes, scales, qcodes[sample], qscales[sample])
+    assert_topk_equivalent(idx[sample], val[sample], ref, w["k"])
+
+
 def test_fifty_million_binary_with_fp16_rescore(gpu):
     capi = gpu
     w = bench.WORKLOADS["binary-50m"]

@@ -1,0 +1,116 @@
+"""The sketch-planned search against the oracle.
+
+A per-vector int8 search on the matrix cores over a large corpus runs a sketch launch (every
+stride-th 64-row block; per row half of a workgroup, the best score of each query), takes the
+j-th best of those scores as a speculative threshold, scans the whole corpus once keeping the keys
+at or above it, and flags a query whose candidate buffers overflowed or which found fewer than k
+keys. Flagged queries are scanned again over the whole corpus by the matrix-core scan with a
+threshold that is a certain lower bound (the rerun), and their selection comes from that. Every
+path must give the oracle's top-k bit for bit: the speculative path itself, the fallback when the
+threshold was too high (ZCGVS_SEARCH_TEST_HIGH_THRESHOLD), the rerun after overflowing candidate
+buffers (ZCGVS_SEARCH_TEST_TINY_SEGMENTS), the last resort (ZCGVS_SEARCH_FORCE_EXACT_PASS), with
+an allow-mask, and with more than one launch of 256 queries."""
+
+from __future__ import annotations
+
+import numpy as np
+import pytest
+
+import oracle
+from helpers import assert_topk_equivalent, normalized
+
+pytestmark = pytest.mark.gpu
+
+N, DIM, BATCH, K = 1_000_000, 256, 256, 100
+
+
+@pytest.fixture(scope="module")
+def corpus(gpu):
+    capi = gpu
+    codes, scales = oracle.quantize_rows_i8(normalized(N, DIM, 91))
+    queries = normalized(300, DIM, 92)
+    return dict(codes=codes, scales=scales, queries=queries,
+                d_codes=capi.DeviceArray.from_host(codes), d_scales=capi.DeviceArray.from_host(scales),
+                d_queries=capi.DeviceArray.from_host(queries[:BATCH]),
+                d_queries_300=capi.DeviceArray.from_host(queries))
+
+
+def _desc(capi, c, batch=BATCH, k=K, flags=0, mask=None):
+    store = capi.store_desc(c["d_codes"], N, DIM, capi.I8, 1.0, c["d_scales"])
+    queries = c["d_queries"] if batch == BATCH else c["d_queries_300"]
+    return capi.search_desc(store, queries, batch, k, capi.COSINE, int8_mode=capi.INT8_PER_VECTOR,
+                            mask=mask, flags=flags)
+
+
+def _exact_scores(c, idx, val, batch, mask=None):
+    # every query: each returned score is the oracle's score of that id, bit for bit
+    qcodes, qscales = oracle.quantize_rows_i8(c["queries"][:batch])
+    for b in range(batch):
+        rows = idx[b]
+        assert len(set(rows.tolist())) == rows.size, f"query {b}: repeated id"
+        exact = oracle.scores_i8i8(c["codes"][rows], c["scales"][rows], qcodes[b:b + 1], qscales[b:b + 1],
+                                   None if mask is None else mask[rows])[0]
+        assert np.array_equal(val[b], exact), f"query {b}: scores differ from the oracle's"
+
+
+def _sampled(c, idx, val, sample, k, mask=None):
+    qcodes, qscales = oracle.quantize_rows_i8(c["queries"][sample])
+    ref = oracle.scores_i8i8(c["codes"], c["scales"], qcodes, qscales, mask)
+    assert_topk_equivalent(idx[sample], val[sample], ref, k)
+
+
+@pytest.fixture(scope="module")
+def baseline(gpu, corpus):
+    capi = gpu
+    desc = _desc(capi, corpus)
+    rows = capi.search_phase_rows(desc)
+    assert len(rows) == 2 and rows[1] == N, f"not sketch-planned: {rows}"
+    idx, val, flags = capi.search(desc)
+    return idx, val, flags
+
+
+def test_speculative_scan_is_exact(corpus, baseline):
+    idx, val, flags = baseline
+    assert not flags.any(), "a random corpus should not need the fallback"
+    _exact_scores(corpus, idx, val, BATCH)
+    _sampled(corpus, idx, val, [0, 1, 97, 128, 200, 255], K)
+
+
+@pytest.mark.parametrize("flag", ["high", "tiny", "force"])
+def test_fallback_paths_match(gpu, corpus, baseline, flag):
+    capi = gpu
+    bits = {"high": capi.SEARCH_TEST_HIGH_THRESHOLD, "tiny": capi.SEARCH_TEST_TINY_SEGMENTS,
+            "force": capi.SEARCH_FORCE_EXACT_PASS}[flag]
+    idx, val, flags = capi.search(_desc(capi, corpus, flags=bits))
+    if flag != "force":
+        assert int(np.count_nonzero(flags)) > BATCH // 2, f"{flag}: expected most queries flagged"
+    ref_idx, ref_val, _ = baseline
+    assert np.array_equal(idx, ref_idx), f"{flag}: ids differ from the speculative path's"
+    assert np.array_equal(val, ref_val), f"{flag}: scores differ from the speculative path's"
+
+
+def test_masked_rerun(gpu, corpus):
+    capi = gpu
+    mask = (np.random.default_rng(93).random(N) > 0.25).astype(np.uint8)
+    d_mask = capi.DeviceArray.from_host(mask)
+    results = []
+    for bits in (0, capi.SEARCH_TEST_TINY_SEGMENTS, capi.SEARCH_TEST_HIGH_THRESHOLD):
+        idx, val, flags = capi.search(_desc(capi, corpus, flags=bits, mask=d_mask))
+        assert not mask[idx.ravel()].size or mask[idx.ravel()].all(), "a masked row was returned"
+        results.append((idx, val))
+    for idx, val in results[1:]:
+        assert np.array_equal(idx, results[0][0]) and np.array_equal(val, results[0][1])
+    _exact_scores(corpus, results[0][0], results[0][1], BATCH, mask)
+    _sampled(corpus, results[0][0], results[0][1], [3, 150], K, mask)
+
+
+def test_two_launches_of_queries(gpu, corpus):
+    # 300 queries: two launches per scan; with tiny segments all of them are flagged, so the
+    # rerun's list spans both launches (entries 256..299 in the second)
+    capi = gpu
+    batch, k = 300, 50
+    plain = capi.search(_desc(capi, corpus, batch=batch, k=k))
+    tiny = capi.search(_desc(capi, corpus, batch=batch, k=k, flags=capi.SEARCH_TEST_TINY_SEGMENTS))
+    assert int(np.count_nonzero(tiny[2])) > batch // 2
+    assert np.array_equal(plain[0], tiny[0]) and np.array_equal(plain[1], tiny[1])
+    _sampled(corpus, plain[0], plain[1], [0, 255, 256, 299], k)

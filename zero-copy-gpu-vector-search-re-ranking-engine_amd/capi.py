@@ -25,6 +25,7 @@ SEARCH_UNSORTED_POSTINGS = 2
 SEARCH_SORTED_POSTINGS = 4
 SEARCH_FORCE_EXACT_PASS = 8
 SEARCH_TEST_TINY_SEGMENTS = 16
+SEARCH_TEST_HIGH_THRESHOLD = 32
 
 _vp = ctypes.c_void_p
 _i32 = ctypes.c_int

@@ -25,6 +25,9 @@ struct PhaseArgs {
     long long skip = 0;
     long long items = 0;
     int dense = 0;
+    // A sketch phase (int8 MFMA scan only) emits no keys: each of its 2 * workgroups slots keeps
+    // the best exact score of its rows per query, written to EmitArgs::sketch.
+    int sketch = 0;
     int block_rows = 64;
 };
 
@@ -35,7 +38,24 @@ struct EmitArgs {
     std::uint64_t* seg = nullptr;        // [n_wg, batch, 1 << seg_log2]
     std::uint32_t* seg_count = nullptr;  // [n_wg, batch]
     int seg_log2 = 0;
+    float* sketch = nullptr;             // sketch phases: [slots, batch] best score per slot
+    // Rerun of the exact fallback (int8 MFMA scan): only the F = *q_list_count queries
+    // q_list[0..F) are scanned. List entry e of query q = q_list[e] owns the segments
+    // seg[(s * F + e) << rerunSegLog2(seg_log2, batch, F)] with counts seg_count[s * F + e], so
+    // the F queries share the whole segment buffer of the batch.
+    const std::uint32_t* q_list = nullptr;
+    const std::uint32_t* q_list_count = nullptr;
 };
+
+// Slots per (segment, list entry) of a rerun over F of the batch's queries: the batch's capacity
+// 2^seg_log2 times the largest power of two <= batch / F (at most 2^23 slots).
+__host__ __device__ inline int rerunSegLog2(int seg_log2, int batch, int listed) {
+    int shift = 0;
+    while (listed > 0 && (static_cast<long long>(listed) << (shift + 1)) <= batch) {
+        ++shift;
+    }
+    return seg_log2 + shift < 23 ? seg_log2 + shift : 23;
+}
 
 // First block of work item j of a phase: the j-th multiple of `stride` that is not a multiple
 // of stride * skip. Item counts and skips stay below 2^31, so the division is 32-bit.
@@ -184,9 +204,10 @@ bool singlePassSupported(const ScanArgs& scan, int width);
 int launchSinglePass(const ScanArgs& scan, const SinglePassArgs& args, hipStream_t stream);
 
 // Exact device fallback (recover.hip): the top-`width` of every query whose flag is set (every
-// query with `force`) over the whole corpus, written sorted to out_keys [batch, width] and, when
-// out_index is set, as (index, score) pairs [batch, width]. The scan arguments are the VALU
-// scan's: original row scales and allow-mask, device-prepared queries, lexical scores.
+// query with `force`; the listed queries in list mode) over the whole corpus, written sorted to
+// out_keys [batch, width] and, when out_index is set, as (index, score) pairs [batch, width].
+// The scan arguments are the VALU scan's: original row scales and allow-mask, device-prepared
+// queries, lexical scores.
 struct RecoverArgs {
     const std::uint32_t* flags = nullptr;
     bool force = false;
@@ -194,6 +215,17 @@ struct RecoverArgs {
     std::uint64_t* out_keys = nullptr;
     int* out_index = nullptr;
     float* out_score = nullptr;
+    // List mode (flag_list set, force clear): block e takes the e-th flagged query
+    // flag_list[e], e < *flag_count. With `seg` set, the rerun (EmitArgs::q_list) wrote entry
+    // e's keys to its segments (n_seg of them, rerunSegLog2(seg_log2, batch, F) slots each);
+    // when none overflowed, the query's selection is taken from them and the corpus is not
+    // read again.
+    const std::uint32_t* flag_list = nullptr;
+    const std::uint32_t* flag_count = nullptr;
+    const std::uint64_t* seg = nullptr;
+    const std::uint32_t* seg_count = nullptr;
+    int n_seg = 0;
+    int seg_log2 = 0;
 };
 bool recoverSupported(const ScanArgs& scan);
 int launchRecover(const ScanArgs& scan, const RecoverArgs& args, hipStream_t stream);

@@ -13,13 +13,17 @@
 // the lagger first filters tile t - 1 and then multiplies tile t. So each wavefront's VALU filter
 // work runs while the other keeps the SIMD's matrix core busy. The two roles run separate loops,
 // so a value one role keeps across the barrier takes no register in the other's multiply. A
-// filter that passes owes an exact pass, which reuses the row scales the filter read (up to
-// d = 768); the lagger runs it right after its filter, the leader right after the next barrier,
-// both before that step's tile copies are issued (its keys go to an LDS staging buffer, so in
-// the loop global stores, which would queue behind the copies in the vmcnt order, happen only
-// when that buffer is full). The leader issues its share of the tile copies after its multiply,
-// the lagger before its own, so neither role's copy issue delays the first MFMAs after the
-// barrier.
+// filter that passes owes an exact pass over the row groups it marked; the lagger runs it right
+// after its filter, the leader right after the next barrier, both before that step's tile copies
+// are issued (its keys go to an LDS staging buffer, so in the loop global stores, which would
+// queue behind the copies in the vmcnt order, happen only when that buffer is full). The leader
+// issues its share of the tile copies after its multiply, the lagger before its own, so neither
+// role's copy issue delays the first MFMAs after the barrier.
+//
+// Modes. A threshold phase emits the keys above each query's threshold; a dense phase writes
+// every key to its fixed slot; a sketch phase emits nothing and records, per slot (a row half of
+// a workgroup's lanes), the best exact score of each query. A rerun (EmitArgs::q_list) scans only
+// the listed queries, with the segment layout the list defines.
 //
 // Candidate staging. A query's candidates in a workgroup come from exactly two lanes (its two
 // row halves), so each lane owns a candidate segment (segment 2 * workgroup + half) and counts
@@ -56,10 +60,10 @@
 // or for the partial last tile, they come from a workspace copy in which masked and padding
 // rows hold NaN; such a row scores -FLT_MAX.
 //
-// Filter of a threshold phase: per lane the largest (float)dot * s_r of the tile is compared with
-// the query's threshold score minus a relative margin of 2^-20 (far above the few-ulp difference
-// between that product order and the exact score's); only when some lane passes is the exact
-// score, its key and the key comparison evaluated.
+// Filter of a threshold phase: per lane and group of four rows the largest (float)dot * s_r is
+// compared with the query's threshold score minus a relative margin of 2^-20 (far above the
+// few-ulp difference between that product order and the exact score's); only for the groups in
+// which some lane passes are the exact scores, their keys and the key comparisons evaluated.
 #include <hip/hip_runtime.h>
 
 #include <algorithm>
@@ -85,9 +89,17 @@ constexpr std::size_t kRingBudget = 150 * 1024;
 constexpr int kStaged = 64;  // candidates parked per wavefront before they reach the segments
 constexpr int kMinBatch = 8;
 
-template <int kKSteps, bool kDense>
+// kMode: kThreshold (emit keys above the threshold), kDense (every key to its fixed slot) or
+// kSketch (per slot the best exact score, no keys).
+constexpr int kThreshold = 0;
+constexpr int kDenseMode = 1;
+constexpr int kSketchMode = 2;
+
+template <int kKSteps, int kMode>
 __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(2, 2)))
 void mfmaScanKernel(ScanArgs scan, PhaseArgs phase, EmitArgs emit, int q_offset, int q_count) {
+    constexpr bool kDense = kMode == kDenseMode;
+    constexpr bool kSketch = kMode == kSketchMode;
     constexpr int kDim = kKSteps * 32;
     constexpr int kSlotsPerRow = kDim / 16;
     constexpr int kTileBytes = kRows * kDim;
@@ -106,9 +118,24 @@ void mfmaScanKernel(ScanArgs scan, PhaseArgs phase, EmitArgs emit, int q_offset,
     __shared__ __attribute__((aligned(16))) std::uint8_t ring[kDepth][kTileBytes];
     __shared__ __attribute__((aligned(16))) float scale_ring[kScaleDepth][kRows];
     __shared__ std::uint32_t lds_simd[4];
-    __shared__ std::uint64_t stage_key[kDense ? 1 : kWaves][kStaged];
+    __shared__ std::uint64_t stage_key[kMode == kThreshold ? kWaves : 1][kStaged];
     // (segment slot << 9) | (half << 8) | local query
-    __shared__ std::uint32_t stage_slot[kDense ? 1 : kWaves][kStaged];
+    __shared__ std::uint32_t stage_slot[kMode == kThreshold ? kWaves : 1][kStaged];
+
+    // A rerun scans list entries [q_offset, q_offset + 256) of q_list; F = *q_list_count entries
+    // exist, so a launch past them has nothing to do (uniform over the workgroup).
+    const bool listed = emit.q_list != nullptr;
+    int seg_batch = scan.batch;     // query rows of the segment layout
+    int seg_log2 = emit.seg_log2;   // slots per segment row
+    if (listed) {
+        const int entries = static_cast<int>(__builtin_amdgcn_readfirstlane(*emit.q_list_count));
+        if (entries <= q_offset) {
+            return;
+        }
+        q_count = min(q_count, entries - q_offset);
+        seg_batch = entries;
+        seg_log2 = rerunSegLog2(emit.seg_log2, scan.batch, entries);
+    }
 
     const int tid = threadIdx.x;
     const int lane = tid & (kWave - 1);
@@ -124,7 +151,9 @@ void mfmaScanKernel(ScanArgs scan, PhaseArgs phase, EmitArgs emit, int q_offset,
     const int qlocal = wave * 32 + col;
     const bool q_valid = qlocal < q_count;
     const bool wave_active = wave * 32 < q_count;
-    const int q = q_offset + min(qlocal, q_count - 1);
+    // entry: the lane's row of the segment layout; q: its query
+    const int entry = q_offset + min(qlocal, q_count - 1);
+    const int q = listed ? static_cast<int>(emit.q_list[entry]) : entry;
     v4i qf[kKSteps];
     {
         const std::int8_t* qrow = queries + static_cast<std::size_t>(q) * kDim + 16 * half;
@@ -137,7 +166,7 @@ void mfmaScanKernel(ScanArgs scan, PhaseArgs phase, EmitArgs emit, int q_offset,
     const float qscale = scan.query_scales[q];
     std::uint64_t tau = 0ull;
     float tau_floor = -INFINITY;
-    if constexpr (!kDense) {
+    if constexpr (kMode == kThreshold) {
         tau = emit.tau[q];
         if (tau != 0ull) {
             const float t = keyScore(tau);
@@ -239,9 +268,6 @@ void mfmaScanKernel(ScanArgs scan, PhaseArgs phase, EmitArgs emit, int q_offset,
     // (reads, then per k-step two MFMAs and the reads kAhead steps further on) so an MFMA never
     // waits on an LDS read issued just before it.
     constexpr int kAhead = kKSteps < 3 ? kKSteps : 3;
-    // The exact pass reuses the row scales the filter read (no second LDS round trip) up to
-    // d = 768; at d = 1024 the 32 registers they take would not fit beside the query operands.
-    constexpr bool kCacheScales = kKSteps <= 24;
     auto multiply = [&](const std::uint8_t* tile, v16i& acc0, v16i& acc1) {
         const std::uint8_t* lane_tile[kPeriod];
 #pragma unroll
@@ -334,68 +360,71 @@ void mfmaScanKernel(ScanArgs scan, PhaseArgs phase, EmitArgs emit, int q_offset,
             relaxed_floor = t - fabsf(t) * kFilterMargin - 1e-30f;
         }
         const bool examine_all = __any(q_valid && kMaskedScore >= tau_floor);
-        // Filter: the wave-uniform set of value slots (slot = 16 * block + result index) in which
-        // some lane's relaxed score (float)dot * s_r reaches the lane's relaxed threshold
-        // (tau_floor / s_q, lowered by 2^-20 relative: far more than the few-ulp gap between
-        // this product order and the exact score's, so every exact candidate's slot is set).
-        // A masked or padding row (NaN scale) never passes here; such rows can qualify only
-        // against a -FLT_MAX threshold, and then every slot is examined.
-        auto filter = [&](const v16i& acc0, const v16i& acc1, const float* scales, float4 (&gs)[8]) -> std::uint32_t {
+        float sketch_best = -INFINITY;  // sketch phases: the lane's best exact score
+        // Filter: the wave-uniform set of row groups (group g holds the value slots 4g..4g+3 of
+        // a lane: row block g / 4, rows 32 (g / 4) + 8 (g % 4) + 4 half + 0..3, whose scales are
+        // one float4) in which some lane's relaxed score (float)dot * s_r reaches the lane's
+        // relaxed threshold (tau_floor / s_q, lowered by 2^-20 relative: far more than the
+        // few-ulp gap between this product order and the exact score's, so every exact
+        // candidate's group is set). A masked or padding row (NaN scale) never passes here; such
+        // rows can qualify only against a -FLT_MAX threshold, and then every group is examined.
+        auto filter = [&](const v16i& acc0, const v16i& acc1, const float* scales) -> std::uint32_t {
+            float4 gs[8];
 #pragma unroll
             for (int grp = 0; grp < 8; ++grp) {
                 gs[grp] = *reinterpret_cast<const float4*>(scales + (grp / 4) * 32 + 8 * (grp % 4) + 4 * half);
             }
-            if (examine_all) {
-                return 0xFFFFFFFFu;
-            }
-            // Per lane the largest relaxed score of each group of four value slots (one float4 of
-            // row scales); the slot set is needed only when some group reaches the lane's threshold
-            // somewhere in the wavefront, and then only inside the groups that do.
-            float group_best[8];
+            if constexpr (kSketch) {
+                // the sketch: the best exact score of the lane's 32 rows (masked and padding
+                // rows score -FLT_MAX), nothing is emitted
 #pragma unroll
-            for (int mb = 0; mb < 2; ++mb) {
-#pragma unroll
-                for (int g = 0; g < 4; ++g) {
-                    const float4 rs = gs[4 * mb + g];
-                    const float rsv[4] = {rs.x, rs.y, rs.z, rs.w};
-                    float p[4];
+                for (int grp = 0; grp < 8; ++grp) {
+                    const float rsv[4] = {gs[grp].x, gs[grp].y, gs[grp].z, gs[grp].w};
 #pragma unroll
                     for (int j = 0; j < 4; ++j) {
-                        const int dot = mb == 0 ? acc0[4 * g + j] : acc1[4 * g + j];
-                        p[j] = static_cast<float>(dot) * rsv[j];
+                        const int slot = 4 * grp + j;
+                        const int dot = slot < 16 ? acc0[slot] : acc1[slot - 16];
+                        const float combined = qscale * rsv[j];
+                        const float score = rsv[j] == rsv[j] ? static_cast<float>(dot) * combined : kMaskedScore;
+                        sketch_best = fmaxf(sketch_best, score);
                     }
-                    group_best[4 * mb + g] = fmaxf(fmaxf(p[0], p[1]), fmaxf(p[2], p[3]));
                 }
+                return 0u;
+            }
+            if (examine_all) {
+                return 0xFFu;
+            }
+            float group_best[8];
+#pragma unroll
+            for (int grp = 0; grp < 8; ++grp) {
+                const float rsv[4] = {gs[grp].x, gs[grp].y, gs[grp].z, gs[grp].w};
+                float p[4];
+#pragma unroll
+                for (int j = 0; j < 4; ++j) {
+                    const int slot = 4 * grp + j;
+                    const int dot = slot < 16 ? acc0[slot] : acc1[slot - 16];
+                    p[j] = static_cast<float>(dot) * rsv[j];
+                }
+                group_best[grp] = fmaxf(fmaxf(p[0], p[1]), fmaxf(p[2], p[3]));
             }
             const float best = fmaxf(fmaxf(fmaxf(group_best[0], group_best[1]), fmaxf(group_best[2], group_best[3])),
                                      fmaxf(fmaxf(group_best[4], group_best[5]), fmaxf(group_best[6], group_best[7])));
             if (!__any(best >= relaxed_floor)) {
                 return 0u;
             }
-            std::uint32_t passing = 0u;
+            std::uint32_t groups = 0u;
 #pragma unroll
             for (int grp = 0; grp < 8; ++grp) {
-                if (__any(group_best[grp] >= relaxed_floor)) {
-                    // the group's products again (same operations, same values)
-                    const float4 rs = gs[grp];
-                    const float rsv[4] = {rs.x, rs.y, rs.z, rs.w};
-#pragma unroll
-                    for (int j = 0; j < 4; ++j) {
-                        const int slot = 4 * grp + j;
-                        const int dot = slot < 16 ? acc0[slot] : acc1[slot - 16];
-                        const bool pass = static_cast<float>(dot) * rsv[j] >= relaxed_floor;
-                        passing |= (__builtin_amdgcn_ballot_w64(pass) != 0 ? 1u : 0u) << slot;
-                    }
-                }
+                groups |= (__builtin_amdgcn_ballot_w64(group_best[grp] >= relaxed_floor) != 0ull ? 1u : 0u) << grp;
             }
-            return passing;
+            return groups;
         };
-        const std::uint32_t seg_capacity = 1u << emit.seg_log2;
-        // this lane's segment row: segment 2 * workgroup + half, query q
-        const std::size_t seg_row = (static_cast<std::size_t>(2 * blockIdx.x + half) * batch + q) << emit.seg_log2;
+        const std::uint32_t seg_capacity = 1u << seg_log2;
+        // this lane's segment row: segment 2 * workgroup + half, entry `entry`
+        const std::size_t seg_row = (static_cast<std::size_t>(2 * blockIdx.x + half) * seg_batch + entry) << seg_log2;
         std::uint32_t seg_used = 0u;  // this lane's candidates so far (may exceed the capacity)
         std::uint32_t parked = 0u;    // wave-uniform: entries of this wavefront's staging buffer
-        const std::uint32_t tag = (static_cast<std::uint32_t>(half) << 8) | static_cast<std::uint32_t>(q - q_offset);
+        const std::uint32_t tag = (static_cast<std::uint32_t>(half) << 8) | static_cast<std::uint32_t>(entry - q_offset);
         // Appends `key` for the lanes with `take` set (called by the whole wavefront).
         auto stageCandidates = [&](bool take, std::uint64_t key) {
             const std::uint32_t slot = seg_used;
@@ -418,43 +447,41 @@ void mfmaScanKernel(ScanArgs scan, PhaseArgs phase, EmitArgs emit, int q_offset,
                 }
             }
         };
-        // Exact scores and keys of the value slots `passing` marks (slot 4 grp + j: row block
-        // grp / 4, rows 32 (grp / 4) + 8 (grp % 4) + 4 half + j); keys above the threshold are
-        // appended. A group's four row scales come in one LDS read.
-        auto exact = [&](const v16i& acc0, const v16i& acc1, const float4 (&gs)[8], const float* scales,
-                         long long row0, std::uint32_t passing) {
+        // Exact scores and keys of the row groups `groups` marks; keys above the threshold are
+        // appended. One compact loop over the set groups (the group index is wave-uniform, so
+        // its accumulator values are picked by register-relative moves; the pass is rare, and the
+        // loop keeps the kernel at a third of the code that every group and slot spelled out
+        // took, at the same speed). The group's four row scales come in one LDS read from the
+        // scale ring, which still holds them, so no scales stay in registers across the barrier.
+        auto exact = [&](const v16i& acc0, const v16i& acc1, const float* scales, long long row0,
+                         std::uint32_t groups) {
             // Tile-relative rows in 32 bits; the empty asm keeps the compiler from hoisting the
             // per-row constants out of the scan loop into registers.
             int hb = 4 * half;
             asm volatile("" : "+v"(hb));
             const int valid_rows = static_cast<int>(min(static_cast<long long>(kRows), doc_count - row0));
             const std::uint32_t row_base = static_cast<std::uint32_t>(row0);
+            while (groups != 0u) {
+                const int grp = __builtin_ctz(groups);
+                groups &= groups - 1u;
+                const int rl0 = (grp >> 2) * 32 + 8 * (grp & 3) + hb;
+                const float4 rs4 = *reinterpret_cast<const float4*>(scales + rl0);
+                const float rsv[4] = {rs4.x, rs4.y, rs4.z, rs4.w};
 #pragma unroll
-            for (int grp = 0; grp < 8; ++grp) {
-                if ((passing >> (4 * grp)) & 0xFu) {
-                    const int rl0 = (grp / 4) * 32 + 8 * (grp % 4) + hb;
-                    const float4 rs4 = kCacheScales ? gs[grp] : *reinterpret_cast<const float4*>(scales + rl0);
-                    const float rsv[4] = {rs4.x, rs4.y, rs4.z, rs4.w};
-#pragma unroll
-                    for (int j = 0; j < 4; ++j) {
-                        const int slot = 4 * grp + j;
-                        if (passing & (1u << slot)) {
-                            const int rl = rl0 + j;
-                            const float rs = rsv[j];
-                            const int dot = slot < 16 ? acc0[slot] : acc1[slot - 16];
-                            const float combined = qscale * rs;
-                            const float score = rs == rs ? static_cast<float>(dot) * combined : kMaskedScore;
-                            const std::uint64_t key = makeKey(score, row_base + static_cast<std::uint32_t>(rl));
-                            stageCandidates(q_valid && rl < valid_rows && score >= tau_floor && key > tau, key);
-                        }
-                    }
+                for (int j = 0; j < 4; ++j) {
+                    const int slot = 4 * grp + j;
+                    const int dot = slot < 16 ? acc0[slot] : acc1[slot - 16];
+                    const float rs = rsv[j];
+                    const float combined = qscale * rs;
+                    const float score = rs == rs ? static_cast<float>(dot) * combined : kMaskedScore;
+                    const std::uint64_t key = makeKey(score, row_base + static_cast<std::uint32_t>(rl0 + j));
+                    stageCandidates(q_valid && rl0 + j < valid_rows && score >= tau_floor && key > tau, key);
                 }
             }
         };
 
         v16i acc0 = {};
         v16i acc1 = {};
-        float4 gs[8];             // row scales of the tile in (acc0, acc1), as the filter read them
         long long acc_row0 = -1;  // first row of the tile in (acc0, acc1); -1 = none yet
         int acc_sslot = 0;
         if (lead) {
@@ -466,7 +493,7 @@ void mfmaScanKernel(ScanArgs scan, PhaseArgs phase, EmitArgs emit, int q_offset,
             for (; item < phase.items; item += stride_items) {
                 arrive(item);
                 if (owed != 0u) {
-                    exact(acc0, acc1, gs, scale_ring[acc_sslot], acc_row0, owed);
+                    exact(acc0, acc1, scale_ring[acc_sslot], acc_row0, owed);
                 }
                 owed = 0u;
                 if (wave_active) {
@@ -474,7 +501,7 @@ void mfmaScanKernel(ScanArgs scan, PhaseArgs phase, EmitArgs emit, int q_offset,
                     refill(item, slot, sslot);
                     acc_row0 = phaseBlock(item, phase.stride, phase.skip) * kRows;
                     acc_sslot = sslot;
-                    owed = filter(acc0, acc1, scale_ring[sslot], gs);
+                    owed = filter(acc0, acc1, scale_ring[sslot]);
                 } else {
                     refill(item, slot, sslot);
                 }
@@ -482,7 +509,7 @@ void mfmaScanKernel(ScanArgs scan, PhaseArgs phase, EmitArgs emit, int q_offset,
                 sslot = sslot + 1 == kScaleDepth ? 0 : sslot + 1;
             }
             if (owed != 0u) {
-                exact(acc0, acc1, gs, scale_ring[acc_sslot], acc_row0, owed);
+                exact(acc0, acc1, scale_ring[acc_sslot], acc_row0, owed);
             }
         } else {
             // Lagger: filter tile t - 1 and run its exact pass, then refill and multiply tile t.
@@ -491,9 +518,9 @@ void mfmaScanKernel(ScanArgs scan, PhaseArgs phase, EmitArgs emit, int q_offset,
             for (; item < phase.items; item += stride_items) {
                 arrive(item);
                 if (wave_active && acc_row0 >= 0) {
-                    const std::uint32_t owed = filter(acc0, acc1, scale_ring[acc_sslot], gs);
+                    const std::uint32_t owed = filter(acc0, acc1, scale_ring[acc_sslot]);
                     if (owed != 0u) {
-                        exact(acc0, acc1, gs, scale_ring[acc_sslot], acc_row0, owed);
+                        exact(acc0, acc1, scale_ring[acc_sslot], acc_row0, owed);
                     }
                 }
                 refill(item, slot, sslot);
@@ -507,25 +534,31 @@ void mfmaScanKernel(ScanArgs scan, PhaseArgs phase, EmitArgs emit, int q_offset,
             }
             // the last tile
             if (wave_active && acc_row0 >= 0) {
-                const std::uint32_t owed = filter(acc0, acc1, scale_ring[acc_sslot], gs);
+                const std::uint32_t owed = filter(acc0, acc1, scale_ring[acc_sslot]);
                 if (owed != 0u) {
-                    exact(acc0, acc1, gs, scale_ring[acc_sslot], acc_row0, owed);
+                    exact(acc0, acc1, scale_ring[acc_sslot], acc_row0, owed);
                 }
             }
         }
 
+        if constexpr (kSketch) {
+            if (q_valid) {
+                emit.sketch[static_cast<std::size_t>(2 * blockIdx.x + half) * batch + q] = sketch_best;
+            }
+            return;
+        }
         // write the parked candidates of this wavefront, then every lane's count
         {
             const std::uint32_t held = min(parked, static_cast<std::uint32_t>(kStaged));
             for (std::uint32_t i = static_cast<std::uint32_t>(lane); i < held; i += kWave) {
                 const std::uint32_t packed = stage_slot[wave][i];
                 const std::size_t segment = 2 * static_cast<std::size_t>(blockIdx.x) + ((packed >> 8) & 1u);
-                const std::size_t qg = static_cast<std::size_t>(q_offset) + (packed & 0xFFu);
-                emit.seg[((segment * batch + qg) << emit.seg_log2) + (packed >> 9)] = stage_key[wave][i];
+                const std::size_t eg = static_cast<std::size_t>(q_offset) + (packed & 0xFFu);
+                emit.seg[((segment * seg_batch + eg) << seg_log2) + (packed >> 9)] = stage_key[wave][i];
             }
         }
         if (q_valid) {
-            emit.seg_count[static_cast<std::size_t>(2 * blockIdx.x + half) * batch + q] = seg_used;
+            emit.seg_count[static_cast<std::size_t>(2 * blockIdx.x + half) * seg_batch + entry] = seg_used;
         }
     }
 }
@@ -533,14 +566,17 @@ void mfmaScanKernel(ScanArgs scan, PhaseArgs phase, EmitArgs emit, int q_offset,
 template <int kKSteps>
 int launchShape(const ScanArgs& scan, const PhaseArgs& phase, const EmitArgs& emit,
                 int workgroups, hipStream_t stream) {
+    // (a sketch phase fills every workgroup's slots; it gets at least one item per workgroup)
     const long long wanted = phase.dense ? std::min<long long>(phase.items, workgroups) : workgroups;
     const dim3 grid(static_cast<unsigned>(std::max(1LL, wanted)));
     for (int q0 = 0; q0 < scan.batch; q0 += kQueriesPerLaunch) {
         const int count = std::min(kQueriesPerLaunch, scan.batch - q0);
         if (phase.dense) {
-            mfmaScanKernel<kKSteps, true><<<grid, kThreads, 0, stream>>>(scan, phase, emit, q0, count);
+            mfmaScanKernel<kKSteps, kDenseMode><<<grid, kThreads, 0, stream>>>(scan, phase, emit, q0, count);
+        } else if (phase.sketch) {
+            mfmaScanKernel<kKSteps, kSketchMode><<<grid, kThreads, 0, stream>>>(scan, phase, emit, q0, count);
         } else {
-            mfmaScanKernel<kKSteps, false><<<grid, kThreads, 0, stream>>>(scan, phase, emit, q0, count);
+            mfmaScanKernel<kKSteps, kThreshold><<<grid, kThreads, 0, stream>>>(scan, phase, emit, q0, count);
         }
         ZCGVS_LAUNCH_CHECK("mfma scan");
     }

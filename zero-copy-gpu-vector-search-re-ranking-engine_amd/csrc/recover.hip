@@ -1,10 +1,16 @@
 // Exact device fallback of the fused search: the top-`width` of one query over the whole corpus,
-// with no candidate buffer that could overflow, for the queries whose threshold-phase segments
-// overflowed (or for every query, with ZCGVS_SEARCH_FORCE_EXACT_PASS).
+// for the queries the search's last merge flagged (a candidate segment overflowed, or a
+// speculative threshold let fewer than width keys through), or for every query with
+// ZCGVS_SEARCH_FORCE_EXACT_PASS.
 //
-// One 1024-thread workgroup per query, launched for the whole batch after the phased scan; a
-// workgroup whose query did not overflow returns at once, so the launch costs a few microseconds
-// when nothing overflowed. A flagged query's workgroup selects by radix passes over recomputed
+// One 1024-thread workgroup per flagged query, launched for the whole batch after the scan; the
+// workgroups past the flagged list return at once, so the launch costs a few microseconds when
+// nothing was flagged. When the scan kernel supports a rerun (the int8 MFMA scan), the flagged
+// queries were scanned once more over the whole corpus, by every workgroup of the GPU, with a
+// threshold that is a lower bound of their width-th best key and the batch's whole segment
+// buffer shared among them; a flagged query whose rerun segments did not overflow takes its
+// selection from them (radix passes over at most a few thousand keys). Otherwise, the last
+// resort: its workgroup selects by radix passes over recomputed
 // scores: three histogram passes over the ordered 32-bit score (11, 11 and 10 bits) find the
 // score t of the width-th best key and how many keys scoring exactly t it must take; a final pass
 // keeps every key above t and the first of those at t in index order (the lowest-index tie rule
@@ -35,6 +41,113 @@ __host__ __device__ constexpr int stagedWordsPerChunk(int kind) {
     return kind == ZCGVS_DTYPE_F32 ? 4 : kind == ZCGVS_DTYPE_F16 ? 8 : kind == ZCGVS_DTYPE_I8 ? 16 : 4;
 }
 
+// The selection of list entry `entry` (query q) from the rerun's segments, written like the last
+// resort's; false (nothing written) when one of its segments overflowed. Called by the whole
+// block.
+__device__ bool selectFromRerun(const RecoverArgs& args, int q, int entry, int listed, int batch) {
+    __shared__ std::uint32_t lds_hist[kSelectBins];
+    __shared__ std::uint32_t lds_scan[kRecoverThreads / kWave];
+    __shared__ std::uint64_t lds_keys[kMaxK];
+    __shared__ SelectState lds_state;
+    __shared__ std::uint32_t lds_over;
+    __shared__ std::uint32_t lds_total;
+    const int t = threadIdx.x;
+    const int lane = t & (kWave - 1);
+    const int wave = t / kWave;
+    constexpr int kWaves = kRecoverThreads / kWave;
+    const int log2 = rerunSegLog2(args.seg_log2, batch, listed);
+    const std::uint32_t cap = 1u << log2;
+    const int width = args.width;
+    if (t == 0) {
+        lds_over = 0u;
+        lds_total = 0u;
+        lds_state.prefix = 0ull;
+        lds_state.bits = 0u;
+        lds_state.need = static_cast<std::uint32_t>(width);
+        lds_state.done = 0u;
+        lds_state.count = 0u;
+    }
+    __syncthreads();
+    std::uint32_t own = 0u;
+    for (int s = t; s < args.n_seg; s += kRecoverThreads) {
+        const std::uint32_t c = args.seg_count[static_cast<std::size_t>(s) * listed + entry];
+        if (c > cap) {
+            lds_over = 1u;
+        }
+        own += min(c, cap);
+    }
+    if (own != 0u) {
+        atomicAdd(&lds_total, own);
+    }
+    __syncthreads();
+    if (lds_over != 0u) {
+        return false;  // uniform: read after a barrier
+    }
+    const std::uint32_t total = lds_total;
+    // every key of the entry's segments: wavefront w walks segments w, w + 16, ...
+    auto forEachKey = [&](auto&& f) {
+        for (int s = wave; s < args.n_seg; s += kWaves) {
+            const std::uint32_t c = min(args.seg_count[static_cast<std::size_t>(s) * listed + entry], cap);
+            const std::uint64_t* src = args.seg + ((static_cast<std::size_t>(s) * listed + entry) << log2);
+            for (std::uint32_t j = static_cast<std::uint32_t>(lane); j < c; j += kWave) {
+                f(src[j]);
+            }
+        }
+    };
+    if (total <= static_cast<std::uint32_t>(width)) {
+        if (t == 0) {
+            lds_state.done = 1u;
+        }
+    }
+    __syncthreads();
+    for (int pass = 0; pass < kSelectPasses && !lds_state.done; ++pass) {
+        const int digit = selectDigitWidth(pass);
+        for (int i = t; i < (1 << digit); i += kRecoverThreads) {
+            lds_hist[i] = 0u;
+        }
+        __syncthreads();
+        const std::uint32_t bits = lds_state.bits;
+        const std::uint64_t prefix = lds_state.prefix;
+        const int shift = 64 - static_cast<int>(bits) - digit;
+        forEachKey([&](std::uint64_t key) {
+            if (bits == 0u || (key >> (64 - bits)) == prefix) {
+                atomicAdd(&lds_hist[(key >> shift) & ((1u << digit) - 1u)], 1u);
+            }
+        });
+        __syncthreads();
+        selectPickBucket<kRecoverThreads>(lds_hist, digit, &lds_state, lds_scan);
+    }
+    const std::uint64_t cut = total <= static_cast<std::uint32_t>(width) ? 1ull : selectThreshold(lds_state);
+    __syncthreads();
+    forEachKey([&](std::uint64_t key) {
+        if (key >= cut) {
+            const std::uint32_t slot = atomicAdd(&lds_state.count, 1u);
+            if (slot < static_cast<std::uint32_t>(kMaxK)) {
+                lds_keys[slot] = key;
+            }
+        }
+    });
+    __syncthreads();
+    const std::uint32_t taken = min(min(lds_state.count, static_cast<std::uint32_t>(kMaxK)),
+                                    static_cast<std::uint32_t>(width));
+    std::uint64_t* dst = args.out_keys + static_cast<std::size_t>(q) * width;
+    forEachRanked(lds_keys, taken, [&](std::uint32_t rank, std::uint64_t key) {
+        dst[rank] = key;
+        if (args.out_index != nullptr) {
+            const std::size_t o = static_cast<std::size_t>(q) * width + rank;
+            writeHit(key, &args.out_index[o], &args.out_score[o]);
+        }
+    });
+    for (int i = static_cast<int>(taken) + t; i < width; i += kRecoverThreads) {
+        dst[i] = 0ull;
+        if (args.out_index != nullptr) {
+            const std::size_t o = static_cast<std::size_t>(q) * width + i;
+            writeHit(0ull, &args.out_index[o], &args.out_score[o]);
+        }
+    }
+    return true;
+}
+
 template <int kKind, int L>
 __global__ __launch_bounds__(kRecoverThreads) void recoverKernel(ScanArgs scan, RecoverArgs args,
                                                                  int chunks) {
@@ -45,14 +158,28 @@ __global__ __launch_bounds__(kRecoverThreads) void recoverKernel(ScanArgs scan, 
     __shared__ SelectState lds_state;
     __shared__ std::uint32_t lds_taken_equal;
 
-    const int q = blockIdx.x;
-    if (!args.force && args.flags[q] == 0u) {
+    int q = blockIdx.x;
+    int entry = 0;
+    int listed = 0;
+    if (args.force) {
+        // every query
+    } else if (args.flag_list != nullptr) {
+        listed = static_cast<int>(*args.flag_count);
+        entry = blockIdx.x;
+        if (entry >= listed) {
+            return;
+        }
+        q = static_cast<int>(args.flag_list[entry]);
+    } else if (args.flags[q] == 0u) {
         return;
     }
     const int t = threadIdx.x;
     const int dim = scan.dim;
     const int width = args.width;
     const long long n = scan.doc_count;
+    if (args.seg != nullptr && !args.force && selectFromRerun(args, q, entry, listed, scan.batch)) {
+        return;
+    }
     const int words = chunks * stagedWordsPerChunk(kKind);
 
     // ---- the query, staged as the VALU scan stages it ----

@@ -20,6 +20,7 @@
 #include <hip/hip_runtime.h>
 
 #include <algorithm>
+#include <cmath>
 #include <mutex>
 #include <string>
 #include <vector>
@@ -79,6 +80,15 @@ struct Plan {
     bool direct_scales = false;  // MFMA path without a mask: only the tail tile's scales are copied
     bool lex_sorted = false;     // hybrid with postings ascending by document: sliced BM25 stage
     bool recover = false;        // threshold phases ran: the exact fallback follows them
+    // int8 MFMA scan over a large corpus: a sketch phase and one speculative full scan instead
+    // of the threshold phases (see makePlan)
+    bool sketch = false;
+    int sketch_slots = 0;        // sketch slots (2 per workgroup)
+    int sketch_rank = 0;         // tau = the sketch_rank-th best slot score
+    // the scan kernel reruns the flagged queries over the whole corpus before the fallback
+    bool rerun = false;
+    int rerun_seg_log2 = 0;      // the segments' normal capacity (the test flag shrinks seg_log2 only)
+    PhaseArgs full;              // every block of the corpus (the rerun's phase)
     bool single_pass = false;    // a few queries: one scan launch and one or two merges
     int sp_cap = 0;              // single pass: LDS list keys per query
     int sp_groups = 1;           // single pass: merge groups (a second merge when above 1)
@@ -95,7 +105,8 @@ struct Plan {
     std::size_t qbits = 0, qi8 = 0, qscale = 0, lex = 0, lexmax = 0, dense = 0, seg = 0,
                 segcnt = 0, keys = 0, tau = 0, overflow = 0, rescored = 0, scores = 0, lexmat = 0,
                 topk_a = 0, topk_b = 0, topk_c = 0, topk_d = 0, cand_idx = 0, cand_val = 0, sp_level = 0,
-                local_idx = 0, rescore_val = 0, lexmax_m = 0, lexbounds = 0;
+                local_idx = 0, rescore_val = 0, lexmax_m = 0, lexbounds = 0, sketchbuf = 0, tau_safe = 0,
+                flag_list = 0, flag_count = 0;
     std::size_t total = 0;
 };
 
@@ -442,14 +453,60 @@ Plan makePlan(const zcgvs_search_desc& d) {
     }
     plan.dense_stride = first.items * plan.block_rows;
     plan.segments = plan.workgroups * (plan.use_mfma ? mfmaSegmentsPerWorkgroup() : 1);
+    plan.full.stride = 1;
+    plan.full.skip = 0;
+    plan.full.items = blocks;
+    plan.full.block_rows = plan.block_rows;
+    plan.rerun = plan.use_mfma;
     // Segment capacity: 4x the expected candidates per (segment, query) of the widest phase.
-    const long long expected = (static_cast<long long>(plan.width) * growth) / plan.segments;
+    long long expected = (static_cast<long long>(plan.width) * growth) / plan.segments;
+
+    // Sketch plan (int8 MFMA scan, when the threshold phases would be three or more): a sketch
+    // phase over every 32nd block keeps per slot (a row half of a workgroup's lanes) the best
+    // exact score of each query; the j-th best of those 2 * workgroups scores is the threshold
+    // of ONE scan over the whole corpus. With f = sketch rows / corpus rows, the number of
+    // corpus rows at or above the sketch's j-th best score is about Gamma(j) / f, so
+    // j = width f + 5.5 sqrt(width f) + 2 (15 at f = 1/32, width = 100) leaves fewer than width
+    // such rows with probability about 1e-6 per query (Poisson tail), while the scan emits about
+    // j / f candidates per query. The merge flags a query for the fallback when fewer than width
+    // candidates reached it; the k-th best slot score is its guaranteed threshold then.
+    const int slots = 2 * plan.workgroups;
+    // (A smaller corpus samples every 16th, 8th or 4th block, so every workgroup still sees at
+    // least 4 sampled blocks; below that the threshold phases stay.)
+    long long sketch_stride = 32;
+    while (sketch_stride > 4 && phaseItems(blocks, sketch_stride, 0) < 4LL * plan.workgroups) {
+        sketch_stride /= 2;
+    }
+    if (plan.use_mfma && plan.phases.size() >= 3 && slots <= kMaxSketchSlots && slots >= plan.width &&
+        phaseItems(blocks, sketch_stride, 0) >= 4LL * plan.workgroups) {
+        PhaseArgs sketch;
+        sketch.stride = sketch_stride;
+        sketch.skip = 0;
+        sketch.items = phaseItems(blocks, sketch_stride, 0);
+        sketch.sketch = 1;
+        sketch.block_rows = plan.block_rows;
+        const double f = static_cast<double>(sketch.items) / static_cast<double>(blocks);
+        const double kf = plan.width * f;
+        const int j = static_cast<int>(std::ceil(kf + 5.5 * std::sqrt(kf) + 2.0));
+        plan.sketch = true;
+        plan.sketch_slots = slots;
+        plan.sketch_rank = std::max(1, std::min({j, plan.width, slots}));
+        if ((d.flags & ZCGVS_SEARCH_TEST_HIGH_THRESHOLD) != 0) {
+            plan.sketch_rank = 1;  // tests: most queries find fewer than width keys above it
+        }
+        plan.phases.clear();
+        plan.phases.push_back(sketch);
+        plan.phases.push_back(plan.full);
+        plan.dense_stride = 0;
+        expected = static_cast<long long>(std::ceil(plan.sketch_rank / f)) / plan.segments;
+    }
     // At least one full work item of candidates (two tiles of the int8 MFMA scan, whose segments
     // take half a tile's rows each) per segment, so a corpus whose best rows sit together in a few
     // blocks (sorted or clustered rows) does not overflow the segments.
     const long long item_rows = plan.use_mfma ? kMfmaBlockRows : plan.block_rows;
     // (at most 2^23 slots: the int8 MFMA scan packs a slot, a half and an 8-bit query into 32 bits)
     plan.seg_log2 = std::min(23, std::max({6, ceilLog2(4 * expected + 16), ceilLog2(item_rows)}));
+    plan.rerun_seg_log2 = plan.seg_log2;
     if ((d.flags & ZCGVS_SEARCH_TEST_TINY_SEGMENTS) != 0) {
         plan.seg_log2 = 1;  // tests: overflow nearly every query so the fallback runs from its flags
     }
@@ -461,11 +518,20 @@ Plan makePlan(const zcgvs_search_desc& d) {
     }
     plan.dense = layout.add(static_cast<std::size_t>(batch) * plan.dense_stride * 8);
     if (plan.phases.size() > 1) {
-        plan.seg = layout.add((static_cast<std::size_t>(plan.segments) * batch << plan.seg_log2) * 8);
+        // (the rerun shares the buffer at the normal capacity, which the test flag may lower
+        // for the first attempt)
+        const int seg_bits = plan.rerun ? std::max(plan.seg_log2, plan.rerun_seg_log2) : plan.seg_log2;
+        plan.seg = layout.add((static_cast<std::size_t>(plan.segments) * batch << seg_bits) * 8);
         plan.segcnt = layout.add(static_cast<std::size_t>(plan.segments) * batch * 4);
     }
     plan.keys = layout.add(static_cast<std::size_t>(batch) * plan.width * 8);
     plan.tau = layout.add(static_cast<std::size_t>(batch) * 8);
+    plan.flag_list = layout.add(static_cast<std::size_t>(batch) * 4);
+    plan.flag_count = layout.add(4);
+    if (plan.sketch) {
+        plan.sketchbuf = layout.add(static_cast<std::size_t>(plan.sketch_slots) * batch * 4);
+        plan.tau_safe = layout.add(static_cast<std::size_t>(batch) * 8);
+    }
     if (plan.rescore) {
         plan.rescored = layout.add(static_cast<std::size_t>(batch) * plan.width * 8);
     }
@@ -814,7 +880,12 @@ int searchTopk(const zcgvs_search_desc* desc, void* d_workspace, std::size_t wor
         emit.seg = plan.phases.size() > 1 ? at<std::uint64_t>(ws, plan.seg) : nullptr;
         emit.seg_count = plan.phases.size() > 1 ? at<std::uint32_t>(ws, plan.segcnt) : nullptr;
         emit.seg_log2 = plan.seg_log2;
+        if (plan.sketch) {
+            emit.sketch = at<float>(ws, plan.sketchbuf);
+        }
         std::uint64_t* tau = at<std::uint64_t>(ws, plan.tau);
+        std::uint32_t* flag_list = at<std::uint32_t>(ws, plan.flag_list);
+        std::uint32_t* flag_count = at<std::uint32_t>(ws, plan.flag_count);
 
         if (phases_out != nullptr) {
             *phases_out = static_cast<int>(plan.phases.size());
@@ -840,12 +911,32 @@ int searchTopk(const zcgvs_search_desc* desc, void* d_workspace, std::size_t wor
             if (timed) {
                 ZCGVS_HIP_RETURN(hipEventRecord(reinterpret_cast<hipEvent_t>(events[2 * p + 1]), s));
             }
+            const bool last = p + 1 == plan.phases.size();
+            if (phase.sketch) {
+                // the speculative threshold and the guaranteed one; clears the flagged list
+                status = launchSketchThreshold(emit.sketch, plan.sketch_slots, batch, plan.sketch_rank, plan.width,
+                                               tau, at<std::uint64_t>(ws, plan.tau_safe), flag_count, s);
+                if (status != ZCGVS_OK) {
+                    return status;
+                }
+                continue;
+            }
             MergeInputs in;
-            if (p == 0) {
+            if (plan.sketch) {
+                // the one merge of the speculative scan
+                in.seg = emit.seg;
+                in.seg_count = emit.seg_count;
+                in.n_seg = plan.segments;
+                in.seg_log2 = plan.seg_log2;
+                in.reset_overflow = true;
+                in.require_full = true;
+                in.fallback_tau = at<std::uint64_t>(ws, plan.tau_safe);
+            } else if (p == 0) {
                 in.dense = emit.dense;
                 in.n_dense = phase.items * phase.block_rows;
                 in.dense_stride = plan.dense_stride;
                 in.reset_overflow = true;
+                in.zero_count = flag_count;
             } else {
                 in.prev = keys;
                 in.k_prev = plan.width;
@@ -854,9 +945,14 @@ int searchTopk(const zcgvs_search_desc* desc, void* d_workspace, std::size_t wor
                 in.n_seg = plan.segments;
                 in.seg_log2 = plan.seg_log2;
             }
-            const bool last = p + 1 == plan.phases.size();
+            if (last) {
+                in.final_merge = true;
+                in.flag_list = flag_list;
+                in.flag_count = flag_count;
+                in.rerun_tau = tau;
+            }
             const bool write_out = last && !plan.rescore;
-            status = launchSelectMerge(in, plan.width, batch, keys, tau, overflow,
+            status = launchSelectMerge(in, plan.width, batch, keys, last ? nullptr : tau, overflow,
                                        write_out ? d_out_indices : nullptr,
                                        write_out ? d_out_values : nullptr, s);
             if (status != ZCGVS_OK) {
@@ -865,15 +961,39 @@ int searchTopk(const zcgvs_search_desc* desc, void* d_workspace, std::size_t wor
         }
     }
 
-    // 4. the exact fallback for queries whose segments overflowed (a near-empty launch otherwise)
+    // 4. the exact fallback for the flagged queries (near-empty launches otherwise): the scan
+    //    kernel's rerun over the whole corpus where it has one, then the selection from the
+    //    rerun's segments, or the last resort's recomputation
     if (plan.recover) {
+        const bool force = (d.flags & ZCGVS_SEARCH_FORCE_EXACT_PASS) != 0;
+        const bool multi_phase = plan.phases.size() > 1;
+        const bool rerun = plan.rerun && multi_phase && !force;
         RecoverArgs recovery;
         recovery.flags = overflow;
-        recovery.force = (d.flags & ZCGVS_SEARCH_FORCE_EXACT_PASS) != 0;
+        recovery.force = force || !multi_phase;
         recovery.width = plan.width;
         recovery.out_keys = keys;
         recovery.out_index = plan.rescore ? nullptr : d_out_indices;
         recovery.out_score = plan.rescore ? nullptr : d_out_values;
+        recovery.flag_list = at<std::uint32_t>(ws, plan.flag_list);
+        recovery.flag_count = at<std::uint32_t>(ws, plan.flag_count);
+        if (rerun) {
+            EmitArgs again;
+            again.tau = at<std::uint64_t>(ws, plan.tau);
+            again.seg = at<std::uint64_t>(ws, plan.seg);
+            again.seg_count = at<std::uint32_t>(ws, plan.segcnt);
+            again.seg_log2 = plan.rerun_seg_log2;
+            again.q_list = recovery.flag_list;
+            again.q_list_count = recovery.flag_count;
+            status = launchMfmaScan(scanArgsOf(d, plan, ws), plan.full, again, plan.workgroups, s);
+            if (status != ZCGVS_OK) {
+                return status;
+            }
+            recovery.seg = again.seg;
+            recovery.seg_count = again.seg_count;
+            recovery.n_seg = plan.segments;
+            recovery.seg_log2 = plan.rerun_seg_log2;
+        }
         status = launchRecover(recoverArgsOf(d, plan, ws), recovery, s);
         if (status != ZCGVS_OK) {
             return status;

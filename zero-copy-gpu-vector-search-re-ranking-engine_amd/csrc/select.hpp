@@ -159,6 +159,22 @@ struct MergeInputs {
     // true for the first merge of a search: it writes every query's overflow flag (0 or 1)
     // instead of only raising flags, so no separate clearing pass is needed
     bool reset_overflow = false;
+    // When set (first merge of a phased search), block 0 clears *zero_count: the exact
+    // fallback's list of flagged queries starts empty.
+    std::uint32_t* zero_count = nullptr;
+    // The search's last merge flags a query for the exact fallback when a segment overflowed in
+    // this or an earlier phase (the overflow flag an earlier merge raised), or, with
+    // require_full, when fewer than k keys reached it (a speculative threshold was above the
+    // k-th best key). A flagged query gets overflow[q] = 1, is appended to flag_list (length in
+    // *flag_count) and gets the fallback's threshold in rerun_tau[q]: its k-th best key minus
+    // one when it has k keys (every key >= that k-th best key passes), else fallback_tau[q] (a
+    // guaranteed lower bound; 0 without one). Other queries get overflow[q] = 0.
+    bool final_merge = false;
+    bool require_full = false;
+    const std::uint64_t* fallback_tau = nullptr;
+    std::uint32_t* flag_list = nullptr;
+    std::uint32_t* flag_count = nullptr;
+    std::uint64_t* rerun_tau = nullptr;
 };
 
 // Selects the best k keys of each query's candidate set; writes them to out_keys[q][0..k)
@@ -179,5 +195,16 @@ constexpr int kSortedMergeMaxK = 32;
 constexpr int kSortedMergeMaxSegments = 1024;
 int launchSortedSegmentMerge(const MergeInputs& in, int k, int batch, std::uint64_t* out_keys,
                              std::uint32_t* overflow, int* out_index, float* out_score, hipStream_t stream);
+
+// Thresholds of a speculative scan from a sketch phase (one block per query). Slot s holds the
+// best exact score of its rows, sketch[s * batch + q] (-inf: the slot saw no row); the slots'
+// rows are disjoint, so their scores belong to distinct corpus rows. tau[q] admits every score
+// >= the j-th best slot score and tau_safe[q] every score >= the k-th best one (as the keys
+// ordered32(score) << 32; 0 = no threshold when fewer slots hold a score). tau_safe is a lower
+// bound of the k-th best key of the corpus; tau is only likely to be one. Block 0 also clears
+// *flag_count.
+constexpr int kMaxSketchSlots = 2048;
+int launchSketchThreshold(const float* sketch, int slots, int batch, int j, int k, std::uint64_t* tau,
+                          std::uint64_t* tau_safe, std::uint32_t* flag_count, hipStream_t stream);
 
 }  // namespace zcgvs_hip

@@ -272,10 +272,15 @@ __global__ __launch_bounds__(kMergeThreads) void selectMergeKernel(
     __shared__ std::uint32_t lds_wave_count[kMergeThreads / kWave];
     __shared__ std::uint64_t lds_wave_lo[kMergeThreads / kWave];
     __shared__ std::uint64_t lds_wave_hi[kMergeThreads / kWave];
+    __shared__ std::uint64_t lds_kth;  // the k-th best key (0: fewer than k keys)
 
     const int q = blockIdx.x;
     const int t = threadIdx.x;
     if (t == 0) {
+        lds_kth = 0ull;
+        if (in.zero_count != nullptr && q == 0) {
+            *in.zero_count = 0u;
+        }
         lds_valid = 0u;
         lds_overflow = 0u;
         lds_state.prefix = 0ull;
@@ -520,8 +525,11 @@ __global__ __launch_bounds__(kMergeThreads) void selectMergeKernel(
             dst[rank] = key;
             const std::size_t o = static_cast<std::size_t>(q) * k + rank;
             writeHit(key, &out_index[o], &out_score[o]);
-            if (threshold != nullptr && rank == static_cast<std::uint32_t>(k) - 1u) {
-                threshold[q] = key;
+            if (rank == static_cast<std::uint32_t>(k) - 1u) {
+                lds_kth = key;
+                if (threshold != nullptr) {
+                    threshold[q] = key;
+                }
             }
         }
     } else {
@@ -541,8 +549,11 @@ __global__ __launch_bounds__(kMergeThreads) void selectMergeKernel(
         if (t < kWave) {  // wavefront 0 reduces the per-wavefront minima
             std::uint64_t v = t < kMergeThreads / kWave ? lds_wave_lo[t] : ~0ull;
             v = waveReduce64(v, [](std::uint64_t a, std::uint64_t b) { return min(a, b); });
-            if (t == 0 && threshold != nullptr && taken >= static_cast<std::uint32_t>(k)) {
-                threshold[q] = v;
+            if (t == 0 && taken >= static_cast<std::uint32_t>(k)) {
+                lds_kth = v;
+                if (threshold != nullptr) {
+                    threshold[q] = v;
+                }
             }
         }
     }
@@ -553,11 +564,22 @@ __global__ __launch_bounds__(kMergeThreads) void selectMergeKernel(
             writeHit(0ull, &out_index[o], &out_score[o]);
         }
     }
+    __syncthreads();  // lds_kth and the threshold written above
     if (t == 0) {
         if (threshold != nullptr && taken < static_cast<std::uint32_t>(k)) {
             threshold[q] = 0ull;
         }
-        if (overflow != nullptr && (lds_overflow != 0u || in.reset_overflow)) {
+        if (in.final_merge) {
+            const bool earlier = !in.reset_overflow && overflow[q] != 0u;
+            const bool flagged = lds_overflow != 0u || earlier ||
+                                 (in.require_full && taken < static_cast<std::uint32_t>(k));
+            overflow[q] = flagged ? 1u : 0u;
+            if (flagged) {
+                const std::uint64_t kth = lds_kth;
+                in.rerun_tau[q] = kth != 0ull ? kth - 1ull : (in.fallback_tau != nullptr ? in.fallback_tau[q] : 0ull);
+                in.flag_list[atomicAdd(in.flag_count, 1u)] = static_cast<std::uint32_t>(q);
+            }
+        } else if (overflow != nullptr && (lds_overflow != 0u || in.reset_overflow)) {
             overflow[q] = lds_overflow != 0u ? 1u : 0u;
         }
     }
@@ -662,6 +684,59 @@ __global__ __launch_bounds__(kSortedMergeThreads) void sortedSegmentMergeKernel(
     }
 }
 
+// ---- thresholds from a sketch phase (one block per query) ----------------------------------------
+
+constexpr int kSketchThreads = 256;
+
+__global__ __launch_bounds__(kSketchThreads) void sketchThresholdKernel(const float* __restrict__ sketch, int slots,
+                                                                         int batch, int j, int k,
+                                                                         std::uint64_t* __restrict__ tau,
+                                                                         std::uint64_t* __restrict__ tau_safe,
+                                                                         std::uint32_t* __restrict__ flag_count) {
+    __shared__ std::uint64_t lds_key[kMaxSketchSlots];
+    __shared__ std::uint64_t lds_pick[2];
+    const int q = blockIdx.x;
+    const int t = threadIdx.x;
+    // unique keys: the slot score's ordered bits, then the slot (an empty slot is key 0)
+    for (int s = t; s < slots; s += kSketchThreads) {
+        const float v = sketch[static_cast<std::size_t>(s) * batch + q];
+        lds_key[s] = v > -INFINITY ? (static_cast<std::uint64_t>(orderedBits(v)) << 32) |
+                                         static_cast<std::uint64_t>(0xFFFFFFFFu - static_cast<std::uint32_t>(s))
+                                   : 0ull;
+    }
+    if (t < 2) {
+        lds_pick[t] = 0ull;
+    }
+    if (q == 0 && t == 0) {
+        *flag_count = 0u;
+    }
+    __syncthreads();
+    // the keys of rank j - 1 and k - 1 (rank = number of larger keys)
+    for (int s = t; s < slots; s += kSketchThreads) {
+        const std::uint64_t key = lds_key[s];
+        if (key == 0ull) {
+            continue;
+        }
+        int rank = 0;
+#pragma unroll 8
+        for (int x = 0; x < slots; ++x) {
+            rank += lds_key[x] > key ? 1 : 0;
+        }
+        const std::uint64_t admit = key & 0xFFFFFFFF00000000ull;  // every score >= this one
+        if (rank == j - 1) {
+            lds_pick[0] = admit;
+        }
+        if (rank == k - 1) {
+            lds_pick[1] = admit;
+        }
+    }
+    __syncthreads();
+    if (t == 0) {
+        tau[q] = lds_pick[0];
+        tau_safe[q] = lds_pick[1];
+    }
+}
+
 int topkScratchElements(int doc_count, int k) {
     if (doc_count <= 0 || k <= 0) {
         return 0;
@@ -682,6 +757,17 @@ int launchSelectMerge(const MergeInputs& in, int k, int batch, std::uint64_t* ou
     selectMergeKernel<<<batch, kMergeThreads, 0, stream>>>(in, k, batch, out_keys, threshold,
                                                             overflow, out_index, out_score);
     ZCGVS_LAUNCH_CHECK("select merge");
+    return ZCGVS_OK;
+}
+
+int launchSketchThreshold(const float* sketch, int slots, int batch, int j, int k, std::uint64_t* tau,
+                          std::uint64_t* tau_safe, std::uint32_t* flag_count, hipStream_t stream) {
+    if (slots < 1 || slots > kMaxSketchSlots || j < 1 || k < 1) {
+        return setError(ZCGVS_ERR_RUNTIME, "zcgvs select: sketch threshold shape out of range");
+    }
+    sketchThresholdKernel<<<batch, kSketchThreads, 0, stream>>>(sketch, slots, batch, j, k, tau, tau_safe,
+                                                                 flag_count);
+    ZCGVS_LAUNCH_CHECK("sketch threshold");
     return ZCGVS_OK;
 }
 
