@@ -322,7 +322,12 @@ size_t zcgvs_search_workspace_bytes(const zcgvs_search_desc* desc);
  * zcgvs_search_overflow_flags tells which queries took the fallback. A search of at most four
  * queries selecting at most 1024 keys each (k, or rescore_candidates with a rescore store) that
  * no matrix-core scan takes reads the corpus in a single pass whose per-workgroup lists are exact
- * (selections above 32 keys merge groups of workgroups first); it never overflows. */
+ * (selections above 32 keys merge groups of workgroups first); it never overflows.
+ * Non-finite inputs: float32 rows of 256 or 384 dims searched with 32 to 128 queries per launch
+ * are scanned on the bf16 matrix cores as exact three-part splits, where a row or query with an
+ * infinite or NaN component scores NaN (it ranks last); every other scan follows the IEEE sum,
+ * where such a score can be +inf and rank first. So with non-finite data the result can depend
+ * on the batch size (the reference defines no order for non-finite scores either). */
 int zcgvs_search_topk(const zcgvs_search_desc* desc, void* d_workspace, size_t workspace_bytes,
                       int* d_out_indices, float* d_out_values, zcgvs_stream_t stream);
 
@@ -333,14 +338,17 @@ int zcgvs_search_topk(const zcgvs_search_desc* desc, void* d_workspace, size_t w
  * (zcgvs_search_workspace_bytes) exceeds that size is rejected with ZCGVS_ERR_INVALID_ARGUMENT;
  * nothing is allocated or freed, on the host's HIP side or the device. Every call on one device
  * shares that device's array: calls that overlap on one GPU (concurrent streams, threads) race
- * and must be serialized by the caller. The results equal zcgvs_search_topk's. */
+ * and must be serialized by the caller. The results equal zcgvs_search_topk's. The array's device
+ * address is looked up on the first call on a device, or earlier by zcgvs_graph_begin_capture,
+ * so a call recorded into a graph performs no lookup. */
 size_t zcgvs_static_scratch_bytes(void);
 int zcgvs_search_topk_noalloc(const zcgvs_search_desc* desc, int* d_out_indices, float* d_out_values,
                               zcgvs_stream_t stream);
 
 /* Measurement hook: zcgvs_search_topk that also records events[2p] and events[2p + 1] on `stream`
  * immediately before and after the scan launches of phase p, for p < max_phases, and returns the
- * number of phases in *phases. The events must have been created with zcgvs_event_create. Not
+ * number of phases in *phases. A fused hybrid search also brackets its lexical (BM25) stage with
+ * the next pair, events[2 * phases] and events[2 * phases + 1], when max_phases > *phases. The events must have been created with zcgvs_event_create. Not
  * meant for graph capture. No reference counterpart (the reference times the whole pipeline with
  * one event pair, src/search/searcher.cpp:358-365). */
 int zcgvs_search_topk_profiled(const zcgvs_search_desc* desc, void* d_workspace,

@@ -100,3 +100,33 @@ def test_split_scan_wide_dynamic_range(gpu, dim, batch):
     idx, val = search(capi, corpus, capi.F32, queries, k, 1)
     ref = oracle.scores_f32(corpus, queries, 1)
     assert_topk_equivalent(idx, val, ref, k, float_tolerance(queries, corpus, 1))
+
+
+def test_non_finite_rows_depend_on_the_scan(gpu):
+    """A float32 row with an infinite component: the bf16 split scan (32-128 queries of 256 or 384
+    dims per launch) scores it NaN, which ranks last; the float32 scans follow the IEEE sum, so for
+    a query whose matching component is positive it scores +inf and ranks first. This pins the
+    documented difference (the reference defines no order for non-finite scores)."""
+    capi = gpu
+    n, dim, k = 40_000, 384, 10
+    corpus = normalized(n, dim, 501)
+    corpus[7, 5] = np.float32(np.inf)
+    queries = normalized(32, dim, 502)
+    queries[:, 5] = np.abs(queries[:, 5]) + np.float32(0.01)  # the inf component meets a positive one
+    idx, val = search(capi, corpus, capi.F32, queries, k, 1)  # 32 queries: the split scan
+    assert not (idx == 7).any(), "the split scan should rank the non-finite row last"
+    one_idx, one_val = search(capi, corpus, capi.F32, queries[:1], k, 1)  # one query: float32 sums
+    assert one_idx[0, 0] == 7 and np.isinf(one_val[0, 0]) and one_val[0, 0] > 0
+    # the finite rows agree with the oracle either way
+    finite = np.ones(n, dtype=bool)
+    finite[7] = False
+    ref = oracle.scores_f32(corpus[finite], queries, 1)
+    remap = np.flatnonzero(finite)
+    ref_idx, _ = oracle.topk(ref, k)
+    tol = float_tolerance(queries, corpus[finite], 1)
+    for b in range(queries.shape[0]):
+        for r in range(k):
+            g, e = int(idx[b, r]), int(remap[ref_idx[b, r]])
+            if g != e:
+                gi = int(np.flatnonzero(remap == g)[0])
+                assert abs(float(ref[b, gi]) - float(ref[b, ref_idx[b, r]])) <= tol[b, gi] + tol[b, ref_idx[b, r]]

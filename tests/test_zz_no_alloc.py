@@ -1,6 +1,7 @@
 """zcgvs_search_topk_noalloc (workspace in the library's static device array) against
 zcgvs_search_topk (caller workspace), through the C ABI: two calls in a row on each path, the
-second with a smaller input, bit-identical ids and scores; a search whose workspace exceeds the
+second with a smaller input, bit-identical ids and scores; the entry point captured into a HIP
+graph and replayed gives the same result on every replay; a search whose workspace exceeds the
 static array is rejected."""
 
 from __future__ import annotations
@@ -75,3 +76,28 @@ def test_noalloc_rejects_a_search_beyond_the_static_scratch(gpu):
     assert capi.search_workspace_bytes(desc) > 64 << 20  # a [64, 2M] score matrix
     with pytest.raises(ValueError, match="static scratch"):
         capi.call("zcgvs_search_topk_noalloc", capi.ctypes.byref(desc), 1 << 20, 1 << 20, None)
+
+
+def test_noalloc_captured_in_a_graph(gpu):
+    """Captured once (zcgvs_graph_begin_capture resolves the static scratch first), replayed
+    three times with other searches in between; every replay equals the direct call."""
+    capi = gpu
+    desc, ref, _keep = _int8_case(capi, 120_000, 16, 51)
+    other, _, _keep2 = _float_case(capi, 90_000, 5, 61)
+    (exp_idx, exp_val, _), _ = _pair(capi, desc)
+    assert np.array_equal(exp_idx, ref[0]) and np.array_equal(exp_val, ref[1])
+    idx = capi.DeviceArray((desc.batch, desc.k), np.int32)
+    val = capi.DeviceArray((desc.batch, desc.k), np.float32)
+    stream = capi.Stream()
+    graph = capi.Graph(stream, lambda: capi.call("zcgvs_search_topk_noalloc", capi.ctypes.byref(desc), idx.ptr,
+                                                 val.ptr, stream.handle))
+    for replay in range(3):
+        capi.call("zcgvs_memset", idx.ptr, 0, idx.nbytes, None)
+        capi.synchronize()
+        graph.launch(stream)
+        stream.synchronize()
+        assert np.array_equal(idx.to_host(), exp_idx), f"replay {replay}: ids differ"
+        assert np.array_equal(val.to_host(), exp_val), f"replay {replay}: scores differ"
+        # eager work on the same static scratch between replays
+        capi.call("zcgvs_search_topk_noalloc", capi.ctypes.byref(other), idx.ptr, val.ptr, None)
+        capi.synchronize()

@@ -65,6 +65,11 @@ inline bool validMetric(int metric) { return metric >= ZCGVS_METRIC_COSINE && me
 // Number of compute units of the current device (cached per device).
 int deviceComputeUnits();
 
+// Looks up the current device's address of the no-allocation entry point's static scratch
+// array (once per device; later calls return at once), so that no lookup happens inside a
+// graph capture: zcgvs_graph_begin_capture calls it before the capture starts.
+int prepareStaticScratch();
+
 // --------------------------------------------------------------------------------------------
 // Device helpers
 // --------------------------------------------------------------------------------------------

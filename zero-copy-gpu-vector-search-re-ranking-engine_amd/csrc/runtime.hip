@@ -281,6 +281,11 @@ int zcgvs_graph_begin_capture(zcgvs_stream_t stream) {
         return setError(ZCGVS_ERR_INVALID_ARGUMENT,
                         "zcgvs: graph capture needs a created (non-null) stream");
     }
+    // the static scratch of zcgvs_search_topk_noalloc is looked up now, outside the capture
+    const int status = prepareStaticScratch();
+    if (status != ZCGVS_OK) {
+        return status;
+    }
     ZCGVS_HIP_RETURN(hipStreamBeginCapture(toStream(stream), hipStreamCaptureModeThreadLocal));
     return clearError();
 }

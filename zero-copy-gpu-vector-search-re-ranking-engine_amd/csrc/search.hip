@@ -680,6 +680,11 @@ int scratchAddress(void** address) {
 
 }  // namespace
 
+int prepareStaticScratch() {
+    void* address = nullptr;
+    return scratchAddress(&address);
+}
+
 }  // namespace zcgvs_hip
 
 using namespace zcgvs_hip;
@@ -762,14 +767,22 @@ int searchTopk(const zcgvs_search_desc* desc, void* d_workspace, std::size_t wor
         return status == ZCGVS_OK ? clearError() : status;
     }
 
-    // 2. lexical scores
+    // 2. lexical scores (timed by the event pair after the scan phases' pairs, when there is one)
     if (plan.hybrid) {
+        const int lex_pair = static_cast<int>(plan.phases.size());
+        const bool timed = events != nullptr && lex_pair < max_phases;
+        if (timed) {
+            ZCGVS_HIP_RETURN(hipEventRecord(reinterpret_cast<hipEvent_t>(events[2 * lex_pair]), s));
+        }
         status = launchLexicalScores(d.lex_offsets, d.lex_docs, d.lex_weights, d.lex_vocab_size, d.query_terms,
                                      d.lexical_stride, batch, static_cast<int>(d.corpus.doc_count),
                                      at<float>(ws, plan.lex), at<float>(ws, plan.lexmax),
                                      plan.lex_sorted ? at<std::int64_t>(ws, plan.lexbounds) : nullptr, s);
         if (status != ZCGVS_OK) {
             return status;
+        }
+        if (timed) {
+            ZCGVS_HIP_RETURN(hipEventRecord(reinterpret_cast<hipEvent_t>(events[2 * lex_pair + 1]), s));
         }
     }
 
