@@ -89,17 +89,21 @@ constexpr std::size_t kRingBudget = 150 * 1024;
 constexpr int kStaged = 64;  // candidates parked per wavefront before they reach the segments
 constexpr int kMinBatch = 8;
 
-// kMode: kThreshold (emit keys above the threshold), kDense (every key to its fixed slot) or
-// kSketch (per slot the best exact score, no keys).
+// kMode: kThreshold (emit keys above the threshold), kDense (every key to its fixed slot),
+// kSketch (per slot the best exact score, no keys) or kRerun (kThreshold over the queries of
+// EmitArgs::q_list; a kernel of its own, so profiles tell the fallback's launches apart).
 constexpr int kThreshold = 0;
 constexpr int kDenseMode = 1;
 constexpr int kSketchMode = 2;
+constexpr int kRerunMode = 3;
 
 template <int kKSteps, int kMode>
 __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(2, 2)))
 void mfmaScanKernel(ScanArgs scan, PhaseArgs phase, EmitArgs emit, int q_offset, int q_count) {
     constexpr bool kDense = kMode == kDenseMode;
     constexpr bool kSketch = kMode == kSketchMode;
+    constexpr bool kListed = kMode == kRerunMode;
+    constexpr bool kEmits = kMode == kThreshold || kListed;  // keys above a threshold
     constexpr int kDim = kKSteps * 32;
     constexpr int kSlotsPerRow = kDim / 16;
     constexpr int kTileBytes = kRows * kDim;
@@ -118,16 +122,15 @@ void mfmaScanKernel(ScanArgs scan, PhaseArgs phase, EmitArgs emit, int q_offset,
     __shared__ __attribute__((aligned(16))) std::uint8_t ring[kDepth][kTileBytes];
     __shared__ __attribute__((aligned(16))) float scale_ring[kScaleDepth][kRows];
     __shared__ std::uint32_t lds_simd[4];
-    __shared__ std::uint64_t stage_key[kMode == kThreshold ? kWaves : 1][kStaged];
+    __shared__ std::uint64_t stage_key[kEmits ? kWaves : 1][kStaged];
     // (segment slot << 9) | (half << 8) | local query
-    __shared__ std::uint32_t stage_slot[kMode == kThreshold ? kWaves : 1][kStaged];
+    __shared__ std::uint32_t stage_slot[kEmits ? kWaves : 1][kStaged];
 
     // A rerun scans list entries [q_offset, q_offset + 256) of q_list; F = *q_list_count entries
     // exist, so a launch past them has nothing to do (uniform over the workgroup).
-    const bool listed = emit.q_list != nullptr;
     int seg_batch = scan.batch;     // query rows of the segment layout
     int seg_log2 = emit.seg_log2;   // slots per segment row
-    if (listed) {
+    if constexpr (kListed) {
         const int entries = static_cast<int>(__builtin_amdgcn_readfirstlane(*emit.q_list_count));
         if (entries <= q_offset) {
             return;
@@ -153,7 +156,7 @@ void mfmaScanKernel(ScanArgs scan, PhaseArgs phase, EmitArgs emit, int q_offset,
     const bool wave_active = wave * 32 < q_count;
     // entry: the lane's row of the segment layout; q: its query
     const int entry = q_offset + min(qlocal, q_count - 1);
-    const int q = listed ? static_cast<int>(emit.q_list[entry]) : entry;
+    const int q = kListed ? static_cast<int>(emit.q_list[entry]) : entry;
     v4i qf[kKSteps];
     {
         const std::int8_t* qrow = queries + static_cast<std::size_t>(q) * kDim + 16 * half;
@@ -166,7 +169,7 @@ void mfmaScanKernel(ScanArgs scan, PhaseArgs phase, EmitArgs emit, int q_offset,
     const float qscale = scan.query_scales[q];
     std::uint64_t tau = 0ull;
     float tau_floor = -INFINITY;
-    if constexpr (kMode == kThreshold) {
+    if constexpr (kEmits) {
         tau = emit.tau[q];
         if (tau != 0ull) {
             const float t = keyScore(tau);
@@ -575,6 +578,8 @@ int launchShape(const ScanArgs& scan, const PhaseArgs& phase, const EmitArgs& em
             mfmaScanKernel<kKSteps, kDenseMode><<<grid, kThreads, 0, stream>>>(scan, phase, emit, q0, count);
         } else if (phase.sketch) {
             mfmaScanKernel<kKSteps, kSketchMode><<<grid, kThreads, 0, stream>>>(scan, phase, emit, q0, count);
+        } else if (emit.q_list != nullptr) {
+            mfmaScanKernel<kKSteps, kRerunMode><<<grid, kThreads, 0, stream>>>(scan, phase, emit, q0, count);
         } else {
             mfmaScanKernel<kKSteps, kThreshold><<<grid, kThreads, 0, stream>>>(scan, phase, emit, q0, count);
         }

@@ -686,54 +686,79 @@ __global__ __launch_bounds__(kSortedMergeThreads) void sortedSegmentMergeKernel(
 
 // ---- thresholds from a sketch phase (one block per query) ----------------------------------------
 
-constexpr int kSketchThreads = 256;
+constexpr int kSketchThreads = 64;  // one wavefront per query
 
+// The slot scores sorted in registers: lane l holds elements l * kPerLane + r (r < kPerLane) of
+// a bitonic sort into descending order, for up to 64 * kPerLane slots; partners in the same lane
+// are compare-exchanged in registers, partners in other lanes (stride >= kPerLane) through
+// lane shuffles, so the sort needs no barrier and no LDS round trip.
+template <int kPerLane>
 __global__ __launch_bounds__(kSketchThreads) void sketchThresholdKernel(const float* __restrict__ sketch, int slots,
                                                                          int batch, int j, int k,
                                                                          std::uint64_t* __restrict__ tau,
                                                                          std::uint64_t* __restrict__ tau_safe,
                                                                          std::uint32_t* __restrict__ flag_count) {
-    __shared__ std::uint64_t lds_key[kMaxSketchSlots];
-    __shared__ std::uint64_t lds_pick[2];
+    constexpr int kN = kSketchThreads * kPerLane;
     const int q = blockIdx.x;
-    const int t = threadIdx.x;
-    // unique keys: the slot score's ordered bits, then the slot (an empty slot is key 0)
-    for (int s = t; s < slots; s += kSketchThreads) {
-        const float v = sketch[static_cast<std::size_t>(s) * batch + q];
-        lds_key[s] = v > -INFINITY ? (static_cast<std::uint64_t>(orderedBits(v)) << 32) |
-                                         static_cast<std::uint64_t>(0xFFFFFFFFu - static_cast<std::uint32_t>(s))
-                                   : 0ull;
+    const int l = threadIdx.x;
+    // the slot scores' ordered bits; an empty slot (-inf: it saw no row) and the padding are 0
+    std::uint32_t v[kPerLane];
+#pragma unroll
+    for (int r = 0; r < kPerLane; ++r) {
+        const int s = l * kPerLane + r;
+        const float x = s < slots ? sketch[static_cast<std::size_t>(s) * batch + q] : -INFINITY;
+        v[r] = x > -INFINITY ? orderedBits(x) : 0u;
     }
-    if (t < 2) {
-        lds_pick[t] = 0ull;
-    }
-    if (q == 0 && t == 0) {
+    if (q == 0 && l == 0) {
         *flag_count = 0u;
     }
-    __syncthreads();
-    // the keys of rank j - 1 and k - 1 (rank = number of larger keys)
-    for (int s = t; s < slots; s += kSketchThreads) {
-        const std::uint64_t key = lds_key[s];
-        if (key == 0ull) {
-            continue;
-        }
-        int rank = 0;
-#pragma unroll 8
-        for (int x = 0; x < slots; ++x) {
-            rank += lds_key[x] > key ? 1 : 0;
-        }
-        const std::uint64_t admit = key & 0xFFFFFFFF00000000ull;  // every score >= this one
-        if (rank == j - 1) {
-            lds_pick[0] = admit;
-        }
-        if (rank == k - 1) {
-            lds_pick[1] = admit;
+#pragma unroll
+    for (int size = 2; size <= kN; size <<= 1) {
+#pragma unroll
+        for (int stride = size >> 1; stride > 0; stride >>= 1) {
+            if (stride < kPerLane) {
+#pragma unroll
+                for (int r = 0; r < kPerLane; ++r) {
+                    if ((r & stride) == 0) {
+                        const bool descending = ((l * kPerLane + r) & size) == 0;
+                        const std::uint32_t a = v[r];
+                        const std::uint32_t b = v[r + stride];
+                        const bool swap = (a < b) == descending;
+                        v[r] = swap ? b : a;
+                        v[r + stride] = swap ? a : b;
+                    }
+                }
+            } else {
+                const int lanes = stride / kPerLane;
+                const bool low = (l & lanes) == 0;
+#pragma unroll
+                for (int r = 0; r < kPerLane; ++r) {
+                    const std::uint32_t other = static_cast<std::uint32_t>(__shfl_xor(static_cast<int>(v[r]), lanes, kWave));
+                    const bool descending = ((l * kPerLane + r) & size) == 0;
+                    const bool keep_max = low == descending;
+                    v[r] = keep_max ? max(v[r], other) : min(v[r], other);
+                }
+            }
         }
     }
-    __syncthreads();
-    if (t == 0) {
-        tau[q] = lds_pick[0];
-        tau_safe[q] = lds_pick[1];
+    // every score >= the j-th (k-th) best slot score; 0 when that slot is empty or missing
+#pragma unroll
+    for (int r = 0; r < kPerLane; ++r) {
+        const int e = l * kPerLane + r;
+        if (e == j - 1) {
+            tau[q] = j <= slots ? static_cast<std::uint64_t>(v[r]) << 32 : 0ull;
+        }
+        if (e == k - 1) {
+            tau_safe[q] = k <= slots ? static_cast<std::uint64_t>(v[r]) << 32 : 0ull;
+        }
+    }
+    if (l == 0) {
+        if (j > kN) {
+            tau[q] = 0ull;
+        }
+        if (k > kN) {
+            tau_safe[q] = 0ull;
+        }
     }
 }
 
@@ -765,8 +790,16 @@ int launchSketchThreshold(const float* sketch, int slots, int batch, int j, int 
     if (slots < 1 || slots > kMaxSketchSlots || j < 1 || k < 1) {
         return setError(ZCGVS_ERR_RUNTIME, "zcgvs select: sketch threshold shape out of range");
     }
-    sketchThresholdKernel<<<batch, kSketchThreads, 0, stream>>>(sketch, slots, batch, j, k, tau, tau_safe,
-                                                                 flag_count);
+    if (slots <= 64 * 8) {
+        sketchThresholdKernel<8><<<batch, kSketchThreads, 0, stream>>>(sketch, slots, batch, j, k, tau, tau_safe,
+                                                                      flag_count);
+    } else if (slots <= 64 * 16) {
+        sketchThresholdKernel<16><<<batch, kSketchThreads, 0, stream>>>(sketch, slots, batch, j, k, tau, tau_safe,
+                                                                       flag_count);
+    } else {
+        sketchThresholdKernel<32><<<batch, kSketchThreads, 0, stream>>>(sketch, slots, batch, j, k, tau, tau_safe,
+                                                                       flag_count);
+    }
     ZCGVS_LAUNCH_CHECK("sketch threshold");
     return ZCGVS_OK;
 }
