@@ -235,9 +235,11 @@ def scan_kernel_name(w):
         lexical = "true" if w["kind"] == "hybrid" else "false"
         return f"mfmaFloatScanKernel<{kind}, {w['dim']}, false, {lexical}>"
     if w["kind"] == "binary" and w["batch"] >= 4 and w["dim"] in (512, 1024):
-        # up to 32 queries per launch: the streaming kernel; more: the shared-tile kernel
-        name = "mfmaBinaryStreamKernel" if w["batch"] <= 32 else "mfmaBinaryScanKernel"
-        return f"{name}<{w['dim'] // 32}, false>"
+        # up to 32 queries per launch: the streaming kernel (mode 0: threshold scan); more: the
+        # shared-tile kernel
+        if w["batch"] <= 32:
+            return f"mfmaBinaryStreamKernel<{w['dim'] // 32}, 0>"
+        return f"mfmaBinaryScanKernel<{w['dim'] // 32}, false>"
     if w["batch"] <= 4:
         return "singlePassScanKernel"
     return "valuScanKernel"

@@ -307,18 +307,20 @@ size_t zcgvs_search_workspace_bytes(const zcgvs_search_desc* desc);
 /* Runs the fused pipeline. d_out_indices/d_out_values are [batch, k]. The workspace must be
  * zcgvs_search_workspace_bytes(desc) bytes; its contents need no initialization. Capture safe.
  * The result is the exact top-k for every input: the scan keeps only candidates above a sampled
- * threshold in bounded per-workgroup buffers. A per-vector int8 search on the matrix cores over a
- * large corpus is sketch-planned: a first launch over every 32nd block records per row half of
- * each workgroup the best score of each query, and one scan of the whole corpus keeps the keys
- * at or above the j-th best of those scores (a threshold that is likely, not certain, to lie
- * below the k-th best key); other searches run threshold phases whose thresholds are certain
+ * threshold in bounded per-workgroup buffers. A per-vector int8 search on the matrix cores, or a
+ * binary search of at most 32 queries, over a large corpus is sketch-planned: a first launch over
+ * every 32nd block records per slot (a row half of an int8 workgroup, a pair of a binary
+ * workgroup's wavefronts) the best score of each query, and one scan of the whole corpus keeps
+ * the keys at or above the j-th best of those scores (a threshold that is likely, not certain, to
+ * lie below the k-th best key); other searches run threshold phases whose thresholds are certain
  * lower bounds. The search's last merge flags a query whose buffers overflowed (a corpus whose
  * best rows crowd into a few blocks) or which found fewer than k keys above a speculative
  * threshold; flagged queries are completed on the device, in the same call and stream, by the
- * exact fallback: the int8 matrix-core scan runs once more over the whole corpus for just those
- * queries with a threshold that is a certain lower bound and the batch's candidate buffers
- * shared among them, and the selection is taken from that; for other scans, or when that rerun
- * overflows too, one workgroup per query selects over recomputed scores (a few corpus reads).
+ * exact fallback: for a sketch-planned search the scan runs once more over the whole corpus for
+ * just those queries with a threshold that is a certain lower bound and the batch's candidate
+ * buffers shared among them, and the selection is taken from that; for other scans, or when that
+ * rerun overflows too, one workgroup per query selects over recomputed scores (a few corpus
+ * reads).
  * zcgvs_search_overflow_flags tells which queries took the fallback. A search of at most four
  * queries selecting at most 1024 keys each (k, or rescore_candidates with a rescore store) that
  * no matrix-core scan takes reads the corpus in a single pass whose per-workgroup lists are exact

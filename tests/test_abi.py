@@ -157,6 +157,25 @@ def test_sketch_plan_samples_then_scans_everything(capi, n, batch, k, stride):
     assert rows == [sampled * 64 - ((blocks * 64 - n) if last_sampled else 0), n]
 
 
+@pytest.mark.parametrize("n,batch,k,stride,sketched", [
+    (50_000_000, 32, 1000, 32, True),   # the binary 50M x 1024 configuration's Hamming stage
+    (2_000_003, 20, 100, 4, True),      # every 4th 384-row block, ragged tail
+    (50_000_000, 33, 1000, 0, False),   # more than 32 queries: the tile scan, threshold phases
+    (1_000_000, 32, 100, 0, False),     # under 4 sampled blocks per workgroup: threshold phases
+])
+def test_binary_sketch_plan(capi, n, batch, k, stride, sketched):
+    # The binary streaming scan (at most 32 queries) takes the sketch plan with 384-row blocks of
+    # 1024-bit rows.
+    rows = capi.search_phase_rows(_desc(capi, n=n, dim=1024, dtype=capi.BINARY, batch=batch, k=k))
+    if sketched:
+        blocks = (n + 383) // 384
+        sampled = (blocks + stride - 1) // stride
+        last_sampled = (blocks - 1) % stride == 0
+        assert rows == [sampled * 384 - ((blocks * 384 - n) if last_sampled else 0), n]
+    else:
+        assert len(rows) >= 3 and sum(rows) == n
+
+
 @pytest.mark.parametrize("n,dtype,int8_mode,batch,k", [
     (100_000, 2, 1, 256, 100),      # per-vector int8 MFMA path below the sketch plan's size
     (1_000_000, 0, 0, 64, 10),      # float32 VALU path

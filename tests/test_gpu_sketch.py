@@ -9,7 +9,11 @@ threshold that is a certain lower bound (the rerun), and their selection comes f
 path must give the oracle's top-k bit for bit: the speculative path itself, the fallback when the
 threshold was too high (ZCGVS_SEARCH_TEST_HIGH_THRESHOLD), the rerun after overflowing candidate
 buffers (ZCGVS_SEARCH_TEST_TINY_SEGMENTS), the last resort (ZCGVS_SEARCH_FORCE_EXACT_PASS), with
-an allow-mask, and with more than one launch of 256 queries."""
+an allow-mask, and with more than one launch of 256 queries.
+
+A binary (Hamming) search of at most 32 queries runs the same plan in the streaming binary scan
+(8 sketch slots per workgroup, one per pair of wavefronts); Hamming scores tie massively, so the
+threshold admits every row at the threshold's distance."""
 
 from __future__ import annotations
 
@@ -114,3 +118,41 @@ def test_two_launches_of_queries(gpu, corpus):
     assert int(np.count_nonzero(tiny[2])) > batch // 2
     assert np.array_equal(plain[0], tiny[0]) and np.array_equal(plain[1], tiny[1])
     _sampled(corpus, plain[0], plain[1], [0, 255, 256, 299], k)
+
+
+BIN_N, BIN_DIM = 2_000_003, 1024
+
+
+@pytest.fixture(scope="module")
+def binary_corpus(gpu):
+    capi = gpu
+    words = np.random.default_rng(94).integers(0, 2**32, size=(BIN_N, BIN_DIM // 32), dtype=np.uint32)
+    queries = normalized(32, BIN_DIM, 95)
+    return dict(words=words, qwords=oracle.pack_binary(queries), d_words=capi.DeviceArray.from_host(words),
+                d_queries=capi.DeviceArray.from_host(queries))
+
+
+def _binary_desc(capi, c, batch, k, flags=0):
+    store = capi.store_desc(c["d_words"], BIN_N, BIN_DIM, capi.BINARY)
+    return capi.search_desc(store, c["d_queries"], batch, k, capi.COSINE, flags=flags)
+
+
+@pytest.mark.parametrize("batch,k", [(32, 100), (20, 1000)])
+def test_binary_sketch_plan(gpu, binary_corpus, batch, k):
+    capi = gpu
+    c = binary_corpus
+    desc = _binary_desc(capi, c, batch, k)
+    rows = capi.search_phase_rows(desc)
+    assert len(rows) == 2 and rows[1] == BIN_N, f"not sketch-planned: {rows}"
+    idx, val, flags = capi.search(desc)
+    assert not flags.any(), "a random corpus should not need the fallback"
+    for name, bits in (("high", capi.SEARCH_TEST_HIGH_THRESHOLD), ("tiny", capi.SEARCH_TEST_TINY_SEGMENTS),
+                       ("force", capi.SEARCH_FORCE_EXACT_PASS)):
+        got_idx, got_val, got_flags = capi.search(_binary_desc(capi, c, batch, k, bits))
+        if name != "force":
+            assert int(np.count_nonzero(got_flags)) > batch // 2, f"{name}: expected most queries flagged"
+        assert np.array_equal(got_idx, idx), f"{name}: ids differ from the speculative path's"
+        assert np.array_equal(got_val, val), f"{name}: scores differ from the speculative path's"
+    sample = [0, 7, 16, batch - 1]
+    ref = oracle.scores_hamming(c["words"], c["qwords"][sample], BIN_DIM)
+    assert_topk_equivalent(idx[sample], val[sample], ref, k)

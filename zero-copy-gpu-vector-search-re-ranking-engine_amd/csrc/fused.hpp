@@ -25,8 +25,9 @@ struct PhaseArgs {
     long long skip = 0;
     long long items = 0;
     int dense = 0;
-    // A sketch phase (int8 MFMA scan only) emits no keys: each of its 2 * workgroups slots keeps
-    // the best exact score of its rows per query, written to EmitArgs::sketch.
+    // A sketch phase (int8 MFMA scan, binary streaming scan) emits no keys: each of its slots (2
+    // per workgroup in the int8 scan, 8 in the binary one) keeps the best exact score of its rows
+    // per query, written to EmitArgs::sketch.
     int sketch = 0;
     int block_rows = 64;
 };
@@ -39,7 +40,7 @@ struct EmitArgs {
     std::uint32_t* seg_count = nullptr;  // [n_wg, batch]
     int seg_log2 = 0;
     float* sketch = nullptr;             // sketch phases: [slots, batch] best score per slot
-    // Rerun of the exact fallback (int8 MFMA scan): only the F = *q_list_count queries
+    // Rerun of the exact fallback (int8 MFMA scan, binary streaming scan): only the F = *q_list_count queries
     // q_list[0..F) are scanned. List entry e of query q = q_list[e] owns the segments
     // seg[(s * F + e) << rerunSegLog2(seg_log2, batch, F)] with counts seg_count[s * F + e], so
     // the F queries share the whole segment buffer of the batch.
@@ -170,6 +171,10 @@ int launchMfmaSplitScan(const ScanArgs& scan, const PhaseArgs& phase, const Emit
 // dim 512 or 1024).
 bool mfmaBinarySupported(const ScanArgs& scan);
 int mfmaBinaryBlockRows(const ScanArgs& scan);
+// Whether the batch runs the streaming kernel (at most 32 queries), the binary scan with sketch
+// and rerun modes; its sketch slots per workgroup.
+bool mfmaBinaryStreams(const ScanArgs& scan);
+int mfmaBinarySketchSlotsPerWorkgroup();
 int launchMfmaBinaryScan(const ScanArgs& scan, const PhaseArgs& phase, const EmitArgs& emit,
                          int workgroups, hipStream_t stream);
 

@@ -384,12 +384,27 @@ constexpr int kStreamWaves = kStreamThreads / kWave;
 // (two 16-row blocks) at a time, the next pair loaded while the current one is multiplied. No
 // tile is shared, so there is no LDS ring and no barrier in the loop, and with the queries out of
 // the registers four wavefronts fit a SIMD, whose loads hide each other's latency. Each B
-// fragment read from LDS feeds four MFMAs (two blocks x two query groups). Wavefront w of
+// fragment read from LDS feeds two MFMAs (the pair's two blocks). Wavefront w of
 // workgroup b takes pairs w * gridDim.x + b, + 16 * gridDim.x, ... of the phase's items (an
 // item's pairs in order), so the pairs spread over the workgroups first.
-template <int kWords, bool kDense>
+//
+// Modes: kStreamThreshold (keys above the threshold to the workgroup's segment), kStreamDense
+// (every key to its fixed slot), kStreamSketch (no keys: per pair of wavefronts the least Hamming
+// distance of each query, as a score, to sketch slot 8 * workgroup + wave / 2) and kStreamRerun
+// (kStreamThreshold over the queries of EmitArgs::q_list, in the list's segment layout; a kernel
+// of its own, so profiles tell the fallback's launches apart).
+constexpr int kStreamThreshold = 0;
+constexpr int kStreamDense = 1;
+constexpr int kStreamSketch = 2;
+constexpr int kStreamRerun = 3;
+constexpr int kStreamSketchSlots = kStreamWaves / 2;  // per workgroup
+
+template <int kWords, int kMode>
 __global__ __launch_bounds__(kStreamThreads)
 void mfmaBinaryStreamKernel(ScanArgs scan, PhaseArgs phase, EmitArgs emit, int q_offset, int q_count) {
+    constexpr bool kDense = kMode == kStreamDense;
+    constexpr bool kSketch = kMode == kStreamSketch;
+    constexpr bool kListed = kMode == kStreamRerun;
     using Tile = BinaryTile<kWords>;
     constexpr int kRows = Tile::kRows;
     constexpr int kRowBytes = Tile::kRowBytes;
@@ -401,6 +416,28 @@ void mfmaBinaryStreamKernel(ScanArgs scan, PhaseArgs phase, EmitArgs emit, int q
 
     __shared__ v4i qlds[kSteps][2][kWave];  // B operand of (step, query group, lane)
     __shared__ std::uint32_t lds_count[kSetQueries];
+    __shared__ int lds_sketch[kSketch ? kStreamWaves : 1][kSetQueries];
+
+    // A rerun scans list entries [q_offset, q_offset + q_count) of q_list, of which
+    // F = *q_list_count exist (uniform over the launch, so a workgroup past them returns at once).
+    int seg_batch = scan.batch;
+    int seg_log2 = emit.seg_log2;
+    if constexpr (kListed) {
+        const int entries = static_cast<int>(__builtin_amdgcn_readfirstlane(*emit.q_list_count));
+        if (entries <= q_offset) {
+            return;
+        }
+        q_count = min(q_count, entries - q_offset);
+        seg_batch = entries;
+        seg_log2 = rerunSegLog2(emit.seg_log2, scan.batch, entries);
+    }
+    // the query of launch-local query `local` (a rerun's list entry q_offset + local)
+    auto queryOf = [&](int local) {
+        if constexpr (kListed) {
+            return static_cast<int>(emit.q_list[q_offset + local]);
+        }
+        return q_offset + local;
+    };
 
     const int tid = threadIdx.x;
     const int lane = tid & (kWave - 1);
@@ -422,7 +459,7 @@ void mfmaBinaryStreamKernel(ScanArgs scan, PhaseArgs phase, EmitArgs emit, int q
         const int qlocal = g * 16 + (l & 15);
         v4i value = {0, 0, 0, 0};
         if (qlocal < q_count) {
-            const std::uint32_t word = qwords[static_cast<std::size_t>(q_offset + qlocal) * kWords +
+            const std::uint32_t word = qwords[static_cast<std::size_t>(queryOf(qlocal)) * kWords +
                                               4 * ((l >> 4) + 4 * (t / 8)) + (t % 8) / 2];
             value = signWord(word, t % 2);
         }
@@ -442,7 +479,7 @@ void mfmaBinaryStreamKernel(ScanArgs scan, PhaseArgs phase, EmitArgs emit, int q
     for (int g = 0; g < 2; ++g) {
         const int qlocal = g * 16 + r16;
         valid_of[g] = qlocal < q_count;
-        const int q = q_offset + min(qlocal, q_count - 1);
+        const int q = queryOf(min(qlocal, q_count - 1));
         q_of[g] = q;
         const std::uint32_t* qrow = qwords + static_cast<std::size_t>(q) * kWords;
         // the four lane groups hold disjoint chunks h + 4 jc of the query
@@ -457,12 +494,13 @@ void mfmaBinaryStreamKernel(ScanArgs scan, PhaseArgs phase, EmitArgs emit, int q
         popq[g] = pop;
         h_limit[g] = kDim + 1;
         row_limit[g] = 0xFFFFFFFFu;
-        if constexpr (!kDense) {
+        if constexpr (!kDense && !kSketch) {
             binaryThreshold<kDim>(emit, q, h_limit[g], row_limit[g]);
         }
         acc_limit[g] = 64 * (valid_of[g] ? h_limit[g] - popq[g] : -(kDim + 1));
     }
     __syncthreads();
+    int best_hd[2] = {kDim + 1, kDim + 1};  // sketch: the lane's least distance per query group
 
     auto emitKeys = [&](const v4i& acc, int g, long long row0, int local0, long long item_) {
         if (!valid_of[g]) {
@@ -486,7 +524,13 @@ void mfmaBinaryStreamKernel(ScanArgs scan, PhaseArgs phase, EmitArgs emit, int q
                 const bool pass = hd < h_limit[g] || (hd == h_limit[g] && r32 < row_limit[g]);
                 if (pass && row < doc_count) {
                     const float score = static_cast<float>(kDim - 2 * hd) / static_cast<float>(kDim);
-                    appendCandidate(emit, lds_count, q, q_offset, scan.batch, makeKey(score, r32));
+                    // to this workgroup's segment of the launch's query g * 16 + r16
+                    const int qlocal = g * 16 + r16;
+                    const std::uint32_t slot = atomicAdd(&lds_count[qlocal], 1u);
+                    if (slot < (1u << seg_log2)) {
+                        emit.seg[((static_cast<std::size_t>(blockIdx.x) * seg_batch + q_offset + qlocal) << seg_log2) +
+                                 slot] = makeKey(score, r32);
+                    }
                 }
             }
         }
@@ -542,7 +586,19 @@ void mfmaBinaryStreamKernel(ScanArgs scan, PhaseArgs phase, EmitArgs emit, int q
         const int pair_row = 32 * static_cast<int>(p32 - it * kPairs);
 #pragma unroll
         for (int b = 0; b < 2; ++b) {
-            if constexpr (kDense) {
+            if constexpr (kSketch) {
+                // the least distance over the lane's rows that exist (rows past the corpus
+                // re-read its last row)
+#pragma unroll
+                for (int g = 0; g < 2; ++g) {
+#pragma unroll
+                    for (int i = 0; i < 4; ++i) {
+                        const long long row = row0 + pair_row + 16 * b + 4 * h + i;
+                        const int hd = (acc[b][g][i] >> 6) + popq[g];
+                        best_hd[g] = row < doc_count ? min(best_hd[g], hd) : best_hd[g];
+                    }
+                }
+            } else if constexpr (kDense) {
                 emitKeys(acc[b][0], 0, row0, pair_row + 16 * b, it);
                 if (two_groups) {
                     emitKeys(acc[b][1], 1, row0, pair_row + 16 * b, it);
@@ -586,10 +642,34 @@ void mfmaBinaryStreamKernel(ScanArgs scan, PhaseArgs phase, EmitArgs emit, int q
         p += stride;
     }
 
+    if constexpr (kSketch) {
+        // the least distance per query over the lane groups h, then over each pair of
+        // wavefronts, written as a score to slot 8 * workgroup + wave / 2
+#pragma unroll
+        for (int g = 0; g < 2; ++g) {
+            best_hd[g] = min(best_hd[g], waveXor(best_hd[g], 16));
+            best_hd[g] = min(best_hd[g], waveXor(best_hd[g], 32));
+        }
+        if (h == 0) {
+            lds_sketch[wave][r16] = best_hd[0];
+            lds_sketch[wave][16 + r16] = best_hd[1];
+        }
+        __syncthreads();
+        for (int i = tid; i < kStreamSketchSlots * q_count; i += kStreamThreads) {
+            const int pair = i / q_count;
+            const int local = i - pair * q_count;
+            const int hd = min(lds_sketch[2 * pair][local], lds_sketch[2 * pair + 1][local]);
+            const float score =
+                hd <= kDim ? static_cast<float>(kDim - 2 * hd) / static_cast<float>(kDim) : -INFINITY;
+            const std::size_t slot = static_cast<std::size_t>(kStreamSketchSlots) * blockIdx.x + pair;
+            emit.sketch[slot * scan.batch + q_offset + local] = score;
+        }
+        return;
+    }
     if constexpr (!kDense) {
         __syncthreads();
         for (int i = tid; i < q_count; i += kStreamThreads) {
-            emit.seg_count[static_cast<std::size_t>(blockIdx.x) * scan.batch + q_offset + i] = lds_count[i];
+            emit.seg_count[static_cast<std::size_t>(blockIdx.x) * seg_batch + q_offset + i] = lds_count[i];
         }
     }
 }
@@ -604,10 +684,20 @@ int launchShape(const ScanArgs& scan, const PhaseArgs& phase, const EmitArgs& em
         if (count <= kSetQueries) {
             // one query set: the streaming kernel
             if (phase.dense) {
-                mfmaBinaryStreamKernel<kWords, true><<<grid, kStreamThreads, 0, stream>>>(scan, phase, emit, q0, count);
+                mfmaBinaryStreamKernel<kWords, kStreamDense>
+                    <<<grid, kStreamThreads, 0, stream>>>(scan, phase, emit, q0, count);
+            } else if (phase.sketch) {
+                mfmaBinaryStreamKernel<kWords, kStreamSketch>
+                    <<<grid, kStreamThreads, 0, stream>>>(scan, phase, emit, q0, count);
+            } else if (emit.q_list != nullptr) {
+                mfmaBinaryStreamKernel<kWords, kStreamRerun>
+                    <<<grid, kStreamThreads, 0, stream>>>(scan, phase, emit, q0, count);
             } else {
-                mfmaBinaryStreamKernel<kWords, false><<<grid, kStreamThreads, 0, stream>>>(scan, phase, emit, q0, count);
+                mfmaBinaryStreamKernel<kWords, kStreamThreshold>
+                    <<<grid, kStreamThreads, 0, stream>>>(scan, phase, emit, q0, count);
             }
+        } else if (phase.sketch || emit.q_list != nullptr) {
+            return setError(ZCGVS_ERR_RUNTIME, "zcgvs: the binary tile scan has no sketch or rerun mode");
         } else if (phase.dense) {
             mfmaBinaryScanKernel<kWords, true><<<grid, kThreads, 0, stream>>>(scan, phase, emit, q0, count);
         } else {
@@ -630,6 +720,10 @@ bool mfmaBinarySupported(const ScanArgs& scan) {
     }
     return scan.dim == 512 || scan.dim == 1024;
 }
+
+bool mfmaBinaryStreams(const ScanArgs& scan) { return scan.batch <= kSetQueries; }
+
+int mfmaBinarySketchSlotsPerWorkgroup() { return kStreamSketchSlots; }
 
 int mfmaBinaryBlockRows(const ScanArgs& scan) {
     return scan.dim == 512 ? BinaryTile<16>::kRows : BinaryTile<32>::kRows;

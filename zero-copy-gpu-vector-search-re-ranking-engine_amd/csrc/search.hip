@@ -80,10 +80,10 @@ struct Plan {
     bool direct_scales = false;  // MFMA path without a mask: only the tail tile's scales are copied
     bool lex_sorted = false;     // hybrid with postings ascending by document: sliced BM25 stage
     bool recover = false;        // threshold phases ran: the exact fallback follows them
-    // int8 MFMA scan over a large corpus: a sketch phase and one speculative full scan instead
-    // of the threshold phases (see makePlan)
+    // int8 MFMA scan or binary streaming scan over a large corpus: a sketch phase and one
+    // speculative full scan instead of the threshold phases (see makePlan)
     bool sketch = false;
-    int sketch_slots = 0;        // sketch slots (2 per workgroup)
+    int sketch_slots = 0;        // sketch slots (2 per workgroup int8, 8 binary)
     int sketch_rank = 0;         // tau = the sketch_rank-th best slot score
     // the scan kernel reruns the flagged queries over the whole corpus before the fallback
     bool rerun = false;
@@ -457,27 +457,31 @@ Plan makePlan(const zcgvs_search_desc& d) {
     plan.full.skip = 0;
     plan.full.items = blocks;
     plan.full.block_rows = plan.block_rows;
+    // (the binary scan runs the sketch and the rerun in its streaming kernel, up to 32 queries)
+    const bool binary_sketch = plan.use_mfma_binary && mfmaBinaryStreams(probe);
     plan.rerun = plan.use_mfma;
     // Segment capacity: 4x the expected candidates per (segment, query) of the widest phase.
     long long expected = (static_cast<long long>(plan.width) * growth) / plan.segments;
 
-    // Sketch plan (int8 MFMA scan, when the threshold phases would be three or more): a sketch
-    // phase over every 32nd block keeps per slot (a row half of a workgroup's lanes) the best
-    // exact score of each query; the j-th best of those 2 * workgroups scores is the threshold
+    // Sketch plan (int8 MFMA scan and binary streaming scan, when the threshold phases would be
+    // three or more): a sketch phase over every 32nd block keeps per slot (a row half of a
+    // workgroup's lanes in the int8 scan, a pair of wavefronts in the binary one) the best exact
+    // score of each query; the j-th best of those slot scores is the threshold
     // of ONE scan over the whole corpus. With f = sketch rows / corpus rows, the number of
     // corpus rows at or above the sketch's j-th best score is about Gamma(j) / f, so
     // j = width f + 5.5 sqrt(width f) + 2 (15 at f = 1/32, width = 100) leaves fewer than width
     // such rows with probability about 1e-6 per query (Poisson tail), while the scan emits about
     // j / f candidates per query. The merge flags a query for the fallback when fewer than width
     // candidates reached it; the k-th best slot score is its guaranteed threshold then.
-    const int slots = 2 * plan.workgroups;
+    const int slots = (plan.use_mfma ? 2 : mfmaBinarySketchSlotsPerWorkgroup()) * plan.workgroups;
     // (A smaller corpus samples every 16th, 8th or 4th block, so every workgroup still sees at
     // least 4 sampled blocks; below that the threshold phases stay.)
     long long sketch_stride = 32;
     while (sketch_stride > 4 && phaseItems(blocks, sketch_stride, 0) < 4LL * plan.workgroups) {
         sketch_stride /= 2;
     }
-    if (plan.use_mfma && plan.phases.size() >= 3 && slots <= kMaxSketchSlots && slots >= plan.width &&
+    if ((plan.use_mfma || binary_sketch) && plan.phases.size() >= 3 && slots <= kMaxSketchSlots &&
+        slots >= plan.width &&
         phaseItems(blocks, sketch_stride, 0) >= 4LL * plan.workgroups) {
         PhaseArgs sketch;
         sketch.stride = sketch_stride;
@@ -489,6 +493,7 @@ Plan makePlan(const zcgvs_search_desc& d) {
         const double kf = plan.width * f;
         const int j = static_cast<int>(std::ceil(kf + 5.5 * std::sqrt(kf) + 2.0));
         plan.sketch = true;
+        plan.rerun = true;
         plan.sketch_slots = slots;
         plan.sketch_rank = std::max(1, std::min({j, plan.width, slots}));
         if ((d.flags & ZCGVS_SEARCH_TEST_HIGH_THRESHOLD) != 0) {
@@ -998,7 +1003,9 @@ int searchTopk(const zcgvs_search_desc* desc, void* d_workspace, std::size_t wor
             again.seg_log2 = plan.rerun_seg_log2;
             again.q_list = recovery.flag_list;
             again.q_list_count = recovery.flag_count;
-            status = launchMfmaScan(scanArgsOf(d, plan, ws), plan.full, again, plan.workgroups, s);
+            const ScanArgs scan = scanArgsOf(d, plan, ws);
+            status = plan.use_mfma ? launchMfmaScan(scan, plan.full, again, plan.workgroups, s)
+                                   : launchMfmaBinaryScan(scan, plan.full, again, plan.workgroups, s);
             if (status != ZCGVS_OK) {
                 return status;
             }
