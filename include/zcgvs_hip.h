@@ -372,6 +372,17 @@ int zcgvs_search_phase_rows(const zcgvs_search_desc* desc, long long* rows, int 
 int zcgvs_search_overflow_flags(const zcgvs_search_desc* desc, void* d_workspace,
                                 uint32_t** d_flags);
 
+/* Device addresses, inside a workspace laid out for `desc`, of a sketch-planned search's sketch
+ * state, valid after the stream has completed the search: the slot scores (*slots x batch
+ * float32, slot-major: the best score of each query over the slot's rows, -inf for a slot that
+ * saw none) and two [batch] threshold keys (a key is kept when it is at least the threshold):
+ * the speculative one, ordered32(the *rank-th best slot score) << 32 (for a flagged query the
+ * merge replaces it by its rerun's threshold), and the certain one, of the *width-th best slot
+ * score. A search that is not sketch-planned sets *slots and *rank to 0 and the addresses to
+ * null. For monitoring and tests; no reference counterpart. */
+int zcgvs_search_sketch_state(const zcgvs_search_desc* desc, void* d_workspace, float** d_slot_scores,
+                              int* slots, int* rank, int* width, uint64_t** d_tau, uint64_t** d_tau_safe);
+
 /* ------------------------------------------------------------------------------------------
  * Synthetic data on the device (benchmarks and large parity runs). Row r of a matrix generated
  * with `seed` depends only on (seed, r): a counter-based splitmix64 stream, Box-Muller in

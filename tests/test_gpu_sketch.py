@@ -57,6 +57,46 @@ def _exact_scores(c, idx, val, batch, mask=None):
         assert np.array_equal(val[b], exact), f"query {b}: scores differ from the oracle's"
 
 
+def _ordered_keys(scores):
+    """ordered32(score) << 32 as the kernels key a score (-0.0 as +0.0; -inf, an empty slot, as 0)."""
+    scores = np.asarray(scores, dtype=np.float32)
+    bits = np.where(scores == 0, np.float32(0), scores).view(np.uint32).astype(np.uint64)
+    ordered = np.where(bits & 0x80000000, ~bits & 0xFFFFFFFF, bits | 0x80000000)
+    return np.where(np.isneginf(scores), 0, ordered).astype(np.uint64) << np.uint64(32)
+
+
+def _search_with_state(capi, desc):
+    size = capi.search_workspace_bytes(desc)
+    workspace = capi.DeviceArray(size, np.uint8)
+    idx = capi.DeviceArray((desc.batch, desc.k), np.int32)
+    val = capi.DeviceArray((desc.batch, desc.k), np.float32)
+    capi.search_topk(desc, workspace, size, idx, val)
+    capi.synchronize()
+    flags = np.empty(desc.batch, dtype=np.uint32)
+    capi.call("zcgvs_memcpy_d2h", flags.ctypes.data, capi.search_overflow_flags(desc, workspace), flags.nbytes, None)
+    state = capi.search_sketch_state(desc, workspace)
+    return idx.to_host(), val.to_host(), flags, state
+
+
+def _check_sketch(state, flags, sampled_scores, queries):
+    """The thresholds are the rank-th and width-th best slot keys (radix select against a sort),
+    and the slots are maxima over disjoint sets of the sampled rows: the i-th best slot score is at
+    most the i-th best sampled row score, with equality for i = 1 (sampled_scores: the oracle's
+    scores of every sampled row, [len(queries), rows])."""
+    keys = _ordered_keys(state["slots"])
+    ranked = np.sort(keys, axis=0)[::-1]
+    rank, width = state["rank"], state["width"]
+    assert 1 <= rank <= width <= keys.shape[0]
+    spec = ~flags.astype(bool)
+    assert np.array_equal(state["tau"][spec], ranked[rank - 1][spec]), "speculative thresholds differ"
+    assert np.array_equal(state["tau_safe"], ranked[width - 1]), "certain thresholds differ"
+    for i, q in enumerate(queries):
+        slot_best = np.sort(state["slots"][:, q])[::-1]
+        rows_best = np.sort(sampled_scores[i])[::-1][:slot_best.size]
+        assert slot_best[0] == rows_best[0], f"query {q}: the best slot is not the best sampled row"
+        assert np.all(slot_best[:rows_best.size] <= rows_best), f"query {q}: a slot beats the sampled rows"
+
+
 def _sampled(c, idx, val, sample, k, mask=None):
     qcodes, qscales = oracle.quantize_rows_i8(c["queries"][sample])
     ref = oracle.scores_i8i8(c["codes"], c["scales"], qcodes, qscales, mask)
@@ -78,6 +118,19 @@ def test_speculative_scan_is_exact(corpus, baseline):
     assert not flags.any(), "a random corpus should not need the fallback"
     _exact_scores(corpus, idx, val, BATCH)
     _sampled(corpus, idx, val, [0, 1, 97, 128, 200, 255], K)
+
+
+def test_sketch_thresholds(gpu, corpus, baseline):
+    # every 8th 64-row block is sampled at 1M rows
+    capi = gpu
+    idx, val, flags, state = _search_with_state(capi, _desc(capi, corpus))
+    assert state is not None and state["slots"].shape[1] == BATCH
+    assert np.array_equal(idx, baseline[0]) and np.array_equal(val, baseline[1])
+    rows = np.concatenate([np.arange(b * 64, min(b * 64 + 64, N)) for b in range(0, (N + 63) // 64, 8)])
+    queries = [0, 101, 255]
+    qcodes, qscales = oracle.quantize_rows_i8(corpus["queries"][queries])
+    sampled = oracle.scores_i8i8(corpus["codes"][rows], corpus["scales"][rows], qcodes, qscales)
+    _check_sketch(state, flags, sampled, queries)
 
 
 @pytest.mark.parametrize("flag", ["high", "tiny", "force"])
@@ -156,3 +209,17 @@ def test_binary_sketch_plan(gpu, binary_corpus, batch, k):
     sample = [0, 7, 16, batch - 1]
     ref = oracle.scores_hamming(c["words"], c["qwords"][sample], BIN_DIM)
     assert_topk_equivalent(idx[sample], val[sample], ref, k)
+
+
+def test_binary_sketch_thresholds(gpu, binary_corpus):
+    # every 4th 384-row block is sampled at 2M rows of 1024 bits
+    capi = gpu
+    c = binary_corpus
+    for batch, k in ((32, 100), (20, 1000)):
+        idx, val, flags, state = _search_with_state(capi, _binary_desc(capi, c, batch, k))
+        assert state is not None and state["slots"].shape[1] == batch
+        rows = np.concatenate([np.arange(b * 384, min(b * 384 + 384, BIN_N))
+                               for b in range(0, (BIN_N + 383) // 384, 4)])
+        queries = [0, batch - 1]
+        sampled = oracle.scores_hamming(c["words"][rows], c["qwords"][queries], BIN_DIM)
+        _check_sketch(state, flags, sampled, queries)

@@ -112,6 +112,9 @@ _SIGNATURES = {
     "zcgvs_search_topk_noalloc": (_i32, [ctypes.POINTER(SearchDesc), _vp, _vp, _vp]),
     "zcgvs_static_scratch_bytes": (_sz, []),
     "zcgvs_search_overflow_flags": (_i32, [ctypes.POINTER(SearchDesc), _vp, ctypes.POINTER(_vp)]),
+    "zcgvs_search_sketch_state": (_i32, [ctypes.POINTER(SearchDesc), _vp, ctypes.POINTER(_vp), ctypes.POINTER(_i32),
+                                         ctypes.POINTER(_i32), ctypes.POINTER(_i32), ctypes.POINTER(_vp),
+                                         ctypes.POINTER(_vp)]),
     "zcgvs_search_topk_profiled": (_i32, [ctypes.POINTER(SearchDesc), _vp, _sz, _vp, _vp, _vp,
                                           ctypes.POINTER(_vp), _i32, ctypes.POINTER(_i32)]),
     "zcgvs_search_phase_rows": (_i32, [ctypes.POINTER(SearchDesc), ctypes.POINTER(_i64), _i32,
@@ -460,6 +463,24 @@ def search_overflow_flags(desc: SearchDesc, workspace) -> int:
     address = _vp()
     call("zcgvs_search_overflow_flags", ctypes.byref(desc), ptr(workspace), ctypes.byref(address))
     return int(address.value or 0)
+
+
+def search_sketch_state(desc: SearchDesc, workspace) -> dict | None:
+    """A completed sketch-planned search's slot scores [slots, batch] and thresholds (host copies),
+    or None when the search is not sketch-planned."""
+    scores, tau, tau_safe = _vp(), _vp(), _vp()
+    slots, rank, width = _i32(0), _i32(0), _i32(0)
+    call("zcgvs_search_sketch_state", ctypes.byref(desc), ptr(workspace), ctypes.byref(scores), ctypes.byref(slots),
+         ctypes.byref(rank), ctypes.byref(width), ctypes.byref(tau), ctypes.byref(tau_safe))
+    if slots.value == 0:
+        return None
+    out = dict(slots=np.empty((slots.value, desc.batch), dtype=np.float32), rank=rank.value, width=width.value,
+               tau=np.empty(desc.batch, dtype=np.uint64), tau_safe=np.empty(desc.batch, dtype=np.uint64))
+    synchronize()
+    for name, address in (("slots", scores), ("tau", tau), ("tau_safe", tau_safe)):
+        call("zcgvs_memcpy_d2h", out[name].ctypes.data, address.value, out[name].nbytes, None)
+    synchronize()
+    return out
 
 
 def search(desc: SearchDesc, stream=None):

@@ -723,6 +723,26 @@ int zcgvs_search_overflow_flags(const zcgvs_search_desc* desc, void* d_workspace
     return clearError();
 }
 
+int zcgvs_search_sketch_state(const zcgvs_search_desc* desc, void* d_workspace, float** d_slot_scores, int* slots,
+                              int* rank, int* width, std::uint64_t** d_tau, std::uint64_t** d_tau_safe) {
+    if (desc == nullptr || d_workspace == nullptr || d_slot_scores == nullptr || slots == nullptr ||
+        rank == nullptr || width == nullptr || d_tau == nullptr || d_tau_safe == nullptr) {
+        return setError(ZCGVS_ERR_INVALID_ARGUMENT, "zcgvs: null argument");
+    }
+    const Plan plan = makePlan(*desc);
+    if (plan.status != ZCGVS_OK) {
+        return setError(plan.status, plan.error);
+    }
+    std::uint8_t* ws = static_cast<std::uint8_t*>(d_workspace);
+    *width = plan.width;
+    *slots = plan.sketch ? plan.sketch_slots : 0;
+    *rank = plan.sketch ? plan.sketch_rank : 0;
+    *d_slot_scores = plan.sketch ? reinterpret_cast<float*>(ws + plan.sketchbuf) : nullptr;
+    *d_tau = plan.sketch ? reinterpret_cast<std::uint64_t*>(ws + plan.tau) : nullptr;
+    *d_tau_safe = plan.sketch ? reinterpret_cast<std::uint64_t*>(ws + plan.tau_safe) : nullptr;
+    return clearError();
+}
+
 namespace {
 
 int searchTopk(const zcgvs_search_desc* desc, void* d_workspace, std::size_t workspace_bytes,

@@ -686,79 +686,98 @@ __global__ __launch_bounds__(kSortedMergeThreads) void sortedSegmentMergeKernel(
 
 // ---- thresholds from a sketch phase (one block per query) ----------------------------------------
 
-constexpr int kSketchThreads = 64;  // one wavefront per query
+constexpr int kSketchThreads = 256;
+constexpr int kSketchPerThread = kMaxSketchSlots / kSketchThreads;  // slot scores per thread
+constexpr int kSketchBins = 2048;                                    // 11-bit digits
+constexpr int kSketchBinsPerThread = kSketchBins / kSketchThreads;
 
-// The slot scores sorted in registers: lane l holds elements l * kPerLane + r (r < kPerLane) of
-// a bitonic sort into descending order, for up to 64 * kPerLane slots; partners in the same lane
-// are compare-exchanged in registers, partners in other lanes (stride >= kPerLane) through
-// lane shuffles, so the sort needs no barrier and no LDS round trip.
-template <int kPerLane>
+// The j-th and k-th best of a query's slot scores: a radix select over the scores' ordered bits in
+// three passes (digits of bits 31..21, 20..10 and 9..0), both ranks in the same passes. A pass
+// counts, per rank, the scores whose higher digits equal that rank's prefix so far into an LDS
+// histogram (rank j's count in the low 16 bits of a bin, rank k's in the high 16 bits; at most
+// 2048 scores, so neither half carries), then a block scan over the bins in descending digit order
+// finds the bin that holds the rank, which fixes the digit and the rank left within the bin.
 __global__ __launch_bounds__(kSketchThreads) void sketchThresholdKernel(const float* __restrict__ sketch, int slots,
-                                                                         int batch, int j, int k,
-                                                                         std::uint64_t* __restrict__ tau,
-                                                                         std::uint64_t* __restrict__ tau_safe,
-                                                                         std::uint32_t* __restrict__ flag_count) {
-    constexpr int kN = kSketchThreads * kPerLane;
+                                                                        int batch, int j, int k,
+                                                                        std::uint64_t* __restrict__ tau,
+                                                                        std::uint64_t* __restrict__ tau_safe,
+                                                                        std::uint32_t* __restrict__ flag_count) {
+    __shared__ std::uint32_t hist[kSketchBins];
+    __shared__ std::uint32_t wave_sums[kSketchThreads / kWave];
+    __shared__ std::uint32_t pick[2][2];  // per rank: the digit, the scores in higher bins
     const int q = blockIdx.x;
-    const int l = threadIdx.x;
+    const int t = threadIdx.x;
     // the slot scores' ordered bits; an empty slot (-inf: it saw no row) and the padding are 0
-    std::uint32_t v[kPerLane];
+    std::uint32_t v[kSketchPerThread];
 #pragma unroll
-    for (int r = 0; r < kPerLane; ++r) {
-        const int s = l * kPerLane + r;
+    for (int r = 0; r < kSketchPerThread; ++r) {
+        const int s = r * kSketchThreads + t;
         const float x = s < slots ? sketch[static_cast<std::size_t>(s) * batch + q] : -INFINITY;
         v[r] = x > -INFINITY ? orderedBits(x) : 0u;
     }
-    if (q == 0 && l == 0) {
+    if (q == 0 && t == 0) {
         *flag_count = 0u;
     }
+    std::uint32_t prefix[2] = {0u, 0u};
+    std::uint32_t rank[2] = {static_cast<std::uint32_t>(j), static_cast<std::uint32_t>(k)};
+    constexpr int kShift[3] = {21, 10, 0};
+    constexpr int kBits[3] = {11, 11, 10};
 #pragma unroll
-    for (int size = 2; size <= kN; size <<= 1) {
+    for (int p = 0; p < 3; ++p) {
+        const int shift = kShift[p];
+        const int high = shift + kBits[p];  // the digits above this one start here (32: none)
+        const std::uint32_t digit_mask = (1u << kBits[p]) - 1u;
 #pragma unroll
-        for (int stride = size >> 1; stride > 0; stride >>= 1) {
-            if (stride < kPerLane) {
+        for (int b = 0; b < kSketchBinsPerThread; ++b) {
+            hist[b * kSketchThreads + t] = 0u;
+        }
+        __syncthreads();
+        // a score matches both ranks' prefixes only when they are equal, so one add per score
 #pragma unroll
-                for (int r = 0; r < kPerLane; ++r) {
-                    if ((r & stride) == 0) {
-                        const bool descending = ((l * kPerLane + r) & size) == 0;
-                        const std::uint32_t a = v[r];
-                        const std::uint32_t b = v[r + stride];
-                        const bool swap = (a < b) == descending;
-                        v[r] = swap ? b : a;
-                        v[r + stride] = swap ? a : b;
-                    }
-                }
-            } else {
-                const int lanes = stride / kPerLane;
-                const bool low = (l & lanes) == 0;
+        for (int r = 0; r < kSketchPerThread; ++r) {
+            const std::uint32_t upper = high < 32 ? v[r] >> (high & 31) : 0u;
+            const std::uint32_t add = (upper == (high < 32 ? prefix[0] >> (high & 31) : 0u) ? 1u : 0u) +
+                                      (upper == (high < 32 ? prefix[1] >> (high & 31) : 0u) ? 0x10000u : 0u);
+            if (add != 0u) {
+                atomicAdd(&hist[(v[r] >> shift) & digit_mask], add);
+            }
+        }
+        __syncthreads();
+        // thread t takes the bins kSketchBins - 1 - 8t - b (b < 8): all bins in descending order
+        std::uint32_t own[kSketchBinsPerThread];
+        std::uint32_t sum = 0u;
 #pragma unroll
-                for (int r = 0; r < kPerLane; ++r) {
-                    const std::uint32_t other = static_cast<std::uint32_t>(__shfl_xor(static_cast<int>(v[r]), lanes, kWave));
-                    const bool descending = ((l * kPerLane + r) & size) == 0;
-                    const bool keep_max = low == descending;
-                    v[r] = keep_max ? max(v[r], other) : min(v[r], other);
+        for (int b = 0; b < kSketchBinsPerThread; ++b) {
+            own[b] = hist[kSketchBins - 1 - kSketchBinsPerThread * t - b];
+            sum += own[b];
+        }
+        std::uint32_t total;
+        std::uint32_t running = blockInclusiveSum<kSketchThreads>(sum, wave_sums, &total) - sum;
+#pragma unroll
+        for (int b = 0; b < kSketchBinsPerThread; ++b) {
+            const std::uint32_t next = running + own[b];
+#pragma unroll
+            for (int i = 0; i < 2; ++i) {
+                const std::uint32_t above = (running >> (16 * i)) & 0xFFFFu;
+                const std::uint32_t through = (next >> (16 * i)) & 0xFFFFu;
+                if (above < rank[i] && through >= rank[i]) {
+                    pick[i][0] = static_cast<std::uint32_t>(kSketchBins - 1 - kSketchBinsPerThread * t - b);
+                    pick[i][1] = above;
                 }
             }
+            running = next;
+        }
+        __syncthreads();
+#pragma unroll
+        for (int i = 0; i < 2; ++i) {
+            prefix[i] |= pick[i][0] << shift;
+            rank[i] -= pick[i][1];
         }
     }
     // every score >= the j-th (k-th) best slot score; 0 when that slot is empty or missing
-#pragma unroll
-    for (int r = 0; r < kPerLane; ++r) {
-        const int e = l * kPerLane + r;
-        if (e == j - 1) {
-            tau[q] = j <= slots ? static_cast<std::uint64_t>(v[r]) << 32 : 0ull;
-        }
-        if (e == k - 1) {
-            tau_safe[q] = k <= slots ? static_cast<std::uint64_t>(v[r]) << 32 : 0ull;
-        }
-    }
-    if (l == 0) {
-        if (j > kN) {
-            tau[q] = 0ull;
-        }
-        if (k > kN) {
-            tau_safe[q] = 0ull;
-        }
+    if (t == 0) {
+        tau[q] = j <= slots ? static_cast<std::uint64_t>(prefix[0]) << 32 : 0ull;
+        tau_safe[q] = k <= slots ? static_cast<std::uint64_t>(prefix[1]) << 32 : 0ull;
     }
 }
 
@@ -790,16 +809,8 @@ int launchSketchThreshold(const float* sketch, int slots, int batch, int j, int 
     if (slots < 1 || slots > kMaxSketchSlots || j < 1 || k < 1) {
         return setError(ZCGVS_ERR_RUNTIME, "zcgvs select: sketch threshold shape out of range");
     }
-    if (slots <= 64 * 8) {
-        sketchThresholdKernel<8><<<batch, kSketchThreads, 0, stream>>>(sketch, slots, batch, j, k, tau, tau_safe,
-                                                                      flag_count);
-    } else if (slots <= 64 * 16) {
-        sketchThresholdKernel<16><<<batch, kSketchThreads, 0, stream>>>(sketch, slots, batch, j, k, tau, tau_safe,
-                                                                       flag_count);
-    } else {
-        sketchThresholdKernel<32><<<batch, kSketchThreads, 0, stream>>>(sketch, slots, batch, j, k, tau, tau_safe,
-                                                                       flag_count);
-    }
+    sketchThresholdKernel<<<batch, kSketchThreads, 0, stream>>>(sketch, slots, batch, j, k, tau, tau_safe,
+                                                                  flag_count);
     ZCGVS_LAUNCH_CHECK("sketch threshold");
     return ZCGVS_OK;
 }
