@@ -17,6 +17,7 @@
 #pragma once
 
 #include "common.hpp"
+#include "select.hpp"
 
 namespace zcgvs_hip {
 
@@ -234,5 +235,12 @@ struct RecoverArgs {
 };
 bool recoverSupported(const ScanArgs& scan);
 int launchRecover(const ScanArgs& scan, const RecoverArgs& args, hipStream_t stream);
+// The final merge of a phased search fused with its exact fallback (not the list mode): one launch
+// of `batch` blocks, each merging its query as launchSelectMerge does (no threshold output) and,
+// when the merge flags the query or args.force is set, recomputing its selection as the last
+// resort of launchRecover does. args.width must equal k.
+int launchMergeRecover(const MergeInputs& in, int k, int batch, std::uint64_t* out_keys, std::uint32_t* overflow,
+                       int* out_index, float* out_score, const ScanArgs& scan, const RecoverArgs& args,
+                       hipStream_t stream);
 
 }  // namespace zcgvs_hip

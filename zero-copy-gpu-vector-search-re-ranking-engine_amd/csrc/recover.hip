@@ -24,6 +24,7 @@
 
 #include "common.hpp"
 #include "fused.hpp"
+#include "merge.hpp"
 #include "scan_core.hpp"
 #include "select.hpp"
 
@@ -148,38 +149,32 @@ __device__ bool selectFromRerun(const RecoverArgs& args, int q, int entry, int l
     return true;
 }
 
-template <int kKind, int L>
-__global__ __launch_bounds__(kRecoverThreads) void recoverKernel(ScanArgs scan, RecoverArgs args,
-                                                                 int chunks) {
-    extern __shared__ std::uint32_t lds_query[];
-    __shared__ std::uint32_t lds_hist[kSelectBins];
-    __shared__ std::uint32_t lds_scan[kRecoverThreads / kWave];
-    __shared__ std::uint64_t lds_keys[kMaxK];
-    __shared__ SelectState lds_state;
-    __shared__ std::uint32_t lds_taken_equal;
+// LDS of the last resort's recomputation: recoverKernel's own, or in mergeRecoverKernel the
+// merge's, free once the merge is over.
+struct RecomputeLds {
+    std::uint32_t* query;  // the staged query: chunks * stagedWordsPerChunk(kind) words
+    std::uint32_t* hist;   // kSelectBins
+    std::uint32_t* scan;   // kRecoverThreads / kWave
+    std::uint64_t* keys;   // kMaxK
+    SelectState* state;
+    std::uint32_t* taken_equal;
+};
 
-    int q = blockIdx.x;
-    int entry = 0;
-    int listed = 0;
-    if (args.force) {
-        // every query
-    } else if (args.flag_list != nullptr) {
-        listed = static_cast<int>(*args.flag_count);
-        entry = blockIdx.x;
-        if (entry >= listed) {
-            return;
-        }
-        q = static_cast<int>(args.flag_list[entry]);
-    } else if (args.flags[q] == 0u) {
-        return;
-    }
+// The last resort for query q, by the whole block: the top-`width` over recomputed scores of the
+// whole corpus, written to the outputs.
+template <int kKind, int L>
+__device__ __forceinline__ void recomputeQuery(const ScanArgs& scan, const RecoverArgs& args, int chunks, int q,
+                                               const RecomputeLds& lds) {
+    std::uint32_t* lds_query = lds.query;
+    std::uint32_t* lds_hist = lds.hist;
+    std::uint32_t* lds_scan = lds.scan;
+    std::uint64_t* lds_keys = lds.keys;
+    SelectState& lds_state = *lds.state;
+    std::uint32_t& lds_taken_equal = *lds.taken_equal;
     const int t = threadIdx.x;
     const int dim = scan.dim;
     const int width = args.width;
     const long long n = scan.doc_count;
-    if (args.seg != nullptr && !args.force && selectFromRerun(args, q, entry, listed, scan.batch)) {
-        return;
-    }
     const int words = chunks * stagedWordsPerChunk(kKind);
 
     // ---- the query, staged as the VALU scan stages it ----
@@ -395,6 +390,59 @@ __global__ __launch_bounds__(kRecoverThreads) void recoverKernel(ScanArgs scan, 
     }
 }
 
+template <int kKind, int L>
+__global__ __launch_bounds__(kRecoverThreads) void recoverKernel(ScanArgs scan, RecoverArgs args,
+                                                                 int chunks) {
+    extern __shared__ std::uint32_t lds_query[];
+    __shared__ std::uint32_t lds_hist[kSelectBins];
+    __shared__ std::uint32_t lds_scan[kRecoverThreads / kWave];
+    __shared__ std::uint64_t lds_keys[kMaxK];
+    __shared__ SelectState lds_state;
+    __shared__ std::uint32_t lds_taken_equal;
+
+    int q = blockIdx.x;
+    int entry = 0;
+    int listed = 0;
+    if (args.force) {
+        // every query
+    } else if (args.flag_list != nullptr) {
+        listed = static_cast<int>(*args.flag_count);
+        entry = blockIdx.x;
+        if (entry >= listed) {
+            return;
+        }
+        q = static_cast<int>(args.flag_list[entry]);
+    } else if (args.flags[q] == 0u) {
+        return;
+    }
+    if (args.seg != nullptr && !args.force && selectFromRerun(args, q, entry, listed, scan.batch)) {
+        return;
+    }
+    recomputeQuery<kKind, L>(scan, args, chunks, q,
+                             RecomputeLds{lds_query, lds_hist, lds_scan, lds_keys, &lds_state, &lds_taken_equal});
+}
+
+// The final merge of a phased search and its exact fallback in one launch: block q merges query
+// q's candidates (merge.hpp) and, when that merge flags the query (or with `force`), recomputes
+// its selection in the merge's LDS. No separate fallback launch runs for a search without flags.
+template <int kKind, int L>
+__global__ __launch_bounds__(kRecoverThreads) void mergeRecoverKernel(MergeInputs in, int k, int batch,
+                                                                      std::uint64_t* __restrict__ out_keys,
+                                                                      std::uint32_t* __restrict__ overflow,
+                                                                      int* __restrict__ out_index,
+                                                                      float* __restrict__ out_score, ScanArgs scan,
+                                                                      RecoverArgs args, int chunks) {
+    __shared__ MergeLds lds;
+    const int q = static_cast<int>(blockIdx.x);
+    const bool flagged = mergeQuery(in, k, batch, out_keys, nullptr, overflow, out_index, out_score, q, lds);
+    if (!flagged && !args.force) {
+        return;  // uniform
+    }
+    recomputeQuery<kKind, L>(scan, args, chunks, q,
+                             RecomputeLds{reinterpret_cast<std::uint32_t*>(lds.cand), lds.hist, lds.scan, lds.keys,
+                                          &lds.state, &lds.valid});
+}
+
 int kindOf(const ScanArgs& scan) {
     if (scan.dtype == ZCGVS_DTYPE_I8 && scan.row_scales != nullptr) {
         return kKindI8I8;
@@ -413,6 +461,33 @@ int launchKind(int lanes, std::size_t shared, const ScanArgs& scan, const Recove
         default: recoverKernel<kKind, 64><<<grid, kRecoverThreads, shared, stream>>>(scan, args, chunks); break;
     }
     ZCGVS_LAUNCH_CHECK("exact recovery");
+    return ZCGVS_OK;
+}
+
+template <int kKind>
+int launchMergeKind(int lanes, const MergeInputs& in, int k, int batch, std::uint64_t* out_keys,
+                    std::uint32_t* overflow, int* out_index, float* out_score, const ScanArgs& scan,
+                    const RecoverArgs& args, int chunks, hipStream_t stream) {
+    const dim3 grid(static_cast<unsigned>(batch));
+    switch (lanes) {
+        case 8:
+            mergeRecoverKernel<kKind, 8><<<grid, kRecoverThreads, 0, stream>>>(in, k, batch, out_keys, overflow,
+                                                                               out_index, out_score, scan, args, chunks);
+            break;
+        case 16:
+            mergeRecoverKernel<kKind, 16><<<grid, kRecoverThreads, 0, stream>>>(in, k, batch, out_keys, overflow,
+                                                                                out_index, out_score, scan, args, chunks);
+            break;
+        case 32:
+            mergeRecoverKernel<kKind, 32><<<grid, kRecoverThreads, 0, stream>>>(in, k, batch, out_keys, overflow,
+                                                                                out_index, out_score, scan, args, chunks);
+            break;
+        default:
+            mergeRecoverKernel<kKind, 64><<<grid, kRecoverThreads, 0, stream>>>(in, k, batch, out_keys, overflow,
+                                                                                out_index, out_score, scan, args, chunks);
+            break;
+    }
+    ZCGVS_LAUNCH_CHECK("merge and exact recovery");
     return ZCGVS_OK;
 }
 
@@ -446,6 +521,46 @@ int launchRecover(const ScanArgs& scan, const RecoverArgs& args, hipStream_t str
         case ZCGVS_DTYPE_BINARY: return launchKind<ZCGVS_DTYPE_BINARY>(lanes, shared, scan, args, chunks, stream);
         case kKindI8I8: return launchKind<kKindI8I8>(lanes, shared, scan, args, chunks, stream);
         default: return launchKind<ZCGVS_DTYPE_F32>(lanes, shared, scan, args, chunks, stream);
+    }
+}
+
+}  // namespace zcgvs_hip
+
+namespace zcgvs_hip {
+
+int launchMergeRecover(const MergeInputs& in, int k, int batch, std::uint64_t* out_keys, std::uint32_t* overflow,
+                       int* out_index, float* out_score, const ScanArgs& scan, const RecoverArgs& args,
+                       hipStream_t stream) {
+    if (args.width != k || k <= 0 || k > kMaxK || batch != scan.batch || batch <= 0 || in.n_seg > kMaxSegments ||
+        args.flag_list != nullptr || args.seg != nullptr) {
+        return setError(ZCGVS_ERR_RUNTIME, "zcgvs merge and recovery: arguments out of range");
+    }
+    if (!recoverSupported(scan)) {
+        return setError(ZCGVS_ERR_RUNTIME, "zcgvs recovery: row layout not supported");
+    }
+    const int chunks = static_cast<int>(rowBytes(scan.dtype, scan.dim) / 16);
+    const int lanes = lanesPerRow(chunks, kRecoverChunksPerLane, kRecoverMinLanes);
+    const int kind = kindOf(scan);
+    // the staged query goes to the merge's candidate LDS
+    if (static_cast<std::size_t>(chunks) * stagedWordsPerChunk(kind) * 4 > sizeof(MergeLds::cand)) {
+        return setError(ZCGVS_ERR_RUNTIME, "zcgvs merge and recovery: query too large for the merge's LDS");
+    }
+    switch (kind) {
+        case ZCGVS_DTYPE_F16:
+            return launchMergeKind<ZCGVS_DTYPE_F16>(lanes, in, k, batch, out_keys, overflow, out_index, out_score, scan,
+                                                    args, chunks, stream);
+        case ZCGVS_DTYPE_I8:
+            return launchMergeKind<ZCGVS_DTYPE_I8>(lanes, in, k, batch, out_keys, overflow, out_index, out_score, scan,
+                                                   args, chunks, stream);
+        case ZCGVS_DTYPE_BINARY:
+            return launchMergeKind<ZCGVS_DTYPE_BINARY>(lanes, in, k, batch, out_keys, overflow, out_index, out_score,
+                                                       scan, args, chunks, stream);
+        case kKindI8I8:
+            return launchMergeKind<kKindI8I8>(lanes, in, k, batch, out_keys, overflow, out_index, out_score, scan,
+                                              args, chunks, stream);
+        default:
+            return launchMergeKind<ZCGVS_DTYPE_F32>(lanes, in, k, batch, out_keys, overflow, out_index, out_score,
+                                                    scan, args, chunks, stream);
     }
 }
 

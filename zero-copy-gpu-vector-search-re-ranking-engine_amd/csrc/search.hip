@@ -830,6 +830,10 @@ int searchTopk(const zcgvs_search_desc* desc, void* d_workspace, std::size_t wor
     }
     std::uint64_t* keys = at<std::uint64_t>(ws, plan.keys);
     std::uint32_t* overflow = at<std::uint32_t>(ws, plan.overflow);
+    // The exact fallback of a phased scan: a plan whose scan kernel reruns flagged queries runs
+    // it after the scan (step 4); any other plan runs it in the launch of its last merge.
+    const bool force = (d.flags & ZCGVS_SEARCH_FORCE_EXACT_PASS) != 0;
+    const bool fuse_recovery = plan.recover && !plan.single_pass && !(plan.rerun && plan.phases.size() > 1 && !force);
     if (plan.single_pass) {
         if (phases_out != nullptr) {
             *phases_out = 1;
@@ -928,6 +932,16 @@ int searchTopk(const zcgvs_search_desc* desc, void* d_workspace, std::size_t wor
         if (phases_out != nullptr) {
             *phases_out = static_cast<int>(plan.phases.size());
         }
+        // Without a rerun, the exact fallback runs in the launch of the last merge (one block per
+        // query merges and, when it flags the query, recomputes its selection).
+        RecoverArgs fused_recovery;
+        if (fuse_recovery) {
+            fused_recovery.force = force || plan.phases.size() <= 1;
+            fused_recovery.width = plan.width;
+            fused_recovery.out_keys = keys;
+            fused_recovery.out_index = plan.rescore ? nullptr : d_out_indices;
+            fused_recovery.out_score = plan.rescore ? nullptr : d_out_values;
+        }
         for (std::size_t p = 0; p < plan.phases.size(); ++p) {
             const PhaseArgs& phase = plan.phases[p];
             const bool timed = events != nullptr && static_cast<int>(p) < max_phases;
@@ -990,20 +1004,26 @@ int searchTopk(const zcgvs_search_desc* desc, void* d_workspace, std::size_t wor
                 in.rerun_tau = tau;
             }
             const bool write_out = last && !plan.rescore;
-            status = launchSelectMerge(in, plan.width, batch, keys, last ? nullptr : tau, overflow,
-                                       write_out ? d_out_indices : nullptr,
-                                       write_out ? d_out_values : nullptr, s);
+            if (last && fuse_recovery) {
+                status = launchMergeRecover(in, plan.width, batch, keys, overflow, write_out ? d_out_indices : nullptr,
+                                            write_out ? d_out_values : nullptr, recoverArgsOf(d, plan, ws),
+                                            fused_recovery, s);
+            } else {
+                status = launchSelectMerge(in, plan.width, batch, keys, last ? nullptr : tau, overflow,
+                                           write_out ? d_out_indices : nullptr,
+                                           write_out ? d_out_values : nullptr, s);
+            }
             if (status != ZCGVS_OK) {
                 return status;
             }
         }
     }
 
-    // 4. the exact fallback for the flagged queries (near-empty launches otherwise): the scan
-    //    kernel's rerun over the whole corpus where it has one, then the selection from the
-    //    rerun's segments, or the last resort's recomputation
-    if (plan.recover) {
-        const bool force = (d.flags & ZCGVS_SEARCH_FORCE_EXACT_PASS) != 0;
+    // 4. the exact fallback for the flagged queries of a rerun plan (near-empty launches
+    //    otherwise): the scan kernel's rerun over the whole corpus, then the selection from the
+    //    rerun's segments, or the last resort's recomputation (other plans ran it with the last
+    //    merge)
+    if (plan.recover && !fuse_recovery) {
         const bool multi_phase = plan.phases.size() > 1;
         const bool rerun = plan.rerun && multi_phase && !force;
         RecoverArgs recovery;
