@@ -291,14 +291,19 @@ typedef struct zcgvs_search_desc {
  * only.
  * ZCGVS_SEARCH_TEST_HIGH_THRESHOLD sets the speculative threshold of a sketch-planned search (see
  * zcgvs_search_topk) to the best sampled score, so that most queries find fewer than k candidates
- * and take the fallback; for tests only (no effect on other plans). */
+ * and take the fallback; for tests only (no effect on other plans).
+ * ZCGVS_SEARCH_TEST_TINY_RERUN gives the rerun of flagged queries (sketch-planned and int8
+ * matrix-core searches) segments of two slots per listed query when every query is listed, so
+ * that, with ZCGVS_SEARCH_TEST_TINY_SEGMENTS listing almost every query, the reruns overflow too
+ * and the last resort runs; for tests only. */
 enum zcgvs_search_flags {
     ZCGVS_SEARCH_MATERIALIZE = 1,
     ZCGVS_SEARCH_UNSORTED_POSTINGS = 2,
     ZCGVS_SEARCH_SORTED_POSTINGS = 4,
     ZCGVS_SEARCH_FORCE_EXACT_PASS = 8,
     ZCGVS_SEARCH_TEST_TINY_SEGMENTS = 16,
-    ZCGVS_SEARCH_TEST_HIGH_THRESHOLD = 32
+    ZCGVS_SEARCH_TEST_HIGH_THRESHOLD = 32,
+    ZCGVS_SEARCH_TEST_TINY_RERUN = 64
 };
 
 /* Bytes of device workspace zcgvs_search_topk needs for this descriptor (0 on error). */

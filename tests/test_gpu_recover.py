@@ -169,3 +169,30 @@ def test_constant_scores_take_the_lowest_indices(gpu):
         desc = capi.search_desc(capi.store_desc(d_corpus, n, dim, capi.F32), d_q, 1, k, flags=flags)
         idx, val, _ = capi.search(desc)
         assert idx[0].tolist() == list(range(k)) and np.all(val == 0.5)
+
+
+@pytest.mark.parametrize("mode", MODES)
+def test_monotone_scores_cut_the_running_list(gpu, mode):
+    # The last resort sweeps the rows in index order with a running list of keys above its
+    # threshold. Scores that ascend with the index append every row, so the list is cut to its
+    # width best many times (70,000 rows against lists of at most 12,288 keys); scores that
+    # descend fill it once; equal scores keep the lowest indices. Dot products of 0.5 * e0 with
+    # rows whose first component is (i + 1) / n are exact in float32.
+    capi = gpu
+    n, dim, k = 70_000, 64, 100
+    corpus = np.zeros((n, dim), np.float32)
+    corpus[:, 0] = (np.arange(n, dtype=np.float64) + 1.0) / n
+    corpus[:, 1] = 1.0
+    queries = np.zeros((3, dim), np.float32)
+    queries[0, 0] = 0.5    # ascends with the row index
+    queries[1, 0] = -0.5   # descends
+    queries[2, 1] = 0.25   # every row scores 0.25
+    d_corpus, d_q = capi.DeviceArray.from_host(corpus), capi.DeviceArray.from_host(queries)
+    desc = capi.search_desc(capi.store_desc(d_corpus, n, dim, capi.F32), d_q, 3, k, capi.DOT,
+                            flags=_flags(capi, mode))
+    idx, val = _run(capi, desc, mode)
+    ref = oracle.scores_f32(corpus, queries, oracle.DOT)
+    ref_idx, ref_val = oracle.topk(ref, k)
+    assert np.array_equal(idx, ref_idx) and np.array_equal(val, ref_val)
+    assert idx[0].tolist() == list(range(n - 1, n - 1 - k, -1))
+    assert idx[1].tolist() == list(range(k)) and idx[2].tolist() == list(range(k))

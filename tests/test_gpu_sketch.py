@@ -8,7 +8,8 @@ keys. Flagged queries are scanned again over the whole corpus by the matrix-core
 threshold that is a certain lower bound (the rerun), and their selection comes from that. Every
 path must give the oracle's top-k bit for bit: the speculative path itself, the fallback when the
 threshold was too high (ZCGVS_SEARCH_TEST_HIGH_THRESHOLD), the rerun after overflowing candidate
-buffers (ZCGVS_SEARCH_TEST_TINY_SEGMENTS), the last resort (ZCGVS_SEARCH_FORCE_EXACT_PASS), with
+buffers (ZCGVS_SEARCH_TEST_TINY_SEGMENTS), the last resort after an overflowing rerun
+(ZCGVS_SEARCH_TEST_TINY_RERUN) or for every query (ZCGVS_SEARCH_FORCE_EXACT_PASS), with
 an allow-mask, and with more than one launch of 256 queries.
 
 A binary (Hamming) search of at most 32 queries runs the same plan in the streaming binary scan
@@ -146,6 +147,16 @@ def test_fallback_paths_match(gpu, corpus, baseline, flag):
     assert np.array_equal(val, ref_val), f"{flag}: scores differ from the speculative path's"
 
 
+def test_overflowing_rerun_takes_the_last_resort(gpu, corpus, baseline):
+    # two-slot segments in the first attempt and in the rerun: nearly every query is listed, its
+    # rerun overflows as well, and recoverKernel recomputes it (one sweep, running list)
+    capi = gpu
+    bits = capi.SEARCH_TEST_TINY_SEGMENTS | capi.SEARCH_TEST_TINY_RERUN
+    idx, val, flags = capi.search(_desc(capi, corpus, flags=bits))
+    assert int(np.count_nonzero(flags)) > BATCH // 2
+    assert np.array_equal(idx, baseline[0]) and np.array_equal(val, baseline[1])
+
+
 def test_masked_rerun(gpu, corpus):
     capi = gpu
     mask = (np.random.default_rng(93).random(N) > 0.25).astype(np.uint8)
@@ -200,6 +211,7 @@ def test_binary_sketch_plan(gpu, binary_corpus, batch, k):
     idx, val, flags = capi.search(desc)
     assert not flags.any(), "a random corpus should not need the fallback"
     for name, bits in (("high", capi.SEARCH_TEST_HIGH_THRESHOLD), ("tiny", capi.SEARCH_TEST_TINY_SEGMENTS),
+                       ("tiny rerun", capi.SEARCH_TEST_TINY_SEGMENTS | capi.SEARCH_TEST_TINY_RERUN),
                        ("force", capi.SEARCH_FORCE_EXACT_PASS)):
         got_idx, got_val, got_flags = capi.search(_binary_desc(capi, c, batch, k, bits))
         if name != "force":

@@ -26,6 +26,7 @@ SEARCH_SORTED_POSTINGS = 4
 SEARCH_FORCE_EXACT_PASS = 8
 SEARCH_TEST_TINY_SEGMENTS = 16
 SEARCH_TEST_HIGH_THRESHOLD = 32
+SEARCH_TEST_TINY_RERUN = 64
 
 _vp = ctypes.c_void_p
 _i32 = ctypes.c_int

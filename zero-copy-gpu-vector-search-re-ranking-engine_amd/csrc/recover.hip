@@ -3,20 +3,20 @@
 // speculative threshold let fewer than width keys through), or for every query with
 // ZCGVS_SEARCH_FORCE_EXACT_PASS.
 //
-// One 1024-thread workgroup per flagged query, launched for the whole batch after the scan; the
-// workgroups past the flagged list return at once, so the launch costs a few microseconds when
-// nothing was flagged. When the scan kernel supports a rerun (the int8 MFMA scan), the flagged
-// queries were scanned once more over the whole corpus, by every workgroup of the GPU, with a
-// threshold that is a lower bound of their width-th best key and the batch's whole segment
-// buffer shared among them; a flagged query whose rerun segments did not overflow takes its
-// selection from them (radix passes over at most a few thousand keys). Otherwise, the last
-// resort: its workgroup selects by radix passes over recomputed
-// scores: three histogram passes over the ordered 32-bit score (11, 11 and 10 bits) find the
-// score t of the width-th best key and how many keys scoring exactly t it must take; a final pass
-// keeps every key above t and the first of those at t in index order (the lowest-index tie rule
-// of tests/cpp/cpu_reference.hpp:26-34). A pass stops early once its bucket holds exactly the
-// keys still needed. Each pass re-reads the corpus, so a recovered query costs a few corpus
-// reads by one workgroup: slow, but exact for any input and with no memory beyond the result.
+// Sketch-planned searches: the scan kernel reran the flagged queries over the whole corpus, by
+// every workgroup of the GPU, with a threshold that is a lower bound of their width-th best key
+// and the batch's whole segment buffer shared among them; recoverKernel (one 1024-thread
+// workgroup per list entry, the entries past the list returning at once) takes each query's
+// selection from its rerun segments (radix passes over at most a few thousand keys). Other
+// searches: mergeRecoverKernel runs the last merge and, in the same block, the last resort for a
+// query that merge flags, so no separate launch runs when nothing is flagged.
+//
+// The last resort (a rerun segment overflowed too, the force flag, or a threshold-phase search):
+// one workgroup sweeps the corpus once in index order, keeps every key above a running
+// threshold in an LDS list and cuts the list to its width best keys whenever it could fill, so
+// the list always holds the exact top-width of the rows swept so far. Keys are unique (score,
+// then index), so this is the lowest-index tie rule of tests/cpp/cpu_reference.hpp:26-34. Its
+// cost is one corpus read at the rate of one compute unit.
 //
 // Scores are computed as the VALU scan computes them (same lanes per row, chunk order and lane
 // group sums, scan_core.hpp), so for every kind they equal that scan's bit for bit.
@@ -35,6 +35,7 @@ namespace {
 constexpr int kRecoverThreads = kMergeThreads;  // 1024
 constexpr int kRecoverChunksPerLane = 8;
 constexpr int kRecoverMinLanes = 8;
+constexpr int kRecoverListKeys = 4096;  // recoverKernel's running list (32 KB of LDS)
 constexpr int kKindI8I8 = 4;
 
 __host__ __device__ constexpr int stagedWordsPerChunk(int kind) {
@@ -156,12 +157,21 @@ struct RecomputeLds {
     std::uint32_t* hist;   // kSelectBins
     std::uint32_t* scan;   // kRecoverThreads / kWave
     std::uint64_t* keys;   // kMaxK
+    std::uint64_t* list;   // `cap` keys: the running list
+    std::uint32_t cap;     // at least kMaxK + kRecoverThreads / 8
     SelectState* state;
-    std::uint32_t* taken_equal;
+    std::uint32_t* fill;   // keys in the list
+    std::uint64_t* tau;    // the list's threshold
 };
 
 // The last resort for query q, by the whole block: the top-`width` over recomputed scores of the
-// whole corpus, written to the outputs.
+// whole corpus, written to the outputs. One sweep over the rows in index order keeps every key
+// above a running threshold in an LDS list; when the next steps could overfill it, the list is
+// cut to its `width` best keys (radix passes over the list, then the keys at or above the cut)
+// and the threshold rises to the smallest kept key. The list so always holds the best `width`
+// keys of the rows swept so far (keys are unique), and after the sweep the query's exact
+// top-`width`. A random corpus appends about width * (1 + ln(n / width)) keys in all; rows that
+// ascend in score append every key and cut the list every (cap - width) rows.
 template <int kKind, int L>
 __device__ __forceinline__ void recomputeQuery(const ScanArgs& scan, const RecoverArgs& args, int chunks, int q,
                                                const RecomputeLds& lds) {
@@ -169,8 +179,10 @@ __device__ __forceinline__ void recomputeQuery(const ScanArgs& scan, const Recov
     std::uint32_t* lds_hist = lds.hist;
     std::uint32_t* lds_scan = lds.scan;
     std::uint64_t* lds_keys = lds.keys;
+    std::uint64_t* lds_list = lds.list;
     SelectState& lds_state = *lds.state;
-    std::uint32_t& lds_taken_equal = *lds.taken_equal;
+    std::uint32_t& lds_fill = *lds.fill;
+    std::uint64_t& lds_tau = *lds.tau;
     const int t = threadIdx.x;
     const int dim = scan.dim;
     const int width = args.width;
@@ -203,12 +215,8 @@ __device__ __forceinline__ void recomputeQuery(const ScanArgs& scan, const Recov
         }
     }
     if (t == 0) {
-        lds_state.prefix = 0ull;
-        lds_state.bits = 0u;
-        lds_state.need = static_cast<std::uint32_t>(width);
-        lds_state.done = 0u;
-        lds_state.count = 0u;
-        lds_taken_equal = 0u;
+        lds_fill = 0u;
+        lds_tau = 0ull;
     }
     float inverse = 0.0f;
     if (scan.lexical != nullptr) {
@@ -302,79 +310,94 @@ __device__ __forceinline__ void recomputeQuery(const ScanArgs& scan, const Recov
         return makeKey(value, static_cast<std::uint32_t>(row));
     };
 
-    // Visits every row in index order, kRowsPerPass rows per step; f(key, row, leader) is called
-    // by every thread of a step (key 0 for threads past the corpus; leader: the row's first lane).
-    auto sweep = [&](auto&& f) {
-        for (long long base = 0; base < n; base += kRowsPerPass) {
-            const long long row = base + t / L;
-            const bool valid = row < n;
-            std::uint64_t key = 0ull;
-            if (__any(valid)) {
-                key = keyOf(valid ? row : n - 1);
-            }
-            f(valid ? key : 0ull, row, valid && group == 0);
+    // Cuts the list's `count` keys (more than width) to its width best at lds_list[0, width) and
+    // raises the threshold to the smallest of them. Whole block; ends with a barrier.
+    auto cutList = [&](std::uint32_t count) {
+        if (t == 0) {
+            lds_state.prefix = 0ull;
+            lds_state.bits = 0u;
+            lds_state.need = static_cast<std::uint32_t>(width);
+            lds_state.done = 0u;
+            lds_state.count = 0u;
+            lds_tau = ~0ull;
         }
+        __syncthreads();
+        for (int pass = 0; pass < kSelectPasses && !lds_state.done; ++pass) {
+            const int digit = selectDigitWidth(pass);
+            for (int i = t; i < (1 << digit); i += kRecoverThreads) {
+                lds_hist[i] = 0u;
+            }
+            __syncthreads();
+            const std::uint32_t bits = lds_state.bits;
+            const std::uint64_t prefix = lds_state.prefix;
+            const int shift = 64 - static_cast<int>(bits) - digit;
+            for (std::uint32_t i = static_cast<std::uint32_t>(t); i < count; i += kRecoverThreads) {
+                const std::uint64_t key = lds_list[i];
+                if (bits == 0u || (key >> (64 - bits)) == prefix) {
+                    atomicAdd(&lds_hist[(key >> shift) & ((1u << digit) - 1u)], 1u);
+                }
+            }
+            __syncthreads();
+            selectPickBucket<kRecoverThreads>(lds_hist, digit, &lds_state, lds_scan);
+        }
+        // exactly width keys reach the cut (the keys are unique)
+        const std::uint64_t cut = selectThreshold(lds_state);
+        for (std::uint32_t i = static_cast<std::uint32_t>(t); i < count; i += kRecoverThreads) {
+            const std::uint64_t key = lds_list[i];
+            if (key >= cut) {
+                const std::uint32_t slot = atomicAdd(&lds_state.count, 1u);
+                if (slot < static_cast<std::uint32_t>(kMaxK)) {
+                    lds_keys[slot] = key;
+                }
+                atomicMin(&lds_tau, key);
+            }
+        }
+        __syncthreads();
+        for (int i = t; i < width; i += kRecoverThreads) {
+            lds_list[i] = lds_keys[i];
+        }
+        if (t == 0) {
+            lds_fill = static_cast<std::uint32_t>(width);
+        }
+        __syncthreads();
     };
 
-    // ---- histogram passes over the ordered score (the key's upper 32 bits) ----
-    for (int pass = 0; pass < 3; ++pass) {
-        const int digit = selectDigitWidth(pass);
-        for (int i = t; i < (1 << digit); i += kRecoverThreads) {
-            lds_hist[i] = 0u;
+    // ---- one sweep in index order, kRowsPerPass rows per step ----
+    // A step appends at most kRowsPerPass keys, so a list at most cap - check_every * kRowsPerPass
+    // long takes check_every steps before the next check.
+    const int check_every = max(1, (static_cast<int>(lds.cap) - width) / kRowsPerPass);
+    const std::uint32_t check_limit = lds.cap - static_cast<std::uint32_t>(check_every * kRowsPerPass);
+    std::uint64_t tau = 0ull;  // lds_tau, read after each barrier that follows a change
+    int step = 0;
+    for (long long base = 0; base < n; base += kRowsPerPass) {
+        const long long row = base + t / L;
+        const bool valid = row < n;
+        std::uint64_t key = 0ull;
+        if (__any(valid)) {
+            key = keyOf(valid ? row : n - 1);
         }
-        __syncthreads();
-        if (lds_state.done) {
-            break;  // uniform: read after a barrier, written only between barriers
+        if (valid && group == 0 && key > tau) {
+            lds_list[atomicAdd(&lds_fill, 1u)] = key;
         }
-        const std::uint32_t bits = lds_state.bits;
-        const std::uint64_t prefix = lds_state.prefix;
-        const int shift = 64 - static_cast<int>(bits) - digit;
-        sweep([&](std::uint64_t key, long long, bool leader) {
-            if (leader && (bits == 0u || (key >> (64 - bits)) == prefix)) {
-                atomicAdd(&lds_hist[(key >> shift) & ((1u << digit) - 1u)], 1u);
+        if (++step == check_every) {
+            step = 0;
+            __syncthreads();
+            const std::uint32_t count = lds_fill;  // uniform: read after the barrier
+            if (count > check_limit) {
+                cutList(count);
+                tau = lds_tau;
             }
-        });
-        __syncthreads();
-        selectPickBucket<kRecoverThreads>(lds_hist, digit, &lds_state, lds_scan);
+        }
     }
     __syncthreads();
+    std::uint32_t taken = lds_fill;
+    if (taken > static_cast<std::uint32_t>(width)) {
+        cutList(taken);
+        taken = static_cast<std::uint32_t>(width);
+    }
 
-    // ---- collection: every key above the cut, plus the first `need` keys at a tied score ----
-    const bool tied = !lds_state.done;  // all 32 score bits decided, more keys at t than needed
-    const std::uint64_t cut = selectThreshold(lds_state);  // lower edge of the chosen bucket
-    const std::uint32_t need_equal = tied ? lds_state.need : 0u;
-    const std::uint32_t above_needed = static_cast<std::uint32_t>(width) - need_equal;
-    (void)above_needed;
-    sweep([&](std::uint64_t key, long long, bool leader) {
-        const std::uint32_t score_bits = static_cast<std::uint32_t>(key >> 32);
-        const std::uint32_t cut_bits = static_cast<std::uint32_t>(cut >> 32);
-        bool take = leader && (tied ? score_bits > cut_bits : key >= cut);
-        if (tied) {
-            // tied keys in index order: a block-wide prefix count over this step's rows (thread
-            // order is row order inside a step)
-            const bool equal = leader && score_bits == cut_bits;
-            std::uint32_t step_total = 0u;
-            const std::uint32_t through = blockInclusiveSum<kRecoverThreads>(equal ? 1u : 0u, lds_scan, &step_total);
-            const std::uint32_t rank = lds_taken_equal + through - 1u;
-            take = take || (equal && rank < need_equal);
-            __syncthreads();
-            if (t == 0) {
-                lds_taken_equal += step_total;
-            }
-        }
-        if (take) {
-            const std::uint32_t slot = atomicAdd(&lds_state.count, 1u);
-            if (slot < static_cast<std::uint32_t>(kMaxK)) {
-                lds_keys[slot] = key;
-            }
-        }
-    });
-    __syncthreads();
-
-    const std::uint32_t taken = min(min(lds_state.count, static_cast<std::uint32_t>(kMaxK)),
-                                    static_cast<std::uint32_t>(width));
     std::uint64_t* dst = args.out_keys + static_cast<std::size_t>(q) * width;
-    forEachRanked(lds_keys, taken, [&](std::uint32_t rank, std::uint64_t key) {
+    forEachRanked(lds_list, taken, [&](std::uint32_t rank, std::uint64_t key) {
         dst[rank] = key;
         if (args.out_index != nullptr) {
             const std::size_t o = static_cast<std::size_t>(q) * width + rank;
@@ -397,8 +420,10 @@ __global__ __launch_bounds__(kRecoverThreads) void recoverKernel(ScanArgs scan, 
     __shared__ std::uint32_t lds_hist[kSelectBins];
     __shared__ std::uint32_t lds_scan[kRecoverThreads / kWave];
     __shared__ std::uint64_t lds_keys[kMaxK];
+    __shared__ std::uint64_t lds_list[kRecoverListKeys];
     __shared__ SelectState lds_state;
-    __shared__ std::uint32_t lds_taken_equal;
+    __shared__ std::uint32_t lds_fill;
+    __shared__ std::uint64_t lds_tau;
 
     int q = blockIdx.x;
     int entry = 0;
@@ -419,7 +444,8 @@ __global__ __launch_bounds__(kRecoverThreads) void recoverKernel(ScanArgs scan, 
         return;
     }
     recomputeQuery<kKind, L>(scan, args, chunks, q,
-                             RecomputeLds{lds_query, lds_hist, lds_scan, lds_keys, &lds_state, &lds_taken_equal});
+                             RecomputeLds{lds_query, lds_hist, lds_scan, lds_keys, lds_list, kRecoverListKeys,
+                                          &lds_state, &lds_fill, &lds_tau});
 }
 
 // The final merge of a phased search and its exact fallback in one launch: block q merges query
@@ -438,9 +464,12 @@ __global__ __launch_bounds__(kRecoverThreads) void mergeRecoverKernel(MergeInput
     if (!flagged && !args.force) {
         return;  // uniform
     }
+    // the staged query at the end of the candidate LDS, the running list before it
+    const std::uint32_t query_keys = (static_cast<std::uint32_t>(chunks * stagedWordsPerChunk(kKind)) + 1u) / 2u;
+    const std::uint32_t cap = kSelectLdsKeys - query_keys;
     recomputeQuery<kKind, L>(scan, args, chunks, q,
-                             RecomputeLds{reinterpret_cast<std::uint32_t*>(lds.cand), lds.hist, lds.scan, lds.keys,
-                                          &lds.state, &lds.valid});
+                             RecomputeLds{reinterpret_cast<std::uint32_t*>(lds.cand + cap), lds.hist, lds.scan,
+                                          lds.keys, lds.cand, cap, &lds.state, &lds.valid, &lds.kth});
 }
 
 int kindOf(const ScanArgs& scan) {
@@ -541,8 +570,10 @@ int launchMergeRecover(const MergeInputs& in, int k, int batch, std::uint64_t* o
     const int chunks = static_cast<int>(rowBytes(scan.dtype, scan.dim) / 16);
     const int lanes = lanesPerRow(chunks, kRecoverChunksPerLane, kRecoverMinLanes);
     const int kind = kindOf(scan);
-    // the staged query goes to the merge's candidate LDS
-    if (static_cast<std::size_t>(chunks) * stagedWordsPerChunk(kind) * 4 > sizeof(MergeLds::cand)) {
+    // the staged query goes to the end of the merge's candidate LDS, before it the running list of
+    // at least kMaxK keys and a step's rows
+    if (static_cast<std::size_t>(chunks) * stagedWordsPerChunk(kind) * 4 >
+        sizeof(MergeLds::cand) - (kMaxK + kRecoverThreads / 8) * sizeof(std::uint64_t)) {
         return setError(ZCGVS_ERR_RUNTIME, "zcgvs merge and recovery: query too large for the merge's LDS");
     }
     switch (kind) {

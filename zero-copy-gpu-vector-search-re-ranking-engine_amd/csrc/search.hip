@@ -512,6 +512,9 @@ Plan makePlan(const zcgvs_search_desc& d) {
     // (at most 2^23 slots: the int8 MFMA scan packs a slot, a half and an 8-bit query into 32 bits)
     plan.seg_log2 = std::min(23, std::max({6, ceilLog2(4 * expected + 16), ceilLog2(item_rows)}));
     plan.rerun_seg_log2 = plan.seg_log2;
+    if ((d.flags & ZCGVS_SEARCH_TEST_TINY_RERUN) != 0) {
+        plan.rerun_seg_log2 = 1;  // tests: the reruns overflow as well (see the flag)
+    }
     if ((d.flags & ZCGVS_SEARCH_TEST_TINY_SEGMENTS) != 0) {
         plan.seg_log2 = 1;  // tests: overflow nearly every query so the fallback runs from its flags
     }
