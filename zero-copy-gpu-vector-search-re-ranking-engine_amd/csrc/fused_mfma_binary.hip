@@ -23,9 +23,11 @@
 //
 // Work split. Launches of up to 32 queries (one set, two MFMA query groups of 16) run
 // mfmaBinaryStreamKernel: the B operands sit in LDS and each of 16 wavefronts streams its own
-// rows into registers (no shared tile, no barrier). Larger launches (up to 4 sets, 128 queries)
-// run mfmaBinaryScanKernel: 8 wavefronts, each with one set's B operands in registers, share the
-// tiles below and split each tile's 16-row blocks among the wavefronts of a set.
+// rows into registers (no shared tile, no barrier). It also serves the sketch plan of a search of
+// at most 32 queries: a sketch mode (the least distance of each query per pair of wavefronts, no
+// keys) and a rerun mode (the device list of flagged queries). Larger launches (up to 4 sets, 128
+// queries) run mfmaBinaryScanKernel: 8 wavefronts, each with one set's B operands in registers,
+// share the tiles below and split each tile's 16-row blocks among the wavefronts of a set.
 //
 // MFMA layout (v_mfma_i32_16x16x64_i8). Lane l supplies row (A) / query (B) l % 16 and 16 dims
 // of lane group h = l / 16 per step: 16-byte chunk h + 4j of the row covers steps 8j .. 8j + 7,
