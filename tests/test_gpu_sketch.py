@@ -235,3 +235,28 @@ def test_binary_sketch_thresholds(gpu, binary_corpus):
         queries = [0, batch - 1]
         sampled = oracle.scores_hamming(c["words"][rows], c["qwords"][queries], BIN_DIM)
         _check_sketch(state, flags, sampled, queries)
+
+
+def test_binary_512_sketch_plan(gpu):
+    # 512-bit rows: 768-row blocks, every 4th one sampled at 3.2M rows; the speculative path, the
+    # rerun and the oracle agree bit for bit
+    capi = gpu
+    n, dim, batch, k = 3_200_001, 512, 24, 100
+    words = np.random.default_rng(96).integers(0, 2**32, size=(n, dim // 32), dtype=np.uint32)
+    queries = normalized(batch, dim, 97)
+    d_words, d_queries = capi.DeviceArray.from_host(words), capi.DeviceArray.from_host(queries)
+
+    def desc(flags=0):
+        return capi.search_desc(capi.store_desc(d_words, n, dim, capi.BINARY), d_queries, batch, k, capi.COSINE,
+                                flags=flags)
+
+    rows = capi.search_phase_rows(desc())
+    assert len(rows) == 2 and rows[1] == n, f"not sketch-planned: {rows}"
+    idx, val, flags = capi.search(desc())
+    assert not flags.any()
+    tiny = capi.search(desc(capi.SEARCH_TEST_TINY_SEGMENTS))
+    assert int(np.count_nonzero(tiny[2])) > batch // 2
+    assert np.array_equal(tiny[0], idx) and np.array_equal(tiny[1], val)
+    sample = [0, 11, batch - 1]
+    ref = oracle.scores_hamming(words, oracle.pack_binary(queries)[sample], dim)
+    assert_topk_equivalent(idx[sample], val[sample], ref, k)
