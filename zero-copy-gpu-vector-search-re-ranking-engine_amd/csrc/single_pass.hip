@@ -14,8 +14,9 @@
 // merge (topk.hip) selects the global top-`width` from the segments: for width <= 32 from the
 // segments whose first key reaches the width-th best first key, for wide selections after
 // merging groups of workgroups first. A
-// list holds max(1024, 4 * width) keys (less when four queries share the LDS), so compactions
-// are rare. Nothing can overflow, so no fallback pass follows.
+// list holds max(1024, 4 * width) keys for a narrow selection and the query's whole share of the
+// list LDS for a wide one (less when four queries share the LDS), so compactions are rare.
+// Nothing can overflow, so no fallback pass follows.
 //
 // Rows are read and scored as the VALU scan and the exact fallback read them (the same lane
 // groups of L lanes and up to 8 16-byte chunks per lane, scan_core.hpp), so scores equal theirs
@@ -92,8 +93,12 @@ __global__ __launch_bounds__(kSpThreads) void singlePassScanKernel(ScanArgs scan
     constexpr int kPerRow = kPer / kSets;
     static_assert(kPerRow * kSets == kPer, "row sets split the lane's chunks evenly");
     // steps between capacity checks: every list takes at most kRowsPerStep keys per step (the
-    // host makes cap - width at least one step's rows)
-    const int check_every = (cap - width) / kRowsPerStep;
+    // host makes cap - width at least one step's rows). A narrow selection checks as often as its
+    // list allows, so the list stays short and its compactions are rankings; a wide one (more
+    // than kSpRankKeys keys, compacted by radix passes) checks half as often, so a list is cut
+    // only once it is about half full.
+    const int check_every = width > kSpRankKeys ? max(1, (cap - width) / (2 * kRowsPerStep))
+                                                : (cap - width) / kRowsPerStep;
     const std::size_t row_bytes = static_cast<std::size_t>(chunks) * 16;
     const std::uint8_t* corpus = static_cast<const std::uint8_t*>(scan.corpus);
     const bool l2 = scan.metric == ZCGVS_METRIC_L2;
@@ -537,11 +542,16 @@ SinglePassShape singlePassShape(const ScanArgs& scan, int width) {
     if ((chunks + layout.lanes - 1) / layout.lanes > kSpChunksPerLane || staged > kSpQueryLds) {
         return shape;
     }
-    // A list holds its width best keys plus at least one check's appends (rows per step); four
-    // times the width, or two steps' rows beyond it, keeps compactions rare.
+    // A list holds its width best keys plus at least one check's appends (rows per step): for a
+    // narrow selection four times the width, or two steps' rows beyond it; a wide one (compacted
+    // by radix passes) takes the queries' whole share of the list LDS, so it is cut about once per
+    // workgroup (binary 50M x 1024, 1000 keys, one query: 1.013 against 1.04-1.05 ms per scan).
     const int rows_per_step = kSpThreads / layout.lanes * layout.sets;
-    const int cap = std::min(kSpListKeys / scan.batch,
-                             std::max({kSpMinCap, (4 * width + 63) / 64 * 64, width + 2 * rows_per_step}));
+    const int share = kSpListKeys / scan.batch / 64 * 64;
+    const int cap = width > kSpRankKeys
+                        ? share
+                        : std::min(share,
+                                   std::max({kSpMinCap, (4 * width + 63) / 64 * 64, width + 2 * rows_per_step}));
     if (cap - width < rows_per_step) {
         return shape;
     }
