@@ -158,7 +158,7 @@ def test_sketch_plan_samples_then_scans_everything(capi, n, batch, k, stride):
 
 
 @pytest.mark.parametrize("n,batch,k,stride,sketched", [
-    (50_000_000, 32, 1000, 32, True),   # the binary 50M x 1024 configuration's Hamming stage
+    (50_000_000, 32, 1000, 64, True),   # the binary 50M x 1024 configuration's Hamming stage
     (2_000_003, 20, 100, 4, True),      # every 4th 384-row block, ragged tail
     (50_000_000, 33, 1000, 0, False),   # more than 32 queries: the tile scan, threshold phases
     (1_000_000, 32, 100, 0, False),     # under 4 sampled blocks per workgroup: threshold phases

@@ -464,9 +464,9 @@ Plan makePlan(const zcgvs_search_desc& d) {
     long long expected = (static_cast<long long>(plan.width) * growth) / plan.segments;
 
     // Sketch plan (int8 MFMA scan and binary streaming scan, when the threshold phases would be
-    // three or more): a sketch phase over every 32nd block keeps per slot (a row half of a
-    // workgroup's lanes in the int8 scan, a pair of wavefronts in the binary one) the best exact
-    // score of each query; the j-th best of those slot scores is the threshold
+    // three or more): a sketch phase over every 32nd block (64th for the binary scan) keeps per
+    // slot (a row half of a workgroup's lanes in the int8 scan, a pair of wavefronts in the binary
+    // one) the best exact score of each query; the j-th best of those slot scores is the threshold
     // of ONE scan over the whole corpus. With f = sketch rows / corpus rows, the number of
     // corpus rows at or above the sketch's j-th best score is about Gamma(j) / f, so
     // j = width f + 5.5 sqrt(width f) + 2 (15 at f = 1/32, width = 100) leaves fewer than width
@@ -475,8 +475,11 @@ Plan makePlan(const zcgvs_search_desc& d) {
     // candidates reached it; the k-th best slot score is its guaranteed threshold then.
     const int slots = (plan.use_mfma ? 2 : mfmaBinarySketchSlotsPerWorkgroup()) * plan.workgroups;
     // (A smaller corpus samples every 16th, 8th or 4th block, so every workgroup still sees at
-    // least 4 sampled blocks; below that the threshold phases stay.)
-    long long sketch_stride = 32;
+    // least 4 sampled blocks; below that the threshold phases stay. The binary scan samples half
+    // as many blocks at full size: its sketch launch costs more per row than its full scan, and at
+    // binary 50M x 1024, B = 32, width 1000 the 64th-block sketch took the step from 1.49-1.50 to
+    // 1.47-1.48 ms; the int8 scan timed the same at 32 and 64.)
+    long long sketch_stride = binary_sketch ? 64 : 32;
     while (sketch_stride > 4 && phaseItems(blocks, sketch_stride, 0) < 4LL * plan.workgroups) {
         sketch_stride /= 2;
     }
