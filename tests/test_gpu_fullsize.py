@@ -2,9 +2,11 @@
 10M x 768 per-vector int8 (batch 256, k=100), 50M x 1024 binary with a float16 rescore of 1000
 candidates (batch 32, k=10) and the 1M-document hybrid BM25 + float16 configuration (batch 16,
 k=10). Inputs are generated on the device at their real shapes by the seeded
-generator the benchmark uses. The CPU oracle checks sampled queries against the whole corpus
-(copied to the host); every query is checked for the properties that hold at any size (ids unique
-and in range, scores sorted, each returned score equal to the oracle's score of that id)."""
+generator the benchmark uses. The CPU oracle checks every query's top-k against the whole corpus,
+copied to the host, at the float, per-vector int8, binary (its Hamming stage) and hybrid
+configurations; the sorted and crowded int8 corpora check their flagged queries and a sample. Every
+query is also checked for the properties that hold at any size (ids unique and in range, scores
+sorted, each returned score equal to the oracle's score of that id)."""
 
 from __future__ import annotations
 
@@ -55,10 +57,12 @@ def test_ten_million_by_768_per_vector_int8(gpu):
         rows = idx[b]
         exact = oracle.scores_i8i8(codes[rows], scales[rows], qcodes[b:b + 1], qscales[b:b + 1])[0]
         assert np.array_equal(val[b], exact), f"query {b}: scores differ from the oracle's"
-    # sampled queries: the whole top-100 against a scan of all 10M rows
-    sample = [0, 1, 77, 128, 255]
-    ref = oracle.scores_i8i8(codes, scales, qcodes[sample], qscales[sample])
-    assert_topk_equivalent(idx[sample], val[sample], ref, w["k"])
+    # every query: the whole top-100 against a scan of all 10M rows, 32 queries per oracle call
+    for b0 in range(0, w["batch"], 32):
+        sel = slice(b0, b0 + 32)
+        ref = oracle.scores_i8i8(codes, scales, qcodes[sel], qscales[sel])
+        assert_topk_equivalent(idx[sel], val[sel], ref, w["k"])
+        del ref
 
 
 def test_ten_million_sorted_rows_are_exact(gpu):
@@ -106,7 +110,7 @@ def test_ten_million_crowded_rows_take_the_fallback(gpu):
         hot.update(range(first, first + 64))
     for b in range(w["hot_queries"]):
         assert set(idx[b].tolist()) <= hot, f"query {b}: its near-copies should be its top-{w['k']}"
-    sample = [0, 7, 15, 16, 255]
+    sample = sorted(flagged | {16, 255})  # every query through the fallback, and two others
     ref = oracle.scores_i8i8(codes, scales, qcodes[sample], qscales[sample])
     assert_topk_equivalent(idx[sample], val[sample], ref, w["k"])
 
@@ -134,18 +138,24 @@ def test_fifty_million_binary_with_fp16_rescore(gpu):
         exact = oracle.rescore(got, host_q[b:b + 1], np.arange(k, dtype=np.int32)[None, :])[0]
         tol = float_tolerance(host_q[b:b + 1], got, oracle.COSINE)[0]
         assert np.all(np.abs(val[b].astype(np.float64) - exact) <= tol), f"query {b}: rescore differs"
-    # sampled queries (8, spread over the batch): the Hamming top-1000 stage alone (the same
-    # search without the rescore, k = 1000) equals the oracle's top-1000 over all 50M rows, ids
-    # and scores bit for bit; then the float16 rescore of those candidates gives the top-10
+    # every query: the Hamming top-1000 stage alone (the same search without the rescore,
+    # k = 1000) equals the oracle's top-1000 over all 50M rows, ids and scores bit for bit (8
+    # queries per oracle call); then, for 8 queries spread over the batch, the float16 rescore of
+    # those candidates gives the top-10
     sample = [0, 5, 9, 14, 18, 23, 27, 31]
     qwords = oracle.pack_binary(host_q)
     stage1 = capi.search_desc(capi.store_desc(corpus, w["n"], dim, capi.BINARY), queries, w["batch"], c,
                               capi.COSINE)
     cand_idx, cand_val, flags = capi.search(stage1)
     assert not flags.any()
-    ref_cand, ref_cand_val = oracle.topk(oracle.scores_hamming(words, qwords[sample], dim), c)
-    assert np.array_equal(cand_idx[sample], ref_cand), "Hamming top-1000 ids differ from the oracle's"
-    assert np.array_equal(cand_val[sample], ref_cand_val), "Hamming top-1000 scores differ"
+    all_cand = np.empty_like(cand_idx)
+    for b0 in range(0, w["batch"], 8):
+        sel = slice(b0, b0 + 8)
+        ref_ids, ref_vals = oracle.topk(oracle.scores_hamming(words, qwords[sel], dim), c)
+        assert np.array_equal(cand_idx[sel], ref_ids), f"queries {b0}..: Hamming top-1000 ids differ"
+        assert np.array_equal(cand_val[sel], ref_vals), f"queries {b0}..: Hamming top-1000 scores differ"
+        all_cand[sel] = ref_ids
+    ref_cand = all_cand[sample]
     for i, b in enumerate(sample):
         cand = ref_cand[i]
         rows = rows_of(cand)
