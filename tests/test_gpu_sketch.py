@@ -172,6 +172,22 @@ def test_masked_rerun(gpu, corpus):
     _sampled(corpus, results[0][0], results[0][1], [3, 150], K, mask)
 
 
+def test_partial_launch_of_queries(gpu, corpus):
+    # 40 queries: the launch's wavefronts past the first two hold 8 or no queries; the sketch, the
+    # speculative scan and the rerun after tiny segments agree with each other and the oracle
+    capi = gpu
+    batch, k = 40, 100
+    assert len(capi.search_phase_rows(_desc(capi, corpus, batch=batch, k=k))) == 2, "not sketch-planned"
+    plain = capi.search(_desc(capi, corpus, batch=batch, k=k))
+    assert not plain[2].any()
+    for bits in (capi.SEARCH_TEST_TINY_SEGMENTS, capi.SEARCH_TEST_HIGH_THRESHOLD):
+        other = capi.search(_desc(capi, corpus, batch=batch, k=k, flags=bits))
+        assert int(np.count_nonzero(other[2])) > batch // 2
+        assert np.array_equal(plain[0], other[0]) and np.array_equal(plain[1], other[1])
+    _exact_scores(corpus, plain[0], plain[1], batch)
+    _sampled(corpus, plain[0], plain[1], [0, 31, 32, 39], k)
+
+
 def test_two_launches_of_queries(gpu, corpus):
     # 300 queries: two launches per scan; with tiny segments all of them are flagged, so the
     # rerun's list spans both launches (entries 256..299 in the second)
