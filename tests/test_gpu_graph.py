@@ -42,19 +42,36 @@ def _binary_rescore_desc(capi, n, dim, batch, k, seed):
                             rescore_candidates=1000)
 
 
+def _int8_tiny_desc(capi, n, dim, batch, k, seed):
+    # two-slot candidate segments: nearly every query is flagged and rerun over the whole corpus
+    desc = _int8_desc(capi, n, dim, batch, k, seed)
+    desc.flags = capi.SEARCH_TEST_TINY_SEGMENTS
+    return desc
+
+
+def _binary_desc(capi, n, dim, batch, k, seed):
+    words = np.random.default_rng(seed).integers(0, 2**32, size=(n, dim // 32), dtype=np.uint32)
+    queries = normalized(batch, dim, seed + 1)
+    return capi.search_desc(capi.store_desc(capi.DeviceArray.from_host(words), n, dim, capi.BINARY),
+                            capi.DeviceArray.from_host(queries), batch, k)
+
+
 @pytest.mark.parametrize("make,n,dim,batch,k", [
     (_int8_desc, 200_000, 768, 64, 100),   # MFMA scan, several threshold phases
     (_f16_desc, 150_000, 384, 1, 10),      # single pass, one query
     (_f16_desc, 150_000, 384, 16, 10),     # fp16 MFMA scan
     (_f32_desc, 200_000, 384, 64, 10),     # fp32 bf16-split MFMA scan
     (_binary_rescore_desc, 200_000, 1024, 1, 10),  # single pass of 1000 keys, group merges, rescore
+    (_int8_desc, 1_000_000, 256, 256, 100),     # sketch plan: sketch, thresholds, one scan, merge
+    (_int8_tiny_desc, 1_000_000, 256, 256, 100),  # sketch plan with every query rerun
+    (_binary_desc, 2_000_003, 1024, 32, 100),   # binary sketch plan
 ])
 def test_graph_replays_match_direct_calls(gpu, make, n, dim, batch, k):
     capi = gpu
     desc = make(capi, n, dim, batch, k, 31)
     other = make(capi, n // 2, dim, batch, k, 57)
     ref_idx, ref_val, flags = capi.search(desc)
-    assert not flags.any()
+    assert not flags.any() or desc.flags & capi.SEARCH_TEST_TINY_SEGMENTS
     other_idx, other_val, _ = capi.search(other)
 
     size = capi.search_workspace_bytes(desc)
