@@ -174,13 +174,20 @@ def build_inputs(capi, w):
         keep["lexical"] = {name: capi.DeviceArray.from_host(index[name])
                            for name in ("offsets", "posting_docs", "posting_weights")}
         keep["terms"] = capi.DeviceArray.from_host(terms)
+        # the index's slice table (built once with the index, outside every timed region)
+        table_bytes = capi.lexical_slice_table_bytes(w["vocab"], n)
+        keep["slice_table"] = capi.DeviceArray(table_bytes // 4, np.uint32)
+        capi.build_lexical_slice_table(keep["lexical"]["offsets"], keep["lexical"]["posting_docs"], w["vocab"], n,
+                                       keep["slice_table"])
+        capi.synchronize()
         keep["postings"] = int(index["offsets"][-1])
         keep["index"] = index
         keep["terms_host"] = terms
         extra.update(lex_offsets=keep["lexical"]["offsets"], lex_docs=keep["lexical"]["posting_docs"],
                      lex_weights=keep["lexical"]["posting_weights"], lex_doc_count=n,
                      lex_vocab_size=w["vocab"], query_terms=keep["terms"], lexical_stride=w["terms"],
-                     dense_weight=w["dense_weight"], flags=capi.SEARCH_SORTED_POSTINGS)
+                     dense_weight=w["dense_weight"], flags=capi.SEARCH_SORTED_POSTINGS,
+                     lex_slice_table=keep["slice_table"])
     desc = capi.search_desc(store, queries, batch, w["k"], capi.COSINE, **extra)
     return desc, corpus, queries, keep
 
@@ -196,7 +203,7 @@ def row_bytes(w):
 
 def lexical_bytes(keep):
     """Algorithmic bytes of the batch's BM25 stage: 8 B (doc id + weight) per posting of every
-    query's terms, plus the two 8-byte offsets of each term (the c5 numerator of the survey)."""
+    query's terms, plus the two 8-byte offsets of each term (the stage's HBM-roofline numerator)."""
     terms = keep["terms_host"]
     offsets = keep["index"]["offsets"]
     valid = terms >= 0

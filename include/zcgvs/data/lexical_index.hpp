@@ -37,14 +37,18 @@ public:
     float averageDocLength() const { return average_doc_length_; }
     // Every term's postings strictly ascending by document (checked at load).
     bool postingsSorted() const { return sorted_postings_; }
+    // Per-term posting counts below every 4096-document boundary (zcgvs_build_lexical_slice_table),
+    // built at load for sorted postings; null otherwise.
+    const std::uint32_t* deviceSliceTable() const { return slice_table_.data(); }
     std::size_t deviceBytes() const {
-        return offsets_.bytes() + posting_docs_.bytes() + posting_weights_.bytes();
+        return offsets_.bytes() + posting_docs_.bytes() + posting_weights_.bytes() + slice_table_.bytes();
     }
 
 private:
     DeviceBuffer<std::int64_t> offsets_;
     DeviceBuffer<int> posting_docs_;
     DeviceBuffer<float> posting_weights_;
+    DeviceBuffer<std::uint32_t> slice_table_;
     std::int64_t doc_count_ = 0;
     std::int64_t posting_count_ = 0;
     int vocab_size_ = 0;

@@ -211,6 +211,18 @@ int zcgvs_launch_bm25_batched(const int64_t* d_offsets, const int* d_docs,
                               const float* d_weights, const int* d_query_terms, int term_stride,
                               int batch, int doc_count, float* d_scores, zcgvs_stream_t stream);
 
+/* Slice table of a lexical index whose postings ascend strictly by document (the
+ * ZCGVS_SEARCH_SORTED_POSTINGS layout): d_table[t * S + c] = the number of term t's postings whose
+ * document is below c * 4096 for c < S - 1, and below doc_count for c = S - 1, with
+ * S = ceil(doc_count / 4096) + 1 (doc_count <= 2^31 - 1). Built once per index (one binary search
+ * per entry), it lets every hybrid search take its terms' 4096-document slice bounds from the
+ * table (zcgvs_search_desc.lex_slice_table). No reference counterpart: the reference's BM25
+ * (src/cuda/lexical.cu:17-42) scatters every posting with atomics and keeps no such table.
+ * zcgvs_lexical_slice_table_bytes returns 0 for an empty index or too many documents. */
+size_t zcgvs_lexical_slice_table_bytes(int vocab_size, int64_t doc_count);
+int zcgvs_build_lexical_slice_table(const int64_t* d_offsets, const int* d_docs, int vocab_size,
+                                    int64_t doc_count, uint32_t* d_table, zcgvs_stream_t stream);
+
 /* src/cuda/lexical.cu:94-105 launchMaxPositive: *d_max = max(*d_max, max_i values[i]) for
  * values >= 0 (caller zeroes *d_max). */
 int zcgvs_launch_max_positive(const float* d_values, int count, float* d_max,
@@ -270,6 +282,10 @@ typedef struct zcgvs_search_desc {
     int lexical_stride;
     float dense_weight;
     int flags;                 /* zcgvs_search_flags bits; 0 for the default pipeline           */
+    /* Optional slice table of the lexical index (zcgvs_build_lexical_slice_table over
+     * lex_doc_count documents); with ZCGVS_SEARCH_SORTED_POSTINGS the BM25 stage reads its terms'
+     * slice bounds from it instead of searching the postings. NULL: searched per call. */
+    const uint32_t* lex_slice_table;
 } zcgvs_search_desc;
 
 /* zcgvs_search_desc.flags. ZCGVS_SEARCH_MATERIALIZE runs the reference-order pipeline (a

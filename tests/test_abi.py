@@ -36,6 +36,13 @@ def test_version_and_sizing_helpers(capi):
     assert lib.zcgvs_similarity_shared_bytes(capi.F32, 384, 11) == 8 * 384 * 4
     assert lib.zcgvs_similarity_shared_bytes(capi.BINARY, 384, 3) == 3 * 12 * 4
     assert lib.zcgvs_rescore_shared_bytes(384) == 384 * 4
+    # the lexical slice table: one count per term and 4096-document boundary, plus the end
+    assert capi.lexical_slice_table_bytes(30_000, 1_000_000) == 30_000 * (245 + 1) * 4
+    assert capi.lexical_slice_table_bytes(7, 4096) == 7 * 2 * 4
+    assert capi.lexical_slice_table_bytes(7, 4097) == 7 * 3 * 4
+    assert capi.lexical_slice_table_bytes(0, 100) == 0
+    assert capi.lexical_slice_table_bytes(7, 0) == 0
+    assert capi.lexical_slice_table_bytes(7, 2**31) == 0
 
 
 def test_empty_work_returns_ok_without_a_gpu(capi):
@@ -97,6 +104,22 @@ def test_search_validation_rescore_store(capi):
         capi.search_workspace_bytes(_desc(capi, query_terms=1 << 22, lexical_stride=4, lex_offsets=1,
                                           lex_docs=1, lex_weights=1, lex_doc_count=10,
                                           lex_vocab_size=100))
+
+
+def test_lexical_slice_table_validation(capi):
+    lexical = dict(query_terms=1 << 22, lexical_stride=4, lex_offsets=1, lex_docs=1, lex_weights=1,
+                   lex_vocab_size=100, lex_slice_table=1 << 23)
+    with pytest.raises(ValueError, match="slice table needs ZCGVS_SEARCH_SORTED_POSTINGS"):
+        capi.search_workspace_bytes(_desc(capi, lex_doc_count=1000, **lexical))
+    with pytest.raises(ValueError, match="at most 2\\^31 - 1 documents"):
+        capi.search_workspace_bytes(_desc(capi, lex_doc_count=2**31, flags=capi.SEARCH_SORTED_POSTINGS,
+                                          **lexical))
+    assert capi.search_workspace_bytes(_desc(capi, lex_doc_count=1000, flags=capi.SEARCH_SORTED_POSTINGS,
+                                             **lexical)) > 0
+    with pytest.raises(ValueError, match="empty index"):
+        capi.build_lexical_slice_table(1, 1, 0, 1000, 1)
+    with pytest.raises(ValueError, match="null device pointer"):
+        capi.build_lexical_slice_table(None, 1, 10, 1000, 1)
 
 
 def test_workspace_sizes(capi):

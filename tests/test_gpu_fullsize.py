@@ -175,19 +175,24 @@ def test_one_million_hybrid_bm25_fp16(gpu):
     """The hybrid configuration at its stated size: N = 1,000,000 documents, vocabulary 30,000,
     Poisson(200) lengths, Zipf(1.1) tokens, 8 distinct Zipf terms per query, BM25 k1 = 1.2,
     b = 0.75, fp16 d = 384 cosine, fusion weight 0.5, batch 16, k = 10 - the sliced BM25 sweep over
-    sorted postings (245 slices of 4096 documents, head terms with df near N) against the oracle's
-    BM25, maximum and fusion (src/cuda/lexical.cu:17-74, tests/cuda/test_lexical.cu:71-93), then the
-    same search with the postings scattered (the default, any order), bit-identical."""
+    sorted postings (245 slices of 4096 documents, head terms with df near N, slice bounds from the
+    index's slice table) against the oracle's BM25, maximum and fusion (src/cuda/lexical.cu:17-74,
+    tests/cuda/test_lexical.cu:71-93), then the same search with the slice bounds searched per call
+    and with the postings scattered (the default, any order), all bit-identical."""
     capi = gpu
     w = bench.WORKLOADS["hybrid-1m"]
     n, k, weight = w["n"], w["k"], w["dense_weight"]
     desc, corpus, queries, keep = bench.build_inputs(capi, w)
-    assert desc.flags == capi.SEARCH_SORTED_POSTINGS
+    assert desc.flags == capi.SEARCH_SORTED_POSTINGS and desc.lex_slice_table
     idx, val, flags = capi.search(desc)
     assert not flags.any()
     _ranked(idx, val, n)
     index, terms = keep["index"], keep["terms_host"]
     assert index["offsets"][-1] > 100_000_000 and terms.shape == (w["batch"], 8)
+    desc.lex_slice_table = None
+    idx2, val2, flags = capi.search(desc)
+    assert not flags.any()
+    assert np.array_equal(idx, idx2) and np.array_equal(val, val2), "slice table and searched bounds differ"
     desc.flags = 0
     idx2, val2, flags = capi.search(desc)
     assert not flags.any()

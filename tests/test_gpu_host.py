@@ -115,6 +115,25 @@ def test_engine_hybrid_bm25(zc, tmp_path):
     assert_topk_equivalent(got_ids, got_scores, fused, k, 0.5 * float_tolerance(queries, corpus, 0, rel=1e-3) + 1e-6)
 
 
+def test_lexical_index_slice_table(zc, tmp_path):
+    # Sorted postings get the slice table at load (one uint32 per term and 4096-document boundary,
+    # plus the end); postings out of document order get none and are scattered by the search.
+    n, vocab = 20_000, 3000
+    built = lexical.build_bm25(lexical.synthetic_corpus(n, vocab_size=vocab, mean_length=60, seed=9), vocab)
+    offsets, docs, weights = built["offsets"], built["posting_docs"], built["posting_weights"]
+    index = zc.LexicalIndex.from_csr(offsets, docs, weights, n)
+    assert index.postings_sorted and index.has_slice_table
+    postings = int(offsets[-1])
+    assert index.device_bytes == (vocab + 1) * 8 + postings * 8 + vocab * ((n + 4095) // 4096 + 1) * 4
+    shuffled = docs.copy()
+    lo, hi = int(offsets[0]), int(offsets[1])
+    assert hi - lo >= 2
+    shuffled[lo:hi] = shuffled[lo:hi][::-1]
+    unsorted = zc.LexicalIndex.from_csr(offsets, shuffled, weights, n)
+    assert not unsorted.postings_sorted and not unsorted.has_slice_table
+    assert unsorted.device_bytes == (vocab + 1) * 8 + postings * 8
+
+
 def test_graph_replay_is_bit_identical(zc, tmp_path):
     n, dim, k = 50_000, 256, 32
     corpus = normalized(n, dim, 11)

@@ -247,23 +247,84 @@ def test_hybrid_sweep_matches_unsorted_scatter(gpu):
     half = oracle.f32_to_f16(normalized(n, dim, 23))
     queries = normalized(batch, dim, 24)
     d_half = capi.DeviceArray.from_host(half)
+    d_offsets, d_docs = capi.DeviceArray.from_host(offsets), capi.DeviceArray.from_host(docs)
+    table = _slice_table(capi, d_offsets, d_docs, vocab, n)
     results = []
-    for doc_array, weight_array, flags in ((docs, weights, capi.SEARCH_SORTED_POSTINGS),
-                                           (shuffled_docs, shuffled_weights, 0)):
+    for doc_array, weight_array, flags, slices in ((docs, weights, capi.SEARCH_SORTED_POSTINGS, None),
+                                                   (shuffled_docs, shuffled_weights, 0, None),
+                                                   (docs, weights, capi.SEARCH_SORTED_POSTINGS, table)):
         results.append(run_search(capi, d_half, n, dim, capi.F16, queries, k,
-                                  lex_offsets=capi.DeviceArray.from_host(offsets),
-                                  lex_docs=capi.DeviceArray.from_host(doc_array),
+                                  lex_offsets=d_offsets, lex_docs=capi.DeviceArray.from_host(doc_array),
                                   lex_weights=capi.DeviceArray.from_host(weight_array), lex_doc_count=n,
                                   lex_vocab_size=vocab, query_terms=capi.DeviceArray.from_host(terms),
-                                  lexical_stride=8, dense_weight=w, flags=flags))
-    assert np.array_equal(results[0][0], results[1][0])
-    assert np.array_equal(results[0][1], results[1][1])
+                                  lexical_stride=8, dense_weight=w, flags=flags, lex_slice_table=slices))
+    for other in results[1:]:
+        assert np.array_equal(results[0][0], other[0])
+        assert np.array_equal(results[0][1], other[1])
     decoded = half.astype(np.float32)
     dense = oracle.scores_f32(decoded, queries, 0)
     fused = np.empty_like(dense)
     known = np.where(terms < vocab, terms, -1)  # the search skips ids past the vocabulary
     for b in range(batch):
         lex = oracle.bm25(offsets, docs, weights, known[b], n)
+        fused[b] = oracle.fuse(dense[b], lex, oracle.max_positive(lex), w)
+    tol = np.float32(w) * float_tolerance(queries, decoded, 0) + 1e-6
+    assert_topk_equivalent(results[0][0], results[0][1], fused, k, tol)
+
+
+def _slice_table(capi, d_offsets, d_docs, vocab, doc_count):
+    table = capi.DeviceArray(capi.lexical_slice_table_bytes(vocab, doc_count) // 4, np.uint32)
+    capi.build_lexical_slice_table(d_offsets, d_docs, vocab, doc_count, table)
+    capi.synchronize()
+    return table
+
+
+def test_lexical_slice_table_counts(gpu):
+    # Entry (t, c) counts term t's postings below document c * 4096, the last column those below
+    # doc_count: numpy's searchsorted over each term's ascending documents gives every entry.
+    capi = gpu
+    n, vocab = 70_001, 30_000
+    offsets, docs, _, _ = zipf_lexical_index(n, vocab, 31)
+    stride = (n + 4095) // 4096 + 1
+    assert capi.lexical_slice_table_bytes(vocab, n) == vocab * stride * 4
+    table = _slice_table(capi, capi.DeviceArray.from_host(offsets), capi.DeviceArray.from_host(docs), vocab, n)
+    got = table.to_host().reshape(vocab, stride)
+    bounds = np.append(np.arange(stride - 1, dtype=np.int64) * 4096, n)
+    expected = np.empty((vocab, stride), np.uint32)
+    for t in range(vocab):
+        expected[t] = np.searchsorted(docs[offsets[t]:offsets[t + 1]], bounds, side="left")
+    assert np.array_equal(got, expected)
+    assert got[:, -1].astype(np.int64).sum() == offsets[-1]  # every posting names a document < n
+
+
+def test_slice_table_of_a_larger_index(gpu):
+    # An index over more documents than the corpus scans: its table's slices run to the index's
+    # own count, so the corpus's partial last slice takes postings of documents past the corpus,
+    # which the BM25 stage skips. Results equal the per-call bounds search and the oracle over
+    # the corpus's documents.
+    capi = gpu
+    n_index, n, vocab, dim, batch, k, w = 70_001, 61_500, 30_000, 256, 6, 10, 0.5
+    offsets, docs, weights, p = zipf_lexical_index(n_index, vocab, 41)
+    rng = np.random.default_rng(42)
+    terms = np.stack([rng.choice(vocab, size=8, replace=False, p=p) for _ in range(batch)]).astype(np.int32)
+    half = oracle.f32_to_f16(normalized(n, dim, 43))
+    queries = normalized(batch, dim, 44)
+    d_offsets, d_docs = capi.DeviceArray.from_host(offsets), capi.DeviceArray.from_host(docs)
+    table = _slice_table(capi, d_offsets, d_docs, vocab, n_index)
+    d_half = capi.DeviceArray.from_host(half)
+    results = [run_search(capi, d_half, n, dim, capi.F16, queries, k, lex_offsets=d_offsets, lex_docs=d_docs,
+                          lex_weights=capi.DeviceArray.from_host(weights), lex_doc_count=n_index,
+                          lex_vocab_size=vocab, query_terms=capi.DeviceArray.from_host(terms),
+                          lexical_stride=8, dense_weight=w, flags=capi.SEARCH_SORTED_POSTINGS,
+                          lex_slice_table=slices)
+               for slices in (table, None)]
+    assert np.array_equal(results[0][0], results[1][0])
+    assert np.array_equal(results[0][1], results[1][1])
+    decoded = half.astype(np.float32)
+    dense = oracle.scores_f32(decoded, queries, 0)
+    fused = np.empty_like(dense)
+    for b in range(batch):
+        lex = oracle.bm25(offsets, docs, weights, terms[b], n)
         fused[b] = oracle.fuse(dense[b], lex, oracle.max_positive(lex), w)
     tol = np.float32(w) * float_tolerance(queries, decoded, 0) + 1e-6
     assert_topk_equivalent(results[0][0], results[0][1], fused, k, tol)

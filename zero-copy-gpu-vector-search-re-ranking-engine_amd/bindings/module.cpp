@@ -222,7 +222,11 @@ PYBIND11_MODULE(zcgvs_engine, module) {
         .def_property_readonly("vocab_size", &zcgvs::LexicalIndex::vocabSize)
         .def_property_readonly("k1", &zcgvs::LexicalIndex::k1)
         .def_property_readonly("b", &zcgvs::LexicalIndex::b)
-        .def_property_readonly("avg_doc_len", &zcgvs::LexicalIndex::averageDocLength);
+        .def_property_readonly("avg_doc_len", &zcgvs::LexicalIndex::averageDocLength)
+        .def_property_readonly("postings_sorted", &zcgvs::LexicalIndex::postingsSorted)
+        .def_property_readonly("has_slice_table",
+                               [](const zcgvs::LexicalIndex& index) { return index.deviceSliceTable() != nullptr; })
+        .def_property_readonly("device_bytes", &zcgvs::LexicalIndex::deviceBytes);
 
     module.def("write_metadata", &zcgvs::Corpus::saveMetadata, py::arg("path"), py::arg("ids"), py::arg("texts"));
 

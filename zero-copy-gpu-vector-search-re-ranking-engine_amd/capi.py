@@ -53,7 +53,8 @@ class SearchDesc(ctypes.Structure):
                 ("k", _i32), ("metric", _i32), ("int8_mode", _i32), ("mask", _vp),
                 ("rescore_candidates", _i32), ("lex_offsets", _vp), ("lex_docs", _vp),
                 ("lex_weights", _vp), ("lex_doc_count", _i64), ("lex_vocab_size", _i32), ("query_terms", _vp),
-                ("lexical_stride", _i32), ("dense_weight", _f32), ("flags", _i32)]
+                ("lexical_stride", _i32), ("dense_weight", _f32), ("flags", _i32),
+                ("lex_slice_table", _vp)]
 
 
 # name -> (restype, argtypes)
@@ -102,6 +103,8 @@ _SIGNATURES = {
     "zcgvs_launch_remap_indices": (_i32, [_vp, _vp, _i32, _i32, _i32, _vp, _vp]),
     "zcgvs_launch_bm25": (_i32, [_vp, _vp, _vp, _vp, _i32, _i32, _vp, _vp]),
     "zcgvs_launch_bm25_batched": (_i32, [_vp, _vp, _vp, _vp, _i32, _i32, _i32, _vp, _vp]),
+    "zcgvs_lexical_slice_table_bytes": (_sz, [_i32, _i64]),
+    "zcgvs_build_lexical_slice_table": (_i32, [_vp, _vp, _i32, _i64, _vp, _vp]),
     "zcgvs_launch_max_positive": (_i32, [_vp, _i32, _vp, _vp]),
     "zcgvs_launch_fuse_scores": (_i32, [_vp, _vp, _vp, _f32, _i32, _vp]),
     "zcgvs_launch_convert_f32_to_f16": (_i32, [_vp, _vp, _sz, _vp]),
@@ -365,6 +368,19 @@ def launch_bm25_batched(offsets, docs, weights, terms, stride, batch, n, scores,
          n, ptr(scores), getattr(stream, "handle", stream))
 
 
+def lexical_slice_table_bytes(vocab_size, doc_count) -> int:
+    """Bytes of the slice table of an index of `vocab_size` terms over `doc_count` documents
+    (0 for an empty index or more than 2^31 - 1 documents)."""
+    return int(library().zcgvs_lexical_slice_table_bytes(vocab_size, doc_count))
+
+
+def build_lexical_slice_table(offsets, docs, vocab_size, doc_count, table, stream=None):
+    """Fills `table` (lexical_slice_table_bytes of device memory, uint32) with, for every term
+    and 4096-document boundary, the number of the term's postings below it (sorted postings)."""
+    call("zcgvs_build_lexical_slice_table", ptr(offsets), ptr(docs), vocab_size, doc_count, ptr(table),
+         getattr(stream, "handle", stream))
+
+
 def launch_max_positive(values, count, out, stream=None):
     call("zcgvs_launch_max_positive", ptr(values), count, ptr(out), getattr(stream, "handle", stream))
 
@@ -415,15 +431,15 @@ def store_desc(data=None, doc_count=0, dim=0, dtype=F32, scale=1.0, row_scales=N
 def search_desc(corpus: StoreDesc, queries, batch, k, metric=COSINE, *, int8_mode=INT8_REFERENCE,
                 mask=None, rescore: StoreDesc | None = None, rescore_candidates=0, lex_offsets=None,
                 lex_docs=None, lex_weights=None, lex_doc_count=0, lex_vocab_size=0, query_terms=None,
-                lexical_stride=0, dense_weight=1.0, flags=0) -> SearchDesc:
+                lexical_stride=0, dense_weight=1.0, flags=0, lex_slice_table=None) -> SearchDesc:
     desc = SearchDesc(corpus, rescore if rescore is not None else StoreDesc(), ptr(queries), batch, k,
                       metric, int8_mode, ptr(mask), rescore_candidates, ptr(lex_offsets), ptr(lex_docs),
                       ptr(lex_weights), lex_doc_count, lex_vocab_size, ptr(query_terms), lexical_stride,
-                      dense_weight, flags)
+                      dense_weight, flags, ptr(lex_slice_table))
     # the nested StoreDesc fields are copied by value: carry their owners over as well
     return _keep_alive(desc, *getattr(corpus, "_owners", []),
                        *(getattr(rescore, "_owners", []) if rescore is not None else []),
-                       queries, mask, lex_offsets, lex_docs, lex_weights, query_terms)
+                       queries, mask, lex_offsets, lex_docs, lex_weights, query_terms, lex_slice_table)
 
 
 def search_workspace_bytes(desc: SearchDesc) -> int:

@@ -15,7 +15,10 @@
 // all at once), and bm25SweepKernel, one workgroup per (query, slice), loads its slice of every
 // term's postings, adds them into an LDS accumulator slot by slot in slot order (the same
 // per-document order), then writes the slice, zeros included, and folds its maximum into the
-// query's.
+// query's. An index may also carry a slice table (built once, zcgvs_build_lexical_slice_table):
+// for every term, the number of its postings below each 4096-document boundary, so a search
+// gathers its terms' slice bounds from it (two loads) instead of binary-searching the postings
+// (about twenty dependent loads per bound).
 #include <hip/hip_runtime.h>
 
 #include <algorithm>
@@ -91,13 +94,34 @@ __device__ __forceinline__ std::int64_t lowerBound(const int* __restrict__ docs,
     return lo;
 }
 
+// table[t * table_stride + c] = the number of term t's postings whose document is below
+// c * kSweepDocs (c = table_stride - 1: below the index's doc_count). One thread per entry.
+__global__ void sliceTableKernel(const std::int64_t* __restrict__ offsets, const int* __restrict__ docs,
+                                 int vocab_size, std::int64_t doc_count, int table_stride,
+                                 std::uint32_t* __restrict__ table) {
+    const long long i = static_cast<long long>(blockIdx.x) * blockDim.x + threadIdx.x;
+    if (i >= static_cast<long long>(vocab_size) * table_stride) {
+        return;
+    }
+    const int c = static_cast<int>(i % table_stride);
+    const int term = static_cast<int>(i / table_stride);
+    const std::int64_t lo = offsets[term];
+    const long long target = c == table_stride - 1 ? doc_count : static_cast<long long>(c) * kSweepDocs;
+    const int bound = static_cast<int>(min(target, static_cast<long long>(INT32_MAX)));
+    table[i] = static_cast<std::uint32_t>(lowerBound(docs, lo, offsets[term + 1], bound) - lo);
+}
+
 // bounds[(q * term_stride + slot) * (slices + 1) + c] = first posting of the term in slot `slot`
 // of query q whose document is >= c * kSweepDocs (c = slices: >= doc_count); an unknown term
-// gets 0 everywhere (an empty range). One thread per entry, so all searches run at once. Also
-// zeroes lexical_max[0, batch) (there are at least batch entries: slices + 1 >= 2, term_stride >= 1).
+// gets 0 everywhere (an empty range). One thread per entry, so all searches run at once. With
+// a slice table the entry is gathered from it instead (for c = slices its count may include
+// postings of documents from doc_count up to the index's own count, inside the last slice's
+// document range; the sweep skips them). Also zeroes lexical_max[0, batch) (there are at least
+// batch entries: slices + 1 >= 2, term_stride >= 1).
 __global__ void bm25BoundsKernel(const std::int64_t* __restrict__ offsets, const int* __restrict__ docs,
                                  const int* __restrict__ query_terms, int term_stride, int batch,
                                  int doc_count, int vocab_size, int slices,
+                                 const std::uint32_t* __restrict__ table, int table_stride,
                                  std::int64_t* __restrict__ bounds, float* __restrict__ lexical_max) {
     const long long total = static_cast<long long>(batch) * term_stride * (slices + 1);
     const long long i = static_cast<long long>(blockIdx.x) * blockDim.x + threadIdx.x;
@@ -112,8 +136,12 @@ __global__ void bm25BoundsKernel(const std::int64_t* __restrict__ offsets, const
     const int term = query_terms[qs];
     std::int64_t position = 0;
     if (term >= 0 && term < vocab_size) {
-        position = lowerBound(docs, offsets[term], offsets[term + 1],
-                              c == slices ? doc_count : c * kSweepDocs);
+        if (table != nullptr) {
+            position = offsets[term] + table[static_cast<std::size_t>(term) * table_stride + c];
+        } else {
+            position = lowerBound(docs, offsets[term], offsets[term + 1],
+                                  c == slices ? doc_count : c * kSweepDocs);
+        }
     }
     bounds[i] = position;
 }
@@ -322,15 +350,22 @@ std::size_t lexicalBoundsBytes(int batch, int term_stride, int doc_count) {
            static_cast<std::size_t>(slices + 1) * sizeof(std::int64_t);
 }
 
+int lexicalSliceTableStride(std::int64_t doc_count) {
+    return static_cast<int>((doc_count + kSweepDocs - 1) / kSweepDocs) + 1;
+}
+
 int launchLexicalScores(const std::int64_t* offsets, const int* docs, const float* weights,
                         int vocab_size, const int* query_terms, int term_stride, int batch,
                         int doc_count, float* lexical, float* lexical_max, std::int64_t* bounds,
+                        const std::uint32_t* slice_table, std::int64_t index_doc_count,
                         hipStream_t stream) {
     if (bounds != nullptr) {
         const int slices = (doc_count + kSweepDocs - 1) / kSweepDocs;
         const long long entries = static_cast<long long>(batch) * term_stride * (slices + 1);
+        const int table_stride = slice_table != nullptr ? lexicalSliceTableStride(index_doc_count) : 0;
         bm25BoundsKernel<<<static_cast<unsigned>((entries + 255) / 256), 256, 0, stream>>>(
-            offsets, docs, query_terms, term_stride, batch, doc_count, vocab_size, slices, bounds, lexical_max);
+            offsets, docs, query_terms, term_stride, batch, doc_count, vocab_size, slices, slice_table,
+            table_stride, bounds, lexical_max);
         ZCGVS_LAUNCH_CHECK("bm25 bounds");
         // queries per launch: the grid's threads stay below 2^31
         const long long per_query = static_cast<long long>((slices + kXcds - 1) / kXcds) * kXcds;
@@ -394,6 +429,33 @@ int zcgvs_launch_bm25_batched(const std::int64_t* d_offsets, const int* d_docs,
             d_scores);
     }
     ZCGVS_LAUNCH_CHECK("bm25");
+    return clearError();
+}
+
+size_t zcgvs_lexical_slice_table_bytes(int vocab_size, int64_t doc_count) {
+    if (vocab_size <= 0 || doc_count <= 0 || doc_count > INT32_MAX) {
+        return 0;
+    }
+    return static_cast<std::size_t>(vocab_size) * static_cast<std::size_t>(lexicalSliceTableStride(doc_count)) *
+           sizeof(std::uint32_t);
+}
+
+int zcgvs_build_lexical_slice_table(const int64_t* d_offsets, const int* d_docs, int vocab_size,
+                                    int64_t doc_count, uint32_t* d_table, zcgvs_stream_t stream) {
+    if (vocab_size <= 0 || doc_count <= 0 || doc_count > INT32_MAX) {
+        return setError(ZCGVS_ERR_INVALID_ARGUMENT, "zcgvs slice table: empty index or too many documents");
+    }
+    if (d_offsets == nullptr || d_docs == nullptr || d_table == nullptr) {
+        return setError(ZCGVS_ERR_INVALID_ARGUMENT, "zcgvs slice table: null device pointer");
+    }
+    const int stride = lexicalSliceTableStride(doc_count);
+    const long long entries = static_cast<long long>(vocab_size) * stride;
+    if (entries > (1LL << 31) - 256) {
+        return setError(ZCGVS_ERR_INVALID_ARGUMENT, "zcgvs slice table: too many entries for one launch");
+    }
+    sliceTableKernel<<<static_cast<unsigned>((entries + 255) / 256), 256, 0, toStream(stream)>>>(
+        d_offsets, d_docs, vocab_size, doc_count, stride, d_table);
+    ZCGVS_LAUNCH_CHECK("slice table");
     return clearError();
 }
 

@@ -210,6 +210,13 @@ Plan validate(const zcgvs_search_desc& d) {
             return fail(ZCGVS_ERR_INVALID_ARGUMENT,
                         "zcgvs: lexical index holds fewer documents than the corpus");
         }
+        if (d.lex_slice_table != nullptr && (d.flags & ZCGVS_SEARCH_SORTED_POSTINGS) == 0) {
+            return fail(ZCGVS_ERR_INVALID_ARGUMENT,
+                        "zcgvs: a lexical slice table needs ZCGVS_SEARCH_SORTED_POSTINGS");
+        }
+        if (d.lex_slice_table != nullptr && d.lex_doc_count > INT32_MAX) {
+            return fail(ZCGVS_ERR_INVALID_ARGUMENT, "zcgvs: a lexical slice table covers at most 2^31 - 1 documents");
+        }
     }
     return plan;
 }
@@ -583,7 +590,7 @@ int runMaterialized(const zcgvs_search_desc& d, const Plan& plan, std::uint8_t* 
         status = launchLexicalScores(d.lex_offsets, d.lex_docs, d.lex_weights, d.lex_vocab_size, d.query_terms,
                                      d.lexical_stride, batch, n, lexical, lexmax,
                                      plan.lex_sorted ? at<std::int64_t>(ws, plan.lexbounds) : nullptr,
-                                     stream);
+                                     d.lex_slice_table, d.lex_doc_count, stream);
         if (status != ZCGVS_OK) {
             return status;
         }
@@ -808,7 +815,8 @@ int searchTopk(const zcgvs_search_desc* desc, void* d_workspace, std::size_t wor
         status = launchLexicalScores(d.lex_offsets, d.lex_docs, d.lex_weights, d.lex_vocab_size, d.query_terms,
                                      d.lexical_stride, batch, static_cast<int>(d.corpus.doc_count),
                                      at<float>(ws, plan.lex), at<float>(ws, plan.lexmax),
-                                     plan.lex_sorted ? at<std::int64_t>(ws, plan.lexbounds) : nullptr, s);
+                                     plan.lex_sorted ? at<std::int64_t>(ws, plan.lexbounds) : nullptr,
+                                     d.lex_slice_table, d.lex_doc_count, s);
         if (status != ZCGVS_OK) {
             return status;
         }

@@ -77,6 +77,13 @@ LexicalIndex LexicalIndex::fromHostCsr(const std::int64_t* offsets, const int* d
         upload(docs, index.posting_docs_.data(), index.posting_docs_.bytes());
         upload(weights, index.posting_weights_.data(), index.posting_weights_.bytes());
     }
+    // Sorted postings get the slice table the device BM25 stage reads its slice bounds from.
+    const std::size_t table_bytes = zcgvs_lexical_slice_table_bytes(vocab_size, doc_count);
+    if (sorted && nnz > 0 && table_bytes > 0) {
+        index.slice_table_.allocate(table_bytes / sizeof(std::uint32_t));
+        check(zcgvs_build_lexical_slice_table(index.offsets_.data(), index.posting_docs_.data(), vocab_size,
+                                              doc_count, index.slice_table_.data(), nullptr));
+    }
     check(zcgvs_device_synchronize());
     return index;
 }

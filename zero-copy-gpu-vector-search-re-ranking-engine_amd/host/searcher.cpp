@@ -166,6 +166,7 @@ zcgvs_search_desc Searcher::describe(const float* queries, int batch, const Sear
         desc.lex_vocab_size = lexical_index_->vocabSize();
         if (lexical_index_->postingsSorted()) {  // checked when the index was loaded
             desc.flags |= ZCGVS_SEARCH_SORTED_POSTINGS;
+            desc.lex_slice_table = lexical_index_->deviceSliceTable();
         }
         desc.query_terms = d_query_terms_.data();
         desc.lexical_stride = params.lexical_stride;
