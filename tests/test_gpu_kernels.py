@@ -107,6 +107,8 @@ def test_similarity_i8i8_bit_exact(gpu):
     (50000, 1024, 3, True),      # heavy ties: lowest index must win
     (4096, 64, 11, False),       # batched (tests/cpp/test_batched.cu)
     (700, 700, 2, True),         # k == n
+    (300_001, 1000, 2, True),    # tile winners merged in groups first; partial last tile; ties
+    (1_000_000, 10, 2, False),   # 123 tiles, one merge of their winners
 ])
 def test_topk_exact(gpu, n, k, batch, quantized):
     capi = gpu

@@ -4,8 +4,9 @@
 // The reference sorts 1024-score tiles with a bitonic network and merges tile winners
 // recursively; ties fall wherever the network puts them. Here the selection is an exact radix
 // select on unique 64-bit keys (select.hpp), so the result is the stable (score desc, index asc)
-// order of tests/cpp/cpu_reference.hpp:26-34 on every run. Each pass reads the scores once; the
-// block that finishes a pass last picks the bucket (no host round trip, capture safe).
+// order of tests/cpp/cpu_reference.hpp:26-34 on every run. zcgvs_launch_topk reads the scores
+// once: each block selects the best k of a tile of 8192-16384 scores in LDS, and one block per
+// query merges the tile winners (two launches, no host round trip, capture safe).
 #include <hip/hip_runtime.h>
 
 #include <algorithm>
@@ -20,148 +21,126 @@ namespace {
 
 constexpr int kTileSize = 1024;      // reference tile (topk.cu:17), kept for the sizing helpers
 constexpr int kMergeTile = 4096;     // reference merge tile (topk.cu:18)
-constexpr int kStateWords = 16;      // SelectState, padded
-constexpr int kMinScratchElements = kStateWords + kSelectBins + 16;
+constexpr int kMinScratchElements = 16 + kSelectBins + 16;
+constexpr int kTopkTileMax = 16384;  // scores one block of zcgvs_launch_topk selects from (128 KB of keys)
 
-struct TopKScratch {
-    __host__ __device__ SelectState* state(int q) const {
-        return reinterpret_cast<SelectState*>(base + static_cast<std::size_t>(q) * stride);
+// Scores per tile of zcgvs_launch_topk: the smallest of 8192, 12288 and 16384 whose tile winners (k
+// per tile) fit the merge's LDS gather; 16384 when none does (the merge then reads the winners
+// from global memory).
+long long topkTileScores(long long doc_count, int k) {
+    for (const long long tile : {8192LL, 12288LL, static_cast<long long>(kTopkTileMax)}) {
+        if ((doc_count + tile - 1) / tile * k <= static_cast<long long>(kSelectLdsKeys)) {
+            return tile;
+        }
     }
-    __host__ __device__ std::uint32_t* hist(int q) const {
-        return base + static_cast<std::size_t>(q) * stride + kStateWords;
-    }
-    std::uint32_t* base;
-    std::size_t stride;  // u32 words per query
-};
-
-struct KeyScratch {
-    __host__ __device__ std::uint64_t* keys(int q) const {
-        return reinterpret_cast<std::uint64_t*>(base + static_cast<std::size_t>(q) * stride);
-    }
-    std::uint32_t* base;
-    std::size_t stride;  // u32 words per query (even)
-};
-
-__global__ void topkInitKernel(TopKScratch scratch, int k) {
-    const int q = blockIdx.x;
-    std::uint32_t* hist = scratch.hist(q);
-    for (int i = threadIdx.x; i < kSelectBins; i += blockDim.x) {
-        hist[i] = 0u;
-    }
-    if (threadIdx.x == 0) {
-        SelectState* s = scratch.state(q);
-        s->prefix = 0ull;
-        s->bits = 0u;
-        s->need = static_cast<std::uint32_t>(k);
-        s->done = 0u;
-        s->arrived = 0u;
-        s->count = 0u;
-    }
+    return kTopkTileMax;
 }
 
-__global__ __launch_bounds__(kSelectThreads) void topkHistKernel(const float* __restrict__ scores,
-                                                                 int doc_count, int pass,
-                                                                 TopKScratch scratch) {
+// Block (t, q) of zcgvs_launch_topk: the keys of scores [t * tile, t * tile + n) of query q
+// (n <= tile) go to LDS, their best min(k, n) are found by radix passes over the LDS keys
+// (select.hpp), and written, in no particular order, to winners[q * stride + t * k + 0..k); the
+// rest of the k slots get key 0 (no candidate).
+__global__ __launch_bounds__(kMergeThreads) void topkTileKernel(const float* __restrict__ scores, int doc_count,
+                                                                int tile, int k, std::uint64_t* __restrict__ winners,
+                                                                std::size_t stride) {
+    __shared__ std::uint64_t lds_keys[kTopkTileMax];
     __shared__ std::uint32_t lds_hist[kSelectBins];
-    __shared__ std::uint32_t lds_scan[kSelectThreads];
+    __shared__ std::uint32_t lds_scan[kMergeThreads / kWave];
+    __shared__ std::uint64_t lds_wave_lo[kMergeThreads / kWave];
+    __shared__ std::uint64_t lds_wave_hi[kMergeThreads / kWave];
     __shared__ SelectState lds_state;
-    __shared__ int is_last;
 
+    const int t = threadIdx.x;
     const int q = blockIdx.y;
-    SelectState* state = scratch.state(q);
-    if (threadIdx.x == 0) {
-        lds_state = *state;
-    }
-    for (int i = threadIdx.x; i < kSelectBins; i += blockDim.x) {
-        lds_hist[i] = 0u;
-    }
-    __syncthreads();
-    if (lds_state.done) {
+    const long long first = static_cast<long long>(blockIdx.x) * tile;
+    std::uint64_t* out = winners + static_cast<std::size_t>(q) * stride + static_cast<std::size_t>(blockIdx.x) * k;
+    if (first >= doc_count) {  // a padding tile of the group layout: no candidates
+        for (int i = t; i < k; i += blockDim.x) {
+            out[i] = 0ull;
+        }
         return;
     }
-    const int width = selectDigitWidth(pass);
-    const std::uint32_t bits = lds_state.bits;
-    const std::uint64_t prefix = lds_state.prefix;
-    const int shift = 64 - static_cast<int>(bits) - width;
-    const std::uint64_t digit_mask = (1ull << width) - 1ull;
-    const float* row = scores + static_cast<std::size_t>(q) * doc_count;
-    for (long long i = static_cast<long long>(blockIdx.x) * blockDim.x + threadIdx.x;
-         i < doc_count; i += static_cast<long long>(gridDim.x) * blockDim.x) {
-        const std::uint64_t key = makeKey(row[i], static_cast<std::uint32_t>(i));
-        if (bits == 0u || (key >> (64 - bits)) == prefix) {
-            atomicAdd(&lds_hist[(key >> shift) & digit_mask], 1u);
-        }
+    const std::uint32_t n = static_cast<std::uint32_t>(min(static_cast<long long>(tile), doc_count - first));
+    const float* row = scores + static_cast<std::size_t>(q) * doc_count + first;
+    std::uint64_t lo = ~0ull;
+    std::uint64_t hi = 0ull;
+    gatherRounds(n, [&](std::uint32_t i) { return makeKey(row[i], static_cast<std::uint32_t>(first + i)); },
+                 [&](std::uint32_t i, std::uint64_t key) {
+                     lds_keys[i] = key;
+                     lo = min(lo, key);
+                     hi = max(hi, key);
+                 });
+    // smallest and largest key of the tile: the radix passes start below the bits they share
+    lo = waveReduce64(lo, [](std::uint64_t x, std::uint64_t y) { return min(x, y); });
+    hi = waveReduce64(hi, [](std::uint64_t x, std::uint64_t y) { return max(x, y); });
+    if ((t & (kWave - 1)) == 0) {
+        lds_wave_lo[t / kWave] = lo;
+        lds_wave_hi[t / kWave] = hi;
     }
-    __syncthreads();
-    std::uint32_t* hist = scratch.hist(q);
-    for (int b = threadIdx.x; b < (1 << width); b += blockDim.x) {
-        if (lds_hist[b] != 0u) {
-            atomicAdd(&hist[b], lds_hist[b]);
-        }
-    }
-    __threadfence();
-    __syncthreads();
-    if (threadIdx.x == 0) {
-        const std::uint32_t ticket = atomicAdd(&state->arrived, 1u);
-        is_last = (ticket == gridDim.x - 1) ? 1 : 0;
-    }
-    __syncthreads();
-    if (!is_last) {
-        return;
-    }
-    __threadfence();
-    for (int b = threadIdx.x; b < (1 << width); b += blockDim.x) {
-        lds_hist[b] = __hip_atomic_load(&hist[b], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-        hist[b] = 0u;
-    }
-    __syncthreads();
-    selectPickBucket(lds_hist, width, &lds_state, lds_scan);
-    if (threadIdx.x == 0) {
-        lds_state.arrived = 0u;
-        *state = lds_state;
-    }
-    __threadfence();
-}
-
-__global__ __launch_bounds__(kSelectThreads) void topkCollectKernel(
-    const float* __restrict__ scores, int doc_count, int k, TopKScratch scratch, KeyScratch out) {
-    const int q = blockIdx.y;
-    SelectState* state = scratch.state(q);
-    const std::uint64_t threshold = selectThreshold(*state);
-    std::uint64_t* keys = out.keys(q);
-    const float* row = scores + static_cast<std::size_t>(q) * doc_count;
-    for (long long i = static_cast<long long>(blockIdx.x) * blockDim.x + threadIdx.x;
-         i < doc_count; i += static_cast<long long>(gridDim.x) * blockDim.x) {
-        const std::uint64_t key = makeKey(row[i], static_cast<std::uint32_t>(i));
-        if (key >= threshold) {
-            const std::uint32_t slot = atomicAdd(&state->count, 1u);
-            if (slot < static_cast<std::uint32_t>(k)) {  // exactly k keys pass; guard anyway
-                keys[slot] = key;
+    __syncthreads();  // (also: the keys are in LDS)
+    if (t < kWave) {
+        constexpr int kSlots = kMergeThreads / kWave;
+        std::uint64_t l = t < kSlots ? lds_wave_lo[t] : ~0ull;
+        std::uint64_t h = t < kSlots ? lds_wave_hi[t] : 0ull;
+        l = waveReduce64(l, [](std::uint64_t x, std::uint64_t y) { return min(x, y); });
+        h = waveReduce64(h, [](std::uint64_t x, std::uint64_t y) { return max(x, y); });
+        if (t == 0) {
+            lds_state.prefix = 0ull;
+            lds_state.bits = 0u;
+            lds_state.need = min(n, static_cast<std::uint32_t>(k));
+            lds_state.done = n <= static_cast<std::uint32_t>(k) ? 1u : 0u;
+            lds_state.count = 0u;
+            if (n > static_cast<std::uint32_t>(k)) {  // at least two distinct keys
+                const int common = __clzll(h ^ l);
+                lds_state.prefix = common == 0 ? 0ull : (h >> (64 - common));
+                lds_state.bits = static_cast<std::uint32_t>(common);
             }
         }
     }
-}
-
-__global__ __launch_bounds__(kSelectThreads) void topkSortKernel(TopKScratch scratch,
-                                                                 KeyScratch in, int k,
-                                                                 int* __restrict__ out_index,
-                                                                 float* __restrict__ out_score) {
-    __shared__ std::uint64_t lds_keys[kMaxK];
-    const int q = blockIdx.x;
-    const std::uint32_t count = min(min(scratch.state(q)->count, static_cast<std::uint32_t>(kMaxK)),
-                                    static_cast<std::uint32_t>(k));
-    const std::uint64_t* keys = in.keys(q);
-    for (std::uint32_t i = threadIdx.x; i < count; i += blockDim.x) {
-        lds_keys[i] = keys[i];
+    __syncthreads();
+    for (int pass = 0; pass < kSelectPasses && !lds_state.done; ++pass) {
+        const int width = min(11, 64 - static_cast<int>(lds_state.bits));
+        for (int i = t; i < (1 << width); i += blockDim.x) {
+            lds_hist[i] = 0u;
+        }
+        __syncthreads();
+        const std::uint32_t bits = lds_state.bits;
+        const std::uint64_t prefix = lds_state.prefix;
+        const int shift = 64 - static_cast<int>(bits) - width;
+        const std::uint64_t digit_mask = (1ull << width) - 1ull;
+        for (std::uint32_t i = static_cast<std::uint32_t>(t); i < n; i += blockDim.x) {
+            const std::uint64_t key = lds_keys[i];
+            if (bits == 0u || (key >> (64 - bits)) == prefix) {
+                atomicAdd(&lds_hist[(key >> shift) & digit_mask], 1u);
+            }
+        }
+        __syncthreads();
+        selectPickBucket<kMergeThreads>(lds_hist, width, &lds_state, lds_scan);  // (ends with a barrier)
+    }
+    // exactly min(n, k) keys reach the cut (keys are unique); one slot reservation per wavefront step
+    const std::uint64_t cut = n <= static_cast<std::uint32_t>(k) ? 1ull : selectThreshold(lds_state);
+    for (std::uint32_t base = 0; base < n; base += blockDim.x) {
+        const std::uint32_t i = base + static_cast<std::uint32_t>(t);
+        const std::uint64_t key = i < n ? lds_keys[i] : 0ull;
+        const bool take = key != 0ull && key >= cut;
+        const std::uint64_t mask = __builtin_amdgcn_ballot_w64(take);
+        if (mask != 0ull) {
+            std::uint32_t slot0 = 0u;
+            if ((t & (kWave - 1)) == 0) {
+                slot0 = atomicAdd(&lds_state.count, static_cast<std::uint32_t>(__builtin_popcountll(mask)));
+            }
+            slot0 = __builtin_amdgcn_readfirstlane(slot0);
+            const std::uint32_t slot = slot0 + __builtin_amdgcn_mbcnt_hi(static_cast<std::uint32_t>(mask >> 32),
+                                                                         __builtin_amdgcn_mbcnt_lo(static_cast<std::uint32_t>(mask), 0u));
+            if (take && slot < static_cast<std::uint32_t>(k)) {
+                out[slot] = key;
+            }
+        }
     }
     __syncthreads();
-    forEachRanked(lds_keys, count, [&](std::uint32_t rank, std::uint64_t key) {
-        const std::size_t o = static_cast<std::size_t>(q) * k + rank;
-        writeHit(key, &out_index[o], &out_score[o]);
-    });
-    for (int i = static_cast<int>(count) + threadIdx.x; i < k; i += blockDim.x) {
-        const std::size_t o = static_cast<std::size_t>(q) * k + i;
-        writeHit(0ull, &out_index[o], &out_score[o]);
+    const std::uint32_t taken = min(lds_state.count, static_cast<std::uint32_t>(k));
+    for (std::uint32_t i = taken + static_cast<std::uint32_t>(t); i < static_cast<std::uint32_t>(k); i += blockDim.x) {
+        out[i] = 0ull;
     }
 }
 
@@ -459,26 +438,53 @@ int zcgvs_launch_topk(const float* d_scores, int doc_count, int k, int batch, in
         d_scratch_values_a == nullptr || d_scratch_indices_a == nullptr) {
         return setError(ZCGVS_ERR_INVALID_ARGUMENT, "zcgvs top-k: null device pointer");
     }
-    const std::size_t elements = static_cast<std::size_t>(topkScratchElements(doc_count, k));
-    TopKScratch scratch{reinterpret_cast<std::uint32_t*>(d_scratch_values_a), elements & ~std::size_t(1)};
-    KeyScratch keys{reinterpret_cast<std::uint32_t*>(d_scratch_indices_a), elements & ~std::size_t(1)};
-    const hipStream_t s = toStream(stream);
-
-    const long long per_query_blocks = (static_cast<long long>(doc_count) + 8191) / 8192;
-    const long long budget = std::max(1LL, 4LL * deviceComputeUnits() / batch);
-    const unsigned tiles = static_cast<unsigned>(std::max(1LL, std::min(per_query_blocks, budget)));
-    const dim3 grid(tiles, static_cast<unsigned>(batch));
-
-    topkInitKernel<<<batch, kSelectThreads, 0, s>>>(scratch, k);
-    ZCGVS_LAUNCH_CHECK("top-k init");
-    for (int pass = 0; pass < kSelectPasses; ++pass) {
-        topkHistKernel<<<grid, kSelectThreads, 0, s>>>(d_scores, doc_count, pass, scratch);
-        ZCGVS_LAUNCH_CHECK("top-k histogram");
+    // Every tile's best k keys (topkTileKernel), then the per-query merge of the tile winners
+    // (merge.hpp), which writes the result in (score desc, index asc) order. When the winners of a
+    // query exceed the merge's LDS gather, groups of tiles are merged first, each (query, group)
+    // pair as a merge query of its own, and the group results after. Scratch b holds the winners,
+    // scratch a the group results or the final keys, scratch values b the final keys after
+    // groups; all fit the per-query size of topkScratchElements (at least 2k + 16 words and
+    // ceil(N / 1024) * k, against 2 * ceil(N / 8192) * k words of winners and 2 * 12 * k of groups).
+    const std::size_t elements = static_cast<std::size_t>(topkScratchElements(doc_count, k)) & ~std::size_t(1);
+    const long long tile = topkTileScores(doc_count, k);
+    const long long tiles = (doc_count + tile - 1) / tile;
+    const long long lds_keys = static_cast<long long>(kSelectLdsKeys);
+    const bool grouped = tiles * k > lds_keys;
+    // groups of tiles_per_group tiles (the last ones padded with empty tiles)
+    const long long groups = grouped ? std::min<long long>(tiles, std::max<long long>(2, lds_keys / k)) : 1;
+    const long long tiles_per_group = (tiles + groups - 1) / groups;
+    const long long padded = groups * tiles_per_group;
+    const std::size_t stride = static_cast<std::size_t>(padded) * static_cast<std::size_t>(k);  // winner keys per query
+    if (stride > elements / 2 || static_cast<std::size_t>(groups) * k > elements / 2 || padded > INT32_MAX ||
+        (grouped && (d_scratch_values_b == nullptr || 2 * static_cast<std::size_t>(k) > elements))) {
+        return setError(ZCGVS_ERR_RUNTIME, "zcgvs top-k: tile winners exceed the scratch");
     }
-    topkCollectKernel<<<grid, kSelectThreads, 0, s>>>(d_scores, doc_count, k, scratch, keys);
-    ZCGVS_LAUNCH_CHECK("top-k collect");
-    topkSortKernel<<<batch, kSelectThreads, 0, s>>>(scratch, keys, k, d_out_indices, d_out_values);
-    ZCGVS_LAUNCH_CHECK("top-k sort");
+    std::uint64_t* winners = reinterpret_cast<std::uint64_t*>(d_scratch_indices_a);
+    const hipStream_t s = toStream(stream);
+    topkTileKernel<<<dim3(static_cast<unsigned>(padded), static_cast<unsigned>(batch)), kMergeThreads, 0, s>>>(
+        d_scores, doc_count, static_cast<int>(tile), k, winners, stride);
+    ZCGVS_LAUNCH_CHECK("top-k tiles");
+    MergeInputs in;
+    in.dense = winners;
+    in.n_dense = tiles_per_group * k;
+    in.dense_stride = tiles_per_group * k;  // merge query q * groups + g: group g of query q
+    std::uint64_t* keys = reinterpret_cast<std::uint64_t*>(d_scratch_values_a);
+    if (grouped) {
+        const int status = launchSelectMerge(in, k, batch * static_cast<int>(groups), keys, nullptr, nullptr,
+                                             nullptr, nullptr, s);
+        if (status != ZCGVS_OK) {
+            return status;
+        }
+        in = MergeInputs{};
+        in.dense = keys;
+        in.n_dense = groups * k;
+        in.dense_stride = groups * k;
+        keys = reinterpret_cast<std::uint64_t*>(d_scratch_values_b);
+    }
+    const int status = launchSelectMerge(in, k, batch, keys, nullptr, nullptr, d_out_indices, d_out_values, s);
+    if (status != ZCGVS_OK) {
+        return status;
+    }
     return clearError();
 }
 
