@@ -171,7 +171,7 @@ def _ramp(n, dim, ascending):
 
 
 @pytest.mark.parametrize("ascending", [True, False])
-@pytest.mark.parametrize("k", [1, 32])
+@pytest.mark.parametrize("k", [1, 32, 100])
 def test_monotone_scores(gpu, ascending, k):
     capi = gpu
     n, dim = 400_000, 64
@@ -198,9 +198,10 @@ def test_small_corpora(gpu, n):
     assert_topk_equivalent(idx, val, oracle.scores_f32(corpus, queries), k, float_tolerance(queries, corpus, 0))
 
 
-def test_constant_scores_take_the_lowest_indices(gpu):
+@pytest.mark.parametrize("k", [32, 100])
+def test_constant_scores_take_the_lowest_indices(gpu, k):
     capi = gpu
-    n, dim, k = 300_000, 64, 32
+    n, dim = 300_000, 64
     corpus = np.zeros((n, dim), np.float32)
     corpus[:, 0] = 1.0
     query = np.zeros((1, dim), np.float32)

@@ -909,7 +909,7 @@ int searchTopk(const zcgvs_search_desc* desc, void* d_workspace, std::size_t wor
             }
         }
         in.reset_overflow = true;  // (segments hold at most width keys: the flags end cleared)
-        if (plan.sp_groups == 1 && plan.width <= kSortedMergeMaxK && in.n_seg <= kSortedMergeMaxSegments) {
+        if (plan.sp_groups == 1 && plan.width <= kSortedSelectMaxK && in.n_seg <= kSortedMergeMaxSegments) {
             // each workgroup's list is sorted (single_pass.hip): the merge reads at most width
             // segments past their first key
             status = launchSortedSegmentMerge(in, plan.width, batch, keys, overflow,

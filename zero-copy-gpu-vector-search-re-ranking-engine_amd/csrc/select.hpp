@@ -190,8 +190,11 @@ int launchSelectMerge(const MergeInputs& in, int k, int batch, std::uint64_t* ou
 // The same selection (segments only, no threshold) for candidate segments that each hold at most
 // k keys sorted descending, as the single-pass scan writes them: the k-th best segment head bounds
 // the result from below, so only the segments whose head reaches it (at most k) are read past
-// their first key. For k <= kSortedMergeMaxK and n_seg <= kSortedMergeMaxSegments.
+// their first key. For k <= kSortedSelectMaxK and n_seg <= kSortedMergeMaxSegments: up to
+// kSortedMergeMaxK the candidates are ranked by comparison, above it the best k of them are first
+// selected by radix passes in LDS (k * k candidates at most).
 constexpr int kSortedMergeMaxK = 32;
+constexpr int kSortedSelectMaxK = 110;  // 110 * 110 candidates fit the merge's 12288 LDS keys
 constexpr int kSortedMergeMaxSegments = 1024;
 int launchSortedSegmentMerge(const MergeInputs& in, int k, int batch, std::uint64_t* out_keys,
                              std::uint32_t* overflow, int* out_index, float* out_score, hipStream_t stream);

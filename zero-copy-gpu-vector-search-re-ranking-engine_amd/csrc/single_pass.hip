@@ -555,12 +555,14 @@ SinglePassShape singlePassShape(const ScanArgs& scan, int width) {
     if (cap - width < rows_per_step) {
         return shape;
     }
-    // Merge groups: one merge of every workgroup's list when the lists fit its LDS gather,
-    // otherwise groups of workgroups merged first (each group's lists in LDS, at most 8192 keys)
-    // and their results merged after.
+    // Merge groups: one merge of every workgroup's list when the lists fit its LDS gather or are
+    // sorted and at most kSortedSelectMaxK long (the sorted-segment merge reads only the lists
+    // whose first key can reach the result), otherwise groups of workgroups merged first (each
+    // group's lists in LDS, at most 8192 keys) and their results merged after.
     const int units = deviceComputeUnits();
     int groups = 1;
-    while (static_cast<long long>(units / groups) * width > (groups == 1 ? kSinglePassMergeKeys : 8192) &&
+    while (width > kSortedSelectMaxK &&
+           static_cast<long long>(units / groups) * width > (groups == 1 ? kSinglePassMergeKeys : 8192) &&
            groups < units) {
         groups *= 2;
     }

@@ -36,6 +36,96 @@ long long topkTileScores(long long doc_count, int k) {
     return kTopkTileMax;
 }
 
+// LDS of ldsSelectCut.
+struct LdsSelect {
+    std::uint32_t hist[kSelectBins];
+    std::uint32_t scan[kMergeThreads / kWave];
+    std::uint64_t wave_lo[kMergeThreads / kWave];
+    std::uint64_t wave_hi[kMergeThreads / kWave];
+    SelectState state;
+    std::uint32_t count;
+};
+
+// The best min(k, n) of the n unique non-zero keys keys[0..n) (in LDS) by radix passes over them
+// (select.hpp), run by a whole block of kMergeThreads threads; lo and hi are the calling thread's
+// smallest and largest key (the passes start below the bits all keys share). Returns the cut:
+// exactly min(k, n) keys are >= it (1 when n <= k). Ends with a barrier.
+__device__ std::uint64_t ldsSelectCut(const std::uint64_t* keys, std::uint32_t n, int k, std::uint64_t lo,
+                                      std::uint64_t hi, LdsSelect& lds) {
+    const int t = threadIdx.x;
+    lo = waveReduce64(lo, [](std::uint64_t x, std::uint64_t y) { return min(x, y); });
+    hi = waveReduce64(hi, [](std::uint64_t x, std::uint64_t y) { return max(x, y); });
+    if ((t & (kWave - 1)) == 0) {
+        lds.wave_lo[t / kWave] = lo;
+        lds.wave_hi[t / kWave] = hi;
+    }
+    __syncthreads();
+    if (t < kWave) {
+        constexpr int kSlots = kMergeThreads / kWave;
+        std::uint64_t l = t < kSlots ? lds.wave_lo[t] : ~0ull;
+        std::uint64_t h = t < kSlots ? lds.wave_hi[t] : 0ull;
+        l = waveReduce64(l, [](std::uint64_t x, std::uint64_t y) { return min(x, y); });
+        h = waveReduce64(h, [](std::uint64_t x, std::uint64_t y) { return max(x, y); });
+        if (t == 0) {
+            lds.state.prefix = 0ull;
+            lds.state.bits = 0u;
+            lds.state.need = min(n, static_cast<std::uint32_t>(k));
+            lds.state.done = n <= static_cast<std::uint32_t>(k) ? 1u : 0u;
+            if (n > static_cast<std::uint32_t>(k)) {  // at least two distinct keys
+                const int common = __clzll(h ^ l);
+                lds.state.prefix = common == 0 ? 0ull : (h >> (64 - common));
+                lds.state.bits = static_cast<std::uint32_t>(common);
+            }
+        }
+    }
+    __syncthreads();
+    for (int pass = 0; pass < kSelectPasses && !lds.state.done; ++pass) {
+        const int width = min(11, 64 - static_cast<int>(lds.state.bits));
+        for (int i = t; i < (1 << width); i += blockDim.x) {
+            lds.hist[i] = 0u;
+        }
+        __syncthreads();
+        const std::uint32_t bits = lds.state.bits;
+        const std::uint64_t prefix = lds.state.prefix;
+        const int shift = 64 - static_cast<int>(bits) - width;
+        const std::uint64_t digit_mask = (1ull << width) - 1ull;
+        for (std::uint32_t i = static_cast<std::uint32_t>(t); i < n; i += blockDim.x) {
+            const std::uint64_t key = keys[i];
+            if (bits == 0u || (key >> (64 - bits)) == prefix) {
+                atomicAdd(&lds.hist[(key >> shift) & digit_mask], 1u);
+            }
+        }
+        __syncthreads();
+        selectPickBucket<kMergeThreads>(lds.hist, width, &lds.state, lds.scan);  // (ends with a barrier)
+    }
+    return n <= static_cast<std::uint32_t>(k) ? 1ull : selectThreshold(lds.state);
+}
+
+// Appends the keys of keys[0..n) that are >= cut to out[0..) (one slot reservation per wavefront
+// step through lds.count, which the caller zeroes before a barrier), keeping at most `room`.
+__device__ void ldsCollect(const std::uint64_t* keys, std::uint32_t n, std::uint64_t cut, std::uint64_t* out,
+                           std::uint32_t room, LdsSelect& lds) {
+    const int t = threadIdx.x;
+    for (std::uint32_t base = 0; base < n; base += blockDim.x) {
+        const std::uint32_t i = base + static_cast<std::uint32_t>(t);
+        const std::uint64_t key = i < n ? keys[i] : 0ull;
+        const bool take = key != 0ull && key >= cut;
+        const std::uint64_t mask = __builtin_amdgcn_ballot_w64(take);
+        if (mask != 0ull) {
+            std::uint32_t slot0 = 0u;
+            if ((t & (kWave - 1)) == 0) {
+                slot0 = atomicAdd(&lds.count, static_cast<std::uint32_t>(__builtin_popcountll(mask)));
+            }
+            slot0 = __builtin_amdgcn_readfirstlane(slot0);
+            const std::uint32_t slot = slot0 + __builtin_amdgcn_mbcnt_hi(static_cast<std::uint32_t>(mask >> 32),
+                                                                         __builtin_amdgcn_mbcnt_lo(static_cast<std::uint32_t>(mask), 0u));
+            if (take && slot < room) {
+                out[slot] = key;
+            }
+        }
+    }
+}
+
 // Block (t, q) of zcgvs_launch_topk: the keys of scores [t * tile, t * tile + n) of query q
 // (n <= tile) go to LDS, their best min(k, n) are found by radix passes over the LDS keys
 // (select.hpp), and written, in no particular order, to winners[q * stride + t * k + 0..k); the
@@ -44,11 +134,7 @@ __global__ __launch_bounds__(kMergeThreads) void topkTileKernel(const float* __r
                                                                 int tile, int k, std::uint64_t* __restrict__ winners,
                                                                 std::size_t stride) {
     __shared__ std::uint64_t lds_keys[kTopkTileMax];
-    __shared__ std::uint32_t lds_hist[kSelectBins];
-    __shared__ std::uint32_t lds_scan[kMergeThreads / kWave];
-    __shared__ std::uint64_t lds_wave_lo[kMergeThreads / kWave];
-    __shared__ std::uint64_t lds_wave_hi[kMergeThreads / kWave];
-    __shared__ SelectState lds_state;
+    __shared__ LdsSelect lds;
 
     const int t = threadIdx.x;
     const int q = blockIdx.y;
@@ -70,75 +156,14 @@ __global__ __launch_bounds__(kMergeThreads) void topkTileKernel(const float* __r
                      lo = min(lo, key);
                      hi = max(hi, key);
                  });
-    // smallest and largest key of the tile: the radix passes start below the bits they share
-    lo = waveReduce64(lo, [](std::uint64_t x, std::uint64_t y) { return min(x, y); });
-    hi = waveReduce64(hi, [](std::uint64_t x, std::uint64_t y) { return max(x, y); });
-    if ((t & (kWave - 1)) == 0) {
-        lds_wave_lo[t / kWave] = lo;
-        lds_wave_hi[t / kWave] = hi;
+    if (t == 0) {
+        lds.count = 0u;
     }
-    __syncthreads();  // (also: the keys are in LDS)
-    if (t < kWave) {
-        constexpr int kSlots = kMergeThreads / kWave;
-        std::uint64_t l = t < kSlots ? lds_wave_lo[t] : ~0ull;
-        std::uint64_t h = t < kSlots ? lds_wave_hi[t] : 0ull;
-        l = waveReduce64(l, [](std::uint64_t x, std::uint64_t y) { return min(x, y); });
-        h = waveReduce64(h, [](std::uint64_t x, std::uint64_t y) { return max(x, y); });
-        if (t == 0) {
-            lds_state.prefix = 0ull;
-            lds_state.bits = 0u;
-            lds_state.need = min(n, static_cast<std::uint32_t>(k));
-            lds_state.done = n <= static_cast<std::uint32_t>(k) ? 1u : 0u;
-            lds_state.count = 0u;
-            if (n > static_cast<std::uint32_t>(k)) {  // at least two distinct keys
-                const int common = __clzll(h ^ l);
-                lds_state.prefix = common == 0 ? 0ull : (h >> (64 - common));
-                lds_state.bits = static_cast<std::uint32_t>(common);
-            }
-        }
-    }
+    // (ldsSelectCut's first barrier also makes the keys and the count visible)
+    const std::uint64_t cut = ldsSelectCut(lds_keys, n, k, lo, hi, lds);
+    ldsCollect(lds_keys, n, cut, out, static_cast<std::uint32_t>(k), lds);  // exactly min(n, k) keys
     __syncthreads();
-    for (int pass = 0; pass < kSelectPasses && !lds_state.done; ++pass) {
-        const int width = min(11, 64 - static_cast<int>(lds_state.bits));
-        for (int i = t; i < (1 << width); i += blockDim.x) {
-            lds_hist[i] = 0u;
-        }
-        __syncthreads();
-        const std::uint32_t bits = lds_state.bits;
-        const std::uint64_t prefix = lds_state.prefix;
-        const int shift = 64 - static_cast<int>(bits) - width;
-        const std::uint64_t digit_mask = (1ull << width) - 1ull;
-        for (std::uint32_t i = static_cast<std::uint32_t>(t); i < n; i += blockDim.x) {
-            const std::uint64_t key = lds_keys[i];
-            if (bits == 0u || (key >> (64 - bits)) == prefix) {
-                atomicAdd(&lds_hist[(key >> shift) & digit_mask], 1u);
-            }
-        }
-        __syncthreads();
-        selectPickBucket<kMergeThreads>(lds_hist, width, &lds_state, lds_scan);  // (ends with a barrier)
-    }
-    // exactly min(n, k) keys reach the cut (keys are unique); one slot reservation per wavefront step
-    const std::uint64_t cut = n <= static_cast<std::uint32_t>(k) ? 1ull : selectThreshold(lds_state);
-    for (std::uint32_t base = 0; base < n; base += blockDim.x) {
-        const std::uint32_t i = base + static_cast<std::uint32_t>(t);
-        const std::uint64_t key = i < n ? lds_keys[i] : 0ull;
-        const bool take = key != 0ull && key >= cut;
-        const std::uint64_t mask = __builtin_amdgcn_ballot_w64(take);
-        if (mask != 0ull) {
-            std::uint32_t slot0 = 0u;
-            if ((t & (kWave - 1)) == 0) {
-                slot0 = atomicAdd(&lds_state.count, static_cast<std::uint32_t>(__builtin_popcountll(mask)));
-            }
-            slot0 = __builtin_amdgcn_readfirstlane(slot0);
-            const std::uint32_t slot = slot0 + __builtin_amdgcn_mbcnt_hi(static_cast<std::uint32_t>(mask >> 32),
-                                                                         __builtin_amdgcn_mbcnt_lo(static_cast<std::uint32_t>(mask), 0u));
-            if (take && slot < static_cast<std::uint32_t>(k)) {
-                out[slot] = key;
-            }
-        }
-    }
-    __syncthreads();
-    const std::uint32_t taken = min(lds_state.count, static_cast<std::uint32_t>(k));
+    const std::uint32_t taken = min(lds.count, static_cast<std::uint32_t>(k));
     for (std::uint32_t i = taken + static_cast<std::uint32_t>(t); i < static_cast<std::uint32_t>(k); i += blockDim.x) {
         out[i] = 0ull;
     }
@@ -242,6 +267,112 @@ __global__ __launch_bounds__(kSortedMergeThreads) void sortedSegmentMergeKernel(
         }
     }
     for (int i = taken + t; i < k; i += kSortedMergeThreads) {
+        dst[i] = 0ull;
+        if (out_index != nullptr) {
+            const std::size_t o = static_cast<std::size_t>(q) * k + i;
+            writeHit(0ull, &out_index[o], &out_score[o]);
+        }
+    }
+    if (t == 0 && overflow != nullptr && in.reset_overflow) {
+        overflow[q] = 0u;  // (no segment holds more than its k keys)
+    }
+}
+
+// The same selection for kSortedMergeMaxK < k <= kSortedSelectMaxK: the keys >= the k-th best head
+// in the segments whose head reaches it (at most k segments of at most k keys, so at most
+// kSelectLdsKeys keys) go to LDS, the best k of them are found by radix passes (ldsSelectCut) and
+// only those k are ranked by comparison.
+__global__ __launch_bounds__(kMergeThreads) void sortedSegmentSelectKernel(
+    MergeInputs in, int k, int batch, std::uint64_t* __restrict__ out_keys, std::uint32_t* __restrict__ overflow,
+    int* __restrict__ out_index, float* __restrict__ out_score) {
+    __shared__ std::uint64_t lds_head[kSortedMergeMaxSegments];
+    __shared__ std::uint32_t lds_count[kSortedMergeMaxSegments];
+    __shared__ int lds_segs[kSortedSelectMaxK];
+    __shared__ std::uint64_t lds_pick[kSortedSelectMaxK * kSortedSelectMaxK];
+    __shared__ std::uint64_t lds_top[kSortedSelectMaxK];
+    __shared__ LdsSelect lds;
+    __shared__ std::uint64_t lds_cut;
+    __shared__ std::uint32_t lds_nsegs;
+    __shared__ std::uint32_t lds_picked;
+
+    const int q = blockIdx.x;
+    const int t = threadIdx.x;
+    const int n_seg = in.n_seg;
+    // a segment holds at most k keys (the scan writes min(count, k)); the clamp keeps the picks
+    // within k * k whatever the counts say
+    const std::uint32_t cap = min(1u << in.seg_log2, static_cast<std::uint32_t>(k));
+    auto segment = [&](int s) { return in.seg + ((static_cast<std::size_t>(s) * batch + q) << in.seg_log2); };
+    for (int s = t; s < n_seg; s += blockDim.x) {
+        const std::uint32_t c = min(in.seg_count[static_cast<std::size_t>(s) * batch + q], cap);
+        const std::uint64_t first = segment(s)[0];
+        lds_count[s] = c;
+        lds_head[s] = c > 0u ? first : 0ull;
+    }
+    if (t == 0) {
+        lds_cut = 1ull;  // fewer than k non-zero heads: every non-zero key
+        lds_nsegs = 0u;
+        lds_picked = 0u;
+        lds.count = 0u;
+    }
+    __syncthreads();
+    for (int s = t; s < n_seg; s += blockDim.x) {
+        const std::uint64_t head = lds_head[s];
+        if (head != 0ull) {
+            int above = 0;
+            for (int j = 0; j < n_seg; ++j) {
+                above += lds_head[j] > head ? 1 : 0;
+            }
+            if (above == k - 1) {
+                lds_cut = head;
+            }
+        }
+    }
+    __syncthreads();
+    const std::uint64_t cut = lds_cut;
+    for (int s = t; s < n_seg; s += blockDim.x) {
+        if (lds_head[s] >= cut) {  // (a zero head never reaches cut >= 1)
+            lds_segs[atomicAdd(&lds_nsegs, 1u)] = s;  // at most k segments
+        }
+    }
+    __syncthreads();
+    const std::uint32_t slots = lds_nsegs * static_cast<std::uint32_t>(k);
+    std::uint64_t lo = ~0ull;
+    std::uint64_t hi = 0ull;
+    // slot i: key i % k of chosen segment i / k (0 past the segment's count); each thread's loads
+    // of a round are in flight together
+    gatherRounds(slots,
+                 [&](std::uint32_t i) {
+                     const int s = lds_segs[i / k];
+                     const std::uint32_t j = i - (i / k) * k;
+                     return j < lds_count[s] ? segment(s)[j] : 0ull;
+                 },
+                 [&](std::uint32_t, std::uint64_t key) {
+                     if (key != 0ull && key >= cut) {
+                         lds_pick[atomicAdd(&lds_picked, 1u)] = key;  // at most k * k keys
+                         lo = min(lo, key);
+                         hi = max(hi, key);
+                     }
+                 });
+    __syncthreads();  // every pick and their count
+    const std::uint32_t n = lds_picked;
+    const std::uint64_t top_cut = ldsSelectCut(lds_pick, n, k, lo, hi, lds);
+    ldsCollect(lds_pick, n, top_cut, lds_top, static_cast<std::uint32_t>(k), lds);  // exactly min(n, k)
+    __syncthreads();
+    const int taken = static_cast<int>(min(lds.count, static_cast<std::uint32_t>(k)));
+    std::uint64_t* dst = out_keys + static_cast<std::size_t>(q) * k;
+    for (int i = t; i < taken; i += blockDim.x) {
+        const std::uint64_t key = lds_top[i];
+        int rank = 0;
+        for (int j = 0; j < taken; ++j) {
+            rank += lds_top[j] > key ? 1 : 0;  // keys are unique
+        }
+        dst[rank] = key;
+        if (out_index != nullptr) {
+            const std::size_t o = static_cast<std::size_t>(q) * k + rank;
+            writeHit(key, &out_index[o], &out_score[o]);
+        }
+    }
+    for (int i = taken + t; i < k; i += blockDim.x) {
         dst[i] = 0ull;
         if (out_index != nullptr) {
             const std::size_t o = static_cast<std::size_t>(q) * k + i;
@@ -386,6 +517,13 @@ int launchSketchThreshold(const float* sketch, int slots, int batch, int j, int 
 
 int launchSortedSegmentMerge(const MergeInputs& in, int k, int batch, std::uint64_t* out_keys,
                              std::uint32_t* overflow, int* out_index, float* out_score, hipStream_t stream) {
+    if (k > kSortedMergeMaxK && k <= kSortedSelectMaxK && in.n_seg >= 1 && in.n_seg <= kSortedMergeMaxSegments &&
+        in.seg != nullptr && in.prev == nullptr && in.dense == nullptr && (1 << in.seg_log2) >= k) {
+        sortedSegmentSelectKernel<<<batch, kMergeThreads, 0, stream>>>(in, k, batch, out_keys, overflow, out_index,
+                                                                       out_score);
+        ZCGVS_LAUNCH_CHECK("sorted-segment select");
+        return ZCGVS_OK;
+    }
     if (k < 1 || k > kSortedMergeMaxK || in.n_seg < 1 || in.n_seg > kSortedMergeMaxSegments || in.seg == nullptr ||
         in.prev != nullptr || in.dense != nullptr || (1 << in.seg_log2) < k) {
         return setError(ZCGVS_ERR_RUNTIME, "zcgvs select: sorted-segment merge does not take this shape");
