@@ -79,6 +79,46 @@ def test_scan_paths(gpu, dim, dtype, metric, use_mask):
     assert_scores_close(scores.to_host(), expected, float_tolerance(queries, decoded, metric))
 
 
+@pytest.mark.parametrize("dtype,dim,batch,metric", [
+    (0, 384, 4, 0),     # float32, the smallest batch the matrix cores take, cosine
+    (0, 256, 64, 1),    # float32 dot, four query groups in one launch
+    (1, 512, 130, 0),   # float16, two launches (128 + 2 queries)
+    (1, 128, 16, 1),    # float16 dot
+])
+def test_similarity_batches_on_matrix_cores(gpu, dtype, dim, batch, metric):
+    # Unmasked cosine/dot batches of float rows take the float matrix-core scan in its store form
+    # (every score written, no keys); 20,003 rows end in a partial tile.
+    capi = gpu
+    n = 20_003
+    corpus = normalized(n, dim, 41 + dim)
+    queries = normalized(batch, dim, 43 + batch)
+    store, decoded = stored(capi, corpus, dtype)
+    scores = capi.DeviceArray((batch, n), np.float32)
+    capi.launch_similarity(store, dtype, 1.0, n, dim, capi.DeviceArray.from_host(queries), batch, None, metric,
+                           scores)
+    capi.synchronize()
+    expected = oracle.scores_f32(decoded, queries, metric)
+    assert_scores_close(scores.to_host(), expected, float_tolerance(queries, decoded, metric))
+
+
+@pytest.mark.parametrize("n,batch", [
+    (19_968, 8),    # 312 whole tiles of 64 rows: the int8 matrix-core scan in its store form
+    (19_968, 300),  # two launches (256 + 44 queries)
+    (20_000, 40),   # a partial last tile: the sdot4 scan
+])
+def test_similarity_i8i8_batches_bit_exact(gpu, n, batch):
+    capi = gpu
+    corpus = normalized(n, 768, 47)
+    queries = normalized(batch, 768, 48)
+    codes, rs = oracle.quantize_rows_i8(corpus)
+    qcodes, qs = oracle.quantize_rows_i8(queries)
+    d_codes, d_rs, d_qcodes, d_qs = (capi.DeviceArray.from_host(a) for a in (codes, rs, qcodes, qs))
+    scores = capi.DeviceArray((batch, n), np.float32)
+    capi.launch_similarity_i8i8(d_codes, d_rs, n, 768, d_qcodes, d_qs, batch, None, capi.DOT, scores)
+    capi.synchronize()
+    assert np.array_equal(scores.to_host(), oracle.scores_i8i8(codes, rs, qcodes, qs, None))
+
+
 def test_similarity_i8i8_bit_exact(gpu):
     capi = gpu
     corpus = normalized(N, 768, 5)

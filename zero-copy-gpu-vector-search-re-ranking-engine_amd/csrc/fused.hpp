@@ -30,6 +30,9 @@ struct PhaseArgs {
     // per workgroup in the int8 scan, 8 in the binary one) keeps the best exact score of its rows
     // per query, written to EmitArgs::sketch.
     int sketch = 0;
+    // A store phase (with dense set; the launchers' score matrix) writes every valid row's score,
+    // as a float, to EmitArgs::scores[q * doc_count + row] instead of a key.
+    int store = 0;
     int block_rows = 64;
 };
 
@@ -41,6 +44,7 @@ struct EmitArgs {
     std::uint32_t* seg_count = nullptr;  // [n_wg, batch]
     int seg_log2 = 0;
     float* sketch = nullptr;             // sketch phases: [slots, batch] best score per slot
+    float* scores = nullptr;             // store phases: [batch, doc_count] scores
     // Rerun of the exact fallback (int8 MFMA scan, binary streaming scan): only the F = *q_list_count queries
     // q_list[0..F) are scanned. List entry e of query q = q_list[e] owns the segments
     // seg[(s * F + e) << rerunSegLog2(seg_log2, batch, F)] with counts seg_count[s * F + e], so

@@ -96,11 +96,13 @@ constexpr int kThreshold = 0;
 constexpr int kDenseMode = 1;
 constexpr int kSketchMode = 2;
 constexpr int kRerunMode = 3;
+constexpr int kStoreMode = 4;  // dense, writing float scores (the launcher's score matrix)
 
 template <int kKSteps, int kMode>
 __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(2, 2)))
 void mfmaScanKernel(ScanArgs scan, PhaseArgs phase, EmitArgs emit, int q_offset, int q_count) {
-    constexpr bool kDense = kMode == kDenseMode;
+    constexpr bool kStore = kMode == kStoreMode;
+    constexpr bool kDense = kMode == kDenseMode || kStore;
     constexpr bool kSketch = kMode == kSketchMode;
     constexpr bool kListed = kMode == kRerunMode;
     constexpr bool kEmits = kMode == kThreshold || kListed;  // keys above a threshold
@@ -322,7 +324,8 @@ void mfmaScanKernel(ScanArgs scan, PhaseArgs phase, EmitArgs emit, int q_offset,
                 const long long row0 = phaseBlock(item, phase.stride, phase.skip) * kRows;
                 const float* scales = scale_ring[sslot];
                 if (q_valid) {
-                    std::uint64_t* dst = emit.dense + static_cast<std::size_t>(q) * emit.dense_stride + item * kRows;
+                    std::uint64_t* dst = kStore ? nullptr : emit.dense + static_cast<std::size_t>(q) * emit.dense_stride + item * kRows;
+                    float* store = kStore ? emit.scores + static_cast<std::size_t>(q) * doc_count + row0 : nullptr;
 #pragma unroll
                     for (int mb = 0; mb < 2; ++mb) {
 #pragma unroll
@@ -336,7 +339,13 @@ void mfmaScanKernel(ScanArgs scan, PhaseArgs phase, EmitArgs emit, int q_offset,
                                 const int dot = mb == 0 ? acc0[4 * g + j] : acc1[4 * g + j];
                                 const float combined = qscale * rsv[j];
                                 const float score = rsv[j] == rsv[j] ? static_cast<float>(dot) * combined : kMaskedScore;
-                                dst[rl0 + j] = row < doc_count ? makeKey(score, static_cast<std::uint32_t>(row)) : 0ull;
+                                if constexpr (kStore) {
+                                    if (row < doc_count) {
+                                        store[rl0 + j] = score;
+                                    }
+                                } else {
+                                    dst[rl0 + j] = row < doc_count ? makeKey(score, static_cast<std::uint32_t>(row)) : 0ull;
+                                }
                             }
                         }
                     }
@@ -574,7 +583,9 @@ int launchShape(const ScanArgs& scan, const PhaseArgs& phase, const EmitArgs& em
     const dim3 grid(static_cast<unsigned>(std::max(1LL, wanted)));
     for (int q0 = 0; q0 < scan.batch; q0 += kQueriesPerLaunch) {
         const int count = std::min(kQueriesPerLaunch, scan.batch - q0);
-        if (phase.dense) {
+        if (phase.store) {
+            mfmaScanKernel<kKSteps, kStoreMode><<<grid, kThreads, 0, stream>>>(scan, phase, emit, q0, count);
+        } else if (phase.dense) {
             mfmaScanKernel<kKSteps, kDenseMode><<<grid, kThreads, 0, stream>>>(scan, phase, emit, q0, count);
         } else if (phase.sketch) {
             mfmaScanKernel<kKSteps, kSketchMode><<<grid, kThreads, 0, stream>>>(scan, phase, emit, q0, count);

@@ -94,9 +94,10 @@ struct FloatTile {
                   "tile and lexical rings fit the LDS");
 };
 
-template <int kKind, int kDim, bool kDense, bool kLex>
+template <int kKind, int kDim, bool kDense, bool kLex, bool kStore = false>
 __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(2, 2)))
 void mfmaFloatScanKernel(ScanArgs scan, PhaseArgs phase, EmitArgs emit, int q_offset, int q_count) {
+    static_assert(!kStore || (kDense && !kLex), "a store phase is a dense phase without lexical scores");
     using Tile = FloatTile<kKind, kDim>;
     constexpr bool kF32 = Tile::kF32;
     constexpr int kRows = Tile::kRows;
@@ -342,7 +343,11 @@ void mfmaFloatScanKernel(ScanArgs scan, PhaseArgs phase, EmitArgs emit, int q_of
                         if constexpr (kLex) {
                             value = fuseHybrid(value, lex_ring[slot][qlocal][local], scan.dense_weight, inverse);
                         }
-                        if constexpr (kDense) {
+                        if constexpr (kStore) {
+                            if (local < valid_rows) {
+                                emit.scores[static_cast<std::size_t>(q) * doc_count + row0 + local] = value;
+                            }
+                        } else if constexpr (kDense) {
                             const std::uint64_t key =
                                 local < valid_rows ? makeKey(value, row_base + static_cast<std::uint32_t>(local)) : 0ull;
                             emit.dense[static_cast<std::size_t>(q) * emit.dense_stride + item * kRows + local] = key;
@@ -374,7 +379,7 @@ int launchQueries(const ScanArgs& scan, const PhaseArgs& phase, const EmitArgs& 
     const int per_launch = kLex ? kLexQueries : kQueriesPerLaunch;
     for (int q0 = 0; q0 < scan.batch; q0 += per_launch) {
         const int count = std::min(per_launch, scan.batch - q0);
-        if (kKind == ZCGVS_DTYPE_F32 && !kLex && mfmaSplitSupported(scan, count)) {
+        if (kKind == ZCGVS_DTYPE_F32 && !kLex && !phase.store && mfmaSplitSupported(scan, count)) {
             // float32 rows against 32 or more queries: the bf16 three-part split scan, whose
             // 32-row tiles and emission are this kernel's
             static_assert(kKind != ZCGVS_DTYPE_F32 || kDim < 256 || kDim > 384 || FloatTile<kKind, kDim>::kRows == 32,
@@ -385,7 +390,12 @@ int launchQueries(const ScanArgs& scan, const PhaseArgs& phase, const EmitArgs& 
             }
             continue;
         }
-        if (phase.dense) {
+        if (phase.store) {
+            if constexpr (!kLex) {
+                mfmaFloatScanKernel<kKind, kDim, true, false, true><<<grid, kThreads, 0, stream>>>(scan, phase, emit, q0,
+                                                                                                    count);
+            }
+        } else if (phase.dense) {
             mfmaFloatScanKernel<kKind, kDim, true, kLex><<<grid, kThreads, 0, stream>>>(scan, phase, emit, q0, count);
         } else {
             mfmaFloatScanKernel<kKind, kDim, false, kLex><<<grid, kThreads, 0, stream>>>(scan, phase, emit, q0, count);

@@ -4,7 +4,10 @@
 // One launch covers the whole batch: blockIdx.y selects a tile of up to kQueryTile queries that
 // is staged in LDS once per block, and the blocks stride over the corpus. Rows whose size is a
 // multiple of 16 bytes (and a 16-byte aligned base) take the chunked path of scan_core.hpp; any
-// other shape takes the scalar path (one wavefront per row, lanes stride the elements). A lane
+// other shape takes the scalar path (one wavefront per row, lanes stride the elements). Query
+// batches that a matrix-core scan takes (float32 / float16 from 4 queries, per-vector int8 from 8;
+// cosine or dot, no mask, its dimensions) run that scan in its store form instead: one pass over
+// the corpus for up to 128 (float) or 256 (int8) queries, every score written to the matrix. A lane
 // holds up to kLoadBatch chunks of its row and issues all their loads before it uses any of them,
 // so they are in flight together; the sums take the chunks in column order as before. Float rows
 // are read with the streaming hint (each byte is read once per query tile; for int8 rows it
@@ -16,6 +19,7 @@
 #include <algorithm>
 
 #include "common.hpp"
+#include "fused.hpp"
 #include "scan_core.hpp"
 
 namespace zcgvs_hip {
@@ -442,6 +446,31 @@ void launchI8I8(const void* corpus, const float* row_scales, int doc_count, int 
         query_scales, dim, batch, mask, scores);
 }
 
+// The score matrix of a query batch by a matrix-core scan in its store form (every row's score,
+// no keys), when one takes the shape: returns false, launching nothing, otherwise.
+bool storeOnMatrixCores(const ScanArgs& scan, float* scores, hipStream_t stream, int* status) {
+    const bool per_vector = scan.dtype == ZCGVS_DTYPE_I8 && scan.row_scales != nullptr;
+    if (per_vector) {
+        // whole tiles only: without a padded copy, the scan's last tile reads 64 row scales
+        if (!mfmaSupported(scan) || scan.doc_count % kMfmaBlockRows != 0) {
+            return false;
+        }
+    } else if (!mfmaFloatSupported(scan)) {
+        return false;
+    }
+    PhaseArgs phase;
+    phase.block_rows = per_vector ? kMfmaBlockRows : mfmaFloatBlockRows(scan);
+    phase.items = (scan.doc_count + phase.block_rows - 1) / phase.block_rows;
+    phase.dense = 1;
+    phase.store = 1;
+    EmitArgs emit;
+    emit.scores = scores;
+    const int workgroups = deviceComputeUnits();
+    *status = per_vector ? launchMfmaScan(scan, phase, emit, workgroups, stream)
+                         : launchMfmaFloatScan(scan, phase, emit, workgroups, stream);
+    return true;
+}
+
 std::size_t stagingBytes(int dtype, int dim) {
     if (dtype == ZCGVS_DTYPE_BINARY) {
         return binaryWords(dim) * 4;
@@ -514,6 +543,21 @@ int zcgvs_launch_similarity(const void* d_corpus, int dtype, float scale, int do
 
     const std::size_t row_bytes = rowBytes(dtype, dim);
     const float* queries = static_cast<const float*>(d_queries);
+    if (dtype != ZCGVS_DTYPE_I8 && d_mask == nullptr) {
+        ScanArgs scan;
+        scan.corpus = d_corpus;
+        scan.doc_count = doc_count;
+        scan.dim = dim;
+        scan.dtype = dtype;
+        scan.scale = scale;
+        scan.queries = d_queries;
+        scan.batch = batch;
+        scan.metric = metric;
+        int status = ZCGVS_OK;
+        if (storeOnMatrixCores(scan, d_scores, s, &status)) {
+            return status == ZCGVS_OK ? clearError() : status;
+        }
+    }
     if (row_bytes % 16 == 0 && aligned16(d_corpus)) {
         const int chunks = static_cast<int>(row_bytes / 16);
         const int lanes = lanesPerRow(chunks, kLoadBatch);
@@ -578,6 +622,22 @@ int zcgvs_launch_similarity_i8i8(const std::int8_t* d_corpus, const float* d_row
     }
     const unsigned tiles = static_cast<unsigned>((batch + kQueryTile - 1) / kQueryTile);
     const hipStream_t s = toStream(stream);
+    if (d_mask == nullptr) {
+        ScanArgs scan;
+        scan.corpus = d_corpus;
+        scan.doc_count = doc_count;
+        scan.dim = dim;
+        scan.dtype = ZCGVS_DTYPE_I8;
+        scan.row_scales = d_row_scales;
+        scan.queries = d_queries;
+        scan.query_scales = d_query_scales;
+        scan.batch = batch;
+        scan.metric = metric;
+        int status = ZCGVS_OK;
+        if (storeOnMatrixCores(scan, d_scores, s, &status)) {
+            return status == ZCGVS_OK ? clearError() : status;
+        }
+    }
     switch (lanesPerRow(chunks, kLoadBatch)) {
         case 1: launchI8I8<1>(d_corpus, d_row_scales, doc_count, chunks, d_queries, d_query_scales, dim, batch, d_mask, d_scores, shared, tiles, s); break;
         case 2: launchI8I8<2>(d_corpus, d_row_scales, doc_count, chunks, d_queries, d_query_scales, dim, batch, d_mask, d_scores, shared, tiles, s); break;
