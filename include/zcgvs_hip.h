@@ -148,14 +148,19 @@ int zcgvs_graph_destroy(zcgvs_graph_t graph);
  * d_queries: [batch, dim] float32, or [batch, ceil(dim/32)] packed uint32 words for a BINARY
  * corpus (bit b of word w = dimension 32w+b, set iff value >= 0). Masked documents (mask byte 0)
  * score -FLT_MAX. Cosine is a raw dot product (inputs are assumed L2-normalized). L2 scores are
- * the negated squared distance. Binary scores are (dim - 2*hamming) / dim. */
+ * the negated squared distance. Binary scores are (dim - 2*hamming) / dim. Unmasked cosine/dot
+ * batches of at least 4 float32/float16 queries with dim 128, 256, 384 or 512 are computed on the
+ * matrix cores (float32 products and sums in another order: equal to the scalar loop within
+ * float32 rounding). */
 int zcgvs_launch_similarity(const void* d_corpus, int dtype, float scale, int doc_count, int dim,
                             const void* d_queries, int batch, const uint8_t* d_mask, int metric,
                             float* d_scores, zcgvs_stream_t stream);
 
 /* Same contract as zcgvs_launch_similarity for an int8 corpus in ZCGVS_INT8_PER_VECTOR mode:
  * d_corpus [doc_count, dim] int8 with d_row_scales [doc_count]; d_queries [batch, dim] int8 with
- * d_query_scales [batch]. Metric must be COSINE or DOT. No reference counterpart. */
+ * d_query_scales [batch]. Metric must be COSINE or DOT. No reference counterpart. Scores are
+ * (float)(int32 dot) * (s_q * s_r) on every path (unmasked batches of at least 8 queries over a
+ * whole number of 64-row tiles with dim 256-1024 run on the matrix cores). */
 int zcgvs_launch_similarity_i8i8(const int8_t* d_corpus, const float* d_row_scales,
                                  int doc_count, int dim, const int8_t* d_queries,
                                  const float* d_query_scales, int batch, const uint8_t* d_mask,
