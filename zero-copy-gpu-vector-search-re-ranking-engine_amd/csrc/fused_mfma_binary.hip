@@ -1,5 +1,6 @@
 // Binary (1-bit) MFMA fused scan: Hamming distances of sign-packed corpus rows to a batch of
-// sign-packed queries on the int8 matrix cores, with the threshold emission of fused.hpp. The
+// sign-packed queries on the matrix cores (fp4 operands for launches of up to 32 queries, int8
+// for larger ones), with the threshold emission of fused.hpp. The
 // reference computes popc(c ^ q) word by word on the VALU (src/cuda/similarity.cu:169-238,
 // hammingScanKernel) and scores (d - 2h) / d (include/zcgvs/cuda/decode.cuh:45-47).
 //
@@ -21,6 +22,12 @@
 // shift for s = 7), shared by the two query groups of 16 a wavefront serves, and every product
 // is 64 r_k (1 - 2 q_k) (|acc| <= 64 d fits int32 easily).
 //
+// fp4 form (mfmaBinaryStreamKernel). The same identity on v_mfma_scale_f32_16x16x128_f8f6f4 with
+// e2m1 operands: row bits become nibbles of 0, 1 or 2 and query bits +-2 or +-1 (spreadNibbles,
+// signNibbles), every product is 2 r_k (1 - 2 q_k), and the fp32 accumulator holds
+// 2 (popc(r) - 2 r.q) exactly (|acc| <= 2 d, far below 2^24). A step covers 128 dims, one word
+// per lane, twice the int8 form's 64 for the same matrix-core cycles.
+//
 // Work split. Launches of up to 32 queries (one set, two MFMA query groups of 16) run
 // mfmaBinaryStreamKernel: the B operands sit in LDS and each of 16 wavefronts streams its own
 // rows into registers (no shared tile, no barrier). It also serves the sketch plan of a search of
@@ -32,7 +39,8 @@
 // MFMA layout (v_mfma_i32_16x16x64_i8). Lane l supplies row (A) / query (B) l % 16 and 16 dims
 // of lane group h = l / 16 per step: 16-byte chunk h + 4j of the row covers steps 8j .. 8j + 7,
 // each of its words in turn, in two halves (above); A and B use the same assignment, so every
-// dim is counted once. D: lane l holds query l % 16 and rows 4h + i, i < 4.
+// dim is counted once. D: lane l holds query l % 16 and rows 4h + i, i < 4. The fp4 form assigns
+// 32 dims per lane and step: chunk h + 4j covers steps 4j .. 4j + 3, one word each; D as above.
 //
 // Corpus streaming as in the other MFMA scans (lds_copy.hpp): 48 KB tiles HBM -> LDS by
 // global_load_lds_dwordx4 in a 3-deep ring (smaller tiles in deeper rings measured slower: the
@@ -52,6 +60,8 @@ namespace zcgvs_hip {
 namespace {
 
 typedef int v4i __attribute__((ext_vector_type(4)));
+typedef int v8i __attribute__((ext_vector_type(8)));
+typedef float v4f __attribute__((ext_vector_type(4)));
 typedef unsigned int u32x4 __attribute__((ext_vector_type(4)));
 
 constexpr int kThreads = 512;
@@ -106,6 +116,42 @@ __device__ __forceinline__ v4i signWord(std::uint32_t word, int p) {
         out[j] = static_cast<int>(w * 0x01010101u + bits * (256u - 2u * w));
     }
     return out;
+}
+
+// fp4 (e2m1) operands of the stream kernel: nibble 0010 is 1, 0100 is 2 and bit 3 is the sign
+// (every value used is a normal number). A row word becomes 32 nibbles: nibble e of dword j holds
+// bit 4e + j of the word, as 0 or 1 (j < 2, the bit moved to nibble bit 1) or 0 or 2 (j >= 2, moved
+// to nibble bit 2). Four ANDs and two shifts per 32 dims, against eight ANDs for the int8 form.
+__device__ __forceinline__ v4i spreadNibbles(std::uint32_t word) {
+    v4i out;
+    out[0] = static_cast<int>((word << 1) & 0x22222222u);
+    out[1] = static_cast<int>(word & 0x22222222u);
+    out[2] = static_cast<int>(word & 0x44444444u);
+    out[3] = static_cast<int>((word >> 1) & 0x44444444u);
+    return out;
+}
+
+// The same 32 dims of a query word as spreadNibbles, as (1 - 2 bit) 2 (j < 2) or (1 - 2 bit)
+// (j >= 2), so that every product with spreadNibbles' nibble is 2 r (1 - 2 q).
+__device__ __forceinline__ v4i signNibbles(std::uint32_t word) {
+    v4i out;
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+        const std::uint32_t magnitude = j < 2 ? 0x44444444u : 0x22222222u;
+        out[j] = static_cast<int>((((word >> j) & 0x11111111u) << 3) | magnitude);
+    }
+    return out;
+}
+
+// v_mfma_scale_f32_16x16x128_f8f6f4 with both operands fp4 (format code 4; the instruction reads
+// the low four registers of each) and unit scales (E8M0 127 = 2^0). Products of +-1 and +-2 and
+// their sums below 2^24 are exact in the fp32 accumulators.
+__device__ __forceinline__ v4f mfmaNibbles(const v4i& a, const v4i& b, const v4f& c) {
+    constexpr int kFp4 = 4;
+    constexpr int kScaleOne = 127;
+    const v8i a8 = __builtin_shufflevector(a, a, 0, 1, 2, 3, 0, 1, 2, 3);
+    const v8i b8 = __builtin_shufflevector(b, b, 0, 1, 2, 3, 0, 1, 2, 3);
+    return __builtin_amdgcn_mfma_scale_f32_16x16x128_f8f6f4(a8, b8, c, kFp4, kFp4, 0, kScaleOne, 0, kScaleOne);
 }
 
 // The word of step t (lane group h) from the lane's chunk words: chunk jc = t / 8, word
@@ -411,7 +457,7 @@ void mfmaBinaryStreamKernel(ScanArgs scan, PhaseArgs phase, EmitArgs emit, int q
     constexpr int kRows = Tile::kRows;
     constexpr int kRowBytes = Tile::kRowBytes;
     constexpr int kLaneChunks = Tile::kLaneChunks;
-    constexpr int kSteps = Tile::kSteps;
+    constexpr int kSteps = kLaneChunks * 4;  // one word (32 dims) per lane and step, 128 per step
     constexpr int kPairs = Tile::kRowBlocks / 2;
     constexpr int kDim = kWords * 32;
     static_assert(Tile::kRowBlocks % 2 == 0, "an item splits into 32-row pairs");
@@ -452,8 +498,8 @@ void mfmaBinaryStreamKernel(ScanArgs scan, PhaseArgs phase, EmitArgs emit, int q
     const std::uint8_t* corpus = static_cast<const std::uint8_t*>(scan.corpus);
     const std::uint32_t* qwords = static_cast<const std::uint32_t*>(scan.queries);
 
-    // B operands: lane l of group g at step t supplies query g * 16 + l % 16, half t % 2 of word
-    // (t % 8) / 2 of its chunk l / 16 + 4 (t / 8) (as the A operand's lanes do for their rows)
+    // B operands: lane l of group g at step t supplies query g * 16 + l % 16, word t % 4 of its
+    // chunk l / 16 + 4 (t / 4) (as the A operand's lanes do for their rows)
     for (int e = tid; e < kSteps * 2 * kWave; e += kStreamThreads) {
         const int t = e / (2 * kWave);
         const int g = (e / kWave) % 2;
@@ -462,8 +508,8 @@ void mfmaBinaryStreamKernel(ScanArgs scan, PhaseArgs phase, EmitArgs emit, int q
         v4i value = {0, 0, 0, 0};
         if (qlocal < q_count) {
             const std::uint32_t word = qwords[static_cast<std::size_t>(queryOf(qlocal)) * kWords +
-                                              4 * ((l >> 4) + 4 * (t / 8)) + (t % 8) / 2];
-            value = signWord(word, t % 2);
+                                              4 * ((l >> 4) + 4 * (t / 4)) + t % 4];
+            value = signNibbles(word);
         }
         qlds[t][g][l] = value;
     }
@@ -476,7 +522,7 @@ void mfmaBinaryStreamKernel(ScanArgs scan, PhaseArgs phase, EmitArgs emit, int q
     bool valid_of[2];
     int h_limit[2];
     std::uint32_t row_limit[2];
-    int acc_limit[2];
+    float acc_limit[2];
 #pragma unroll
     for (int g = 0; g < 2; ++g) {
         const int qlocal = g * 16 + r16;
@@ -499,12 +545,14 @@ void mfmaBinaryStreamKernel(ScanArgs scan, PhaseArgs phase, EmitArgs emit, int q
         if constexpr (!kDense && !kSketch) {
             binaryThreshold<kDim>(emit, q, h_limit[g], row_limit[g]);
         }
-        acc_limit[g] = 64 * (valid_of[g] ? h_limit[g] - popq[g] : -(kDim + 1));
+        acc_limit[g] = static_cast<float>(2 * (valid_of[g] ? h_limit[g] - popq[g] : -(kDim + 1)));
     }
     __syncthreads();
     int best_hd[2] = {kDim + 1, kDim + 1};  // sketch: the lane's least distance per query group
 
-    auto emitKeys = [&](const v4i& acc, int g, long long row0, int local0, long long item_) {
+    // acc holds 2 (popc(r) - 2 r.q) exactly, so h = acc / 2 + popc(q)
+    auto distance = [&](float acc, int g) { return (static_cast<int>(acc) >> 1) + popq[g]; };
+    auto emitKeys = [&](const v4f& acc, int g, long long row0, int local0, long long item_) {
         if (!valid_of[g]) {
             return;
         }
@@ -513,7 +561,7 @@ void mfmaBinaryStreamKernel(ScanArgs scan, PhaseArgs phase, EmitArgs emit, int q
         for (int i = 0; i < 4; ++i) {
             const int local = local0 + 4 * h + i;  // row within the item
             const long long row = row0 + local;
-            const int hd = (acc[i] >> 6) + popq[g];  // acc is 64 times the +-1 dot, exactly
+            const int hd = distance(acc[i], g);
             if constexpr (kDense) {
                 std::uint64_t key = 0ull;
                 if (row < doc_count) {
@@ -554,38 +602,50 @@ void mfmaBinaryStreamKernel(ScanArgs scan, PhaseArgs phase, EmitArgs emit, int q
         }
     };
     auto processPair = [&](const u32x4 (&cur)[2][kLaneChunks], long long p) {
-        v4i acc[2][2] = {};
+        // the pair's rows first: phaseBlock branches, and products computed before a branch whose
+        // far side uses them would be sunk past it, out of the step-by-step schedule below
+        const std::uint32_t p32 = static_cast<std::uint32_t>(p);
+        const std::uint32_t it = p32 / kPairs;
+        const long long row0 = phaseBlock(it, phase.stride, phase.skip) * kRows;
+        const int pair_row = 32 * static_cast<int>(p32 - it * kPairs);
+        v4f acc[2][2] = {};
         v4i a[2];
-        a[0] = spreadWord(stepWord<kLaneChunks>(cur[0], 0), 0);
-        a[1] = spreadWord(stepWord<kLaneChunks>(cur[1], 0), 0);
-        // the B operands of step t + 1 are read from LDS during step t
-        v4i b0 = qlds[0][0][lane];
-        v4i b1 = qlds[0][1][lane];
+        a[0] = spreadNibbles(cur[0][0][0]);
+        a[1] = spreadNibbles(cur[1][0][0]);
+        // The B operands of step t + 1 are read from LDS during step t. The lane's index is
+        // opaque to the compiler, which would otherwise keep every step's B operands in registers
+        // across pairs (64 more registers, and spills).
+        int ql = lane;
+        asm volatile("" : "+v"(ql));
+        v4i b0 = qlds[0][0][ql];
+        v4i b1 = qlds[0][1][ql];
 #pragma unroll
         for (int t = 0; t < kSteps; ++t) {
             v4i nb0 = b0;
             v4i nb1 = b1;
             if (t + 1 < kSteps) {
-                nb0 = qlds[t + 1][0][lane];
-                nb1 = qlds[t + 1][1][lane];
+                nb0 = qlds[t + 1][0][ql];
+                nb1 = qlds[t + 1][1][ql];
             }
-            acc[0][0] = __builtin_amdgcn_mfma_i32_16x16x64_i8(a[0], b0, acc[0][0], 0, 0, 0);
-            acc[0][1] = __builtin_amdgcn_mfma_i32_16x16x64_i8(a[0], b1, acc[0][1], 0, 0, 0);
-            acc[1][0] = __builtin_amdgcn_mfma_i32_16x16x64_i8(a[1], b0, acc[1][0], 0, 0, 0);
-            acc[1][1] = __builtin_amdgcn_mfma_i32_16x16x64_i8(a[1], b1, acc[1][1], 0, 0, 0);
+            acc[0][0] = mfmaNibbles(a[0], b0, acc[0][0]);
+            acc[0][1] = mfmaNibbles(a[0], b1, acc[0][1]);
+            acc[1][0] = mfmaNibbles(a[1], b0, acc[1][0]);
+            acc[1][1] = mfmaNibbles(a[1], b1, acc[1][1]);
             if (t + 1 < kSteps) {
-                a[0] = spreadWord(stepWord<kLaneChunks>(cur[0], t + 1), (t + 1) % 2);
-                a[1] = spreadWord(stepWord<kLaneChunks>(cur[1], t + 1), (t + 1) % 2);
+                a[0] = spreadNibbles(cur[0][(t + 1) / 4][(t + 1) % 4]);
+                a[1] = spreadNibbles(cur[1][(t + 1) / 4][(t + 1) % 4]);
             }
             b0 = nb0;
             b1 = nb1;
             // step by step: the compiler would otherwise hoist every step's B reads up front
             __builtin_amdgcn_sched_barrier(0);
         }
-        const std::uint32_t p32 = static_cast<std::uint32_t>(p);
-        const std::uint32_t it = p32 / kPairs;
-        const long long row0 = phaseBlock(it, phase.stride, phase.skip) * kRows;
-        const int pair_row = 32 * static_cast<int>(p32 - it * kPairs);
+        // every product is finished here: block 1's are otherwise sunk past block 0's emission,
+        // keeping its operands live across it
+#pragma unroll
+        for (int b = 0; b < 2; ++b) {
+            asm volatile("" : "+v"(acc[b][0]), "+v"(acc[b][1]));
+        }
 #pragma unroll
         for (int b = 0; b < 2; ++b) {
             if constexpr (kSketch) {
@@ -596,7 +656,7 @@ void mfmaBinaryStreamKernel(ScanArgs scan, PhaseArgs phase, EmitArgs emit, int q
 #pragma unroll
                     for (int i = 0; i < 4; ++i) {
                         const long long row = row0 + pair_row + 16 * b + 4 * h + i;
-                        const int hd = (acc[b][g][i] >> 6) + popq[g];
+                        const int hd = distance(acc[b][g][i], g);
                         best_hd[g] = row < doc_count ? min(best_hd[g], hd) : best_hd[g];
                     }
                 }
@@ -606,9 +666,9 @@ void mfmaBinaryStreamKernel(ScanArgs scan, PhaseArgs phase, EmitArgs emit, int q
                     emitKeys(acc[b][1], 1, row0, pair_row + 16 * b, it);
                 }
             } else {
-                // fast reject: a key can pass only if acc <= 64 (h_limit - popc(q))
-                const int m0 = min(min(acc[b][0][0], acc[b][0][1]), min(acc[b][0][2], acc[b][0][3]));
-                const int m1 = min(min(acc[b][1][0], acc[b][1][1]), min(acc[b][1][2], acc[b][1][3]));
+                // fast reject: a key can pass only if acc <= 2 (h_limit - popc(q))
+                const float m0 = fminf(fminf(acc[b][0][0], acc[b][0][1]), fminf(acc[b][0][2], acc[b][0][3]));
+                const float m1 = fminf(fminf(acc[b][1][0], acc[b][1][1]), fminf(acc[b][1][2], acc[b][1][3]));
                 if (__builtin_amdgcn_ballot_w64(m0 <= acc_limit[0] || m1 <= acc_limit[1]) != 0) {
                     emitKeys(acc[b][0], 0, row0, pair_row + 16 * b, it);
                     if (two_groups) {
