@@ -30,7 +30,7 @@
 //
 // Work split. Launches of up to 32 queries (one set, two MFMA query groups of 16) run
 // mfmaBinaryStreamKernel: the B operands sit in LDS and each of 16 wavefronts streams its own
-// rows into registers (no shared tile, no barrier). It also serves the sketch plan of a search of
+// rows through LDS slots of its own (no shared tile, no barrier). It also serves the sketch plan of a search of
 // at most 32 queries: a sketch mode (the least distance of each query per pair of wavefronts, no
 // keys) and a rerun mode (the device list of flagged queries). Larger launches (up to 4 sets, 128
 // queries) run mfmaBinaryScanKernel: 8 wavefronts, each with one set's B operands in registers,
@@ -426,13 +426,17 @@ void mfmaBinaryScanKernel(ScanArgs scan, PhaseArgs phase, EmitArgs emit, int q_o
 
 constexpr int kStreamThreads = 1024;
 constexpr int kStreamWaves = kStreamThreads / kWave;
+constexpr int kStreamSlots = 2;  // LDS pair slots per wavefront
 
 // One query set (<= 32 queries): the set's B operands sit in LDS, shared by the workgroup's 16
-// wavefronts, and each wavefront streams its own rows from HBM straight into registers, 32 rows
-// (two 16-row blocks) at a time, the next pair loaded while the current one is multiplied. No
-// tile is shared, so there is no LDS ring and no barrier in the loop, and with the queries out of
-// the registers four wavefronts fit a SIMD, whose loads hide each other's latency. Each B
-// fragment read from LDS feeds two MFMAs (the pair's two blocks). Wavefront w of
+// wavefronts, and each wavefront streams its own rows, 32 rows (two 16-row blocks) at a time,
+// through two LDS pair slots of its own: global_load_lds copies of whole cache lines land a pair
+// two pairs ahead, and the pair being multiplied is read from its slot into registers in the
+// MFMA layout. No tile is shared, so there is no barrier in the loop, and with the queries out of
+// the registers four wavefronts fit a SIMD, whose copies hide each other's latency. (Loading the
+// MFMA layout straight into registers reads half cache lines per quarter-wave: measured 8%
+// slower for 50M x 1024, B = 32.) Each B fragment read from LDS feeds two MFMAs (the pair's two
+// blocks). Wavefront w of
 // workgroup b takes pairs w * gridDim.x + b, + 16 * gridDim.x, ... of the phase's items (an
 // item's pairs in order), so the pairs spread over the workgroups first.
 //
@@ -462,7 +466,13 @@ void mfmaBinaryStreamKernel(ScanArgs scan, PhaseArgs phase, EmitArgs emit, int q
     constexpr int kDim = kWords * 32;
     static_assert(Tile::kRowBlocks % 2 == 0, "an item splits into 32-row pairs");
 
+    constexpr int kChunks = Tile::kChunks;
+    constexpr int kPairBytes = 32 * kRowBytes;
+    constexpr int kPairCopies = kPairBytes / 1024;  // one 1 KB global_load_lds_dwordx4 per 1024 / kRowBytes rows
+    constexpr int kRowsPerCopy = 1024 / kRowBytes;
     __shared__ v4i qlds[kSteps][2][kWave];  // B operand of (step, query group, lane)
+    // each wavefront's two pair slots; slot position s of pair row r holds chunk s ^ swizzle(r)
+    __shared__ __attribute__((aligned(16))) std::uint8_t pair_lds[kStreamWaves][kStreamSlots][kPairBytes];
     __shared__ std::uint32_t lds_count[kSetQueries];
     __shared__ int lds_sketch[kSketch ? kStreamWaves : 1][kSetQueries];
 
@@ -585,19 +595,35 @@ void mfmaBinaryStreamKernel(ScanArgs scan, PhaseArgs phase, EmitArgs emit, int q
             }
         }
     };
-    // rows past the corpus re-read its last row (their keys are never emitted)
-    // (pair indices stay below 2^31: 32-bit division by the constant kPairs)
-    auto loadPair = [&](long long p, u32x4 (&dst)[2][kLaneChunks]) {
+    // Pair p's rows into LDS slot `slot` of this wavefront: copy k moves pair rows
+    // k * kRowsPerCopy .. + kRowsPerCopy - 1, lane l the 16 bytes of row k * kRowsPerCopy + l / kChunks
+    // that land at slot position l % kChunks, so every copy reads 1 KB of consecutive rows (whole
+    // cache lines per quarter-wave). Rows past the corpus re-read its last row (their keys are never
+    // emitted). Pair indices stay below 2^31: 32-bit division by the constant kPairs.
+    auto copyPair = [&](long long p, int slot) {
         const std::uint32_t p32 = static_cast<std::uint32_t>(p);
         const std::uint32_t it = p32 / kPairs;
         const long long row0 = phaseBlock(it, phase.stride, phase.skip) * kRows + 32 * static_cast<int>(p32 - it * kPairs);
+        const std::uint32_t base = ldsAddress(&pair_lds[wave][slot][0]);
+#pragma unroll
+        for (int k = 0; k < kPairCopies; ++k) {
+            const int r = k * kRowsPerCopy + lane / kChunks;
+            const int position = lane % kChunks;
+            const long long row = min(row0 + r, doc_count - 1);
+            copyToLds(corpus + static_cast<std::size_t>(row) * kRowBytes + (position ^ Tile::swizzle(r)) * 16,
+                      base + k * 1024);
+        }
+    };
+    // The lane's A chunks of a staged pair: row 16 b + r16, chunk h + 4 jc (the 16 rows of one
+    // ds_read_b128 quarter-wave hit 16 distinct 16-byte bank groups through the swizzle).
+    auto readPair = [&](int slot, u32x4 (&dst)[2][kLaneChunks]) {
 #pragma unroll
         for (int b = 0; b < 2; ++b) {
-            const long long row = min(row0 + 16 * b + r16, doc_count - 1);
-            const u32x4* src = reinterpret_cast<const u32x4*>(corpus + static_cast<std::size_t>(row) * kRowBytes);
+            const int r = 16 * b + r16;
 #pragma unroll
             for (int jc = 0; jc < kLaneChunks; ++jc) {
-                dst[b][jc] = __builtin_nontemporal_load(src + h + 4 * jc);
+                const int position = (h + 4 * jc) ^ Tile::swizzle(r);
+                dst[b][jc] = *reinterpret_cast<const u32x4*>(&pair_lds[wave][slot][r * kRowBytes + position * 16]);
             }
         }
     };
@@ -683,26 +709,30 @@ void mfmaBinaryStreamKernel(ScanArgs scan, PhaseArgs phase, EmitArgs emit, int q
     const long long stride = static_cast<long long>(gridDim.x) * kStreamWaves;
     // workgroup-first: with few pairs every workgroup (candidate segment) still gets its share
     long long p = static_cast<long long>(wave) * gridDim.x + blockIdx.x;
-    // Ping-pong between two register buffers, so no buffer is copied while its loads are in flight.
-    // The next pair is loaded unconditionally (past the phase's end, its last pair again): with a
-    // conditional load the loop head would be reached with two different load counts, and the
-    // compiler would then wait for the prefetch halfway through the current pair's products.
-    u32x4 buf0[2][kLaneChunks];
-    u32x4 buf1[2][kLaneChunks];
-    if (p < pairs) {
-        loadPair(p, buf0);
+    // Two pairs in flight while one is multiplied, with no registers held for them: pair i waits in
+    // slot i % 2 of the wavefront's LDS, copied there two pairs ahead. Every iteration issues one
+    // pair's copies (past the phase's end, its last pair again), so before pair i is read only pair
+    // i + 1's copies may still be pending (later global stores of the emission only make the
+    // wait stricter). The copies are inline assembly the compiler does not count, hence the
+    // explicit waits; the memory clobbers keep the LDS reads between them.
+    const long long mine = p < pairs ? (pairs - p + stride - 1) / stride : 0;  // this wave's pairs
+    if (mine > 0) {
+        copyPair(p, 0);
+        copyPair(min(p + stride, pairs - 1), 1);
     }
-    while (p < pairs) {
-        loadPair(min(p + stride, pairs - 1), buf1);
-        processPair(buf0, p);
-        p += stride;
-        if (p >= pairs) {
-            break;
-        }
-        loadPair(min(p + stride, pairs - 1), buf0);
-        processPair(buf1, p);
+    for (long long i = 0; i < mine; ++i) {
+        const int slot = static_cast<int>(i & 1);
+        asm volatile("s_waitcnt vmcnt(%0)" : : "n"(kPairCopies) : "memory");
+        u32x4 cur[2][kLaneChunks];
+        readPair(slot, cur);
+        // the slot's reads are done before its next copy is issued
+        asm volatile("s_waitcnt lgkmcnt(0)" : : : "memory");
+        copyPair(min(p + 2 * stride, pairs - 1), slot);
+        processPair(cur, p);
         p += stride;
     }
+    // no copy may land in LDS after the wavefront ends
+    asm volatile("s_waitcnt vmcnt(0)" : : : "memory");
 
     if constexpr (kSketch) {
         // the least distance per query over the lane groups h, then over each pair of
