@@ -600,18 +600,33 @@ void mfmaBinaryStreamKernel(ScanArgs scan, PhaseArgs phase, EmitArgs emit, int q
     // that land at slot position l % kChunks, so every copy reads 1 KB of consecutive rows (whole
     // cache lines per quarter-wave). Rows past the corpus re-read its last row (their keys are never
     // emitted). Pair indices stay below 2^31: 32-bit division by the constant kPairs.
+    // this lane's byte offset within a pair for each copy
+    std::uint32_t copy_offset[kPairCopies];
+#pragma unroll
+    for (int k = 0; k < kPairCopies; ++k) {
+        const int r = k * kRowsPerCopy + lane / kChunks;
+        copy_offset[k] = static_cast<std::uint32_t>(r * kRowBytes + ((lane % kChunks) ^ Tile::swizzle(r)) * 16);
+    }
     auto copyPair = [&](long long p, int slot) {
         const std::uint32_t p32 = static_cast<std::uint32_t>(p);
         const std::uint32_t it = p32 / kPairs;
         const long long row0 = phaseBlock(it, phase.stride, phase.skip) * kRows + 32 * static_cast<int>(p32 - it * kPairs);
         const std::uint32_t base = ldsAddress(&pair_lds[wave][slot][0]);
+        if (row0 + 32 <= doc_count) {
+            // a whole pair: a wave-uniform base and the lane's fixed offsets
+            const std::uint8_t* pair_base = corpus + static_cast<std::size_t>(row0) * kRowBytes;
 #pragma unroll
-        for (int k = 0; k < kPairCopies; ++k) {
-            const int r = k * kRowsPerCopy + lane / kChunks;
-            const int position = lane % kChunks;
-            const long long row = min(row0 + r, doc_count - 1);
-            copyToLds(corpus + static_cast<std::size_t>(row) * kRowBytes + (position ^ Tile::swizzle(r)) * 16,
-                      base + k * 1024);
+            for (int k = 0; k < kPairCopies; ++k) {
+                copyToLds(pair_base, copy_offset[k], base + k * 1024);
+            }
+        } else {
+#pragma unroll
+            for (int k = 0; k < kPairCopies; ++k) {
+                const int r = k * kRowsPerCopy + lane / kChunks;
+                const long long row = min(row0 + r, doc_count - 1);
+                copyToLds(corpus + static_cast<std::size_t>(row) * kRowBytes + (copy_offset[k] - r * kRowBytes),
+                          base + k * 1024);
+            }
         }
     };
     // The lane's A chunks of a staged pair: row 16 b + r16, chunk h + 4 jc (the 16 rows of one
