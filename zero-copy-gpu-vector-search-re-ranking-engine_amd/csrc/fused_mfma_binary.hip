@@ -1,32 +1,23 @@
 // Binary (1-bit) MFMA fused scan: Hamming distances of sign-packed corpus rows to a batch of
-// sign-packed queries on the matrix cores (fp4 operands for launches of up to 32 queries, int8
-// for larger ones), with the threshold emission of fused.hpp. The
+// sign-packed queries on the fp4 matrix cores, with the threshold emission of fused.hpp. The
 // reference computes popc(c ^ q) word by word on the VALU (src/cuda/similarity.cu:169-238,
 // hammingScanKernel) and scores (d - 2h) / d (include/zcgvs/cuda/decode.cuh:45-47).
 //
 // Arithmetic. With r the row's bits and q the query's bits as 0/1 values,
-//   sum_k r_k (1 - 2 q_k) = popc(r) - 2 r.q,  so  h = popc(r) + popc(q) - 2 r.q = acc / 64 + popc(q)
-// where acc is the int8 MFMA product of the row's bytes (A) with the query's (B), which are
-// scaled so that every product is 64 r_k (1 - 2 q_k) (below). Integer arithmetic throughout, so
-// h is exact; the score is the reference's IEEE division
-// (d - 2h) / d. A threshold phase compares h itself with the integer threshold equivalent to the
-// query's key threshold (scores are strictly decreasing in h), so the division runs only for
-// keys that pass.
+//   sum_k r_k (1 - 2 q_k) = popc(r) - 2 r.q,  so  h = popc(r) + popc(q) - 2 r.q = acc / 2 + popc(q)
+// where acc is the v_mfma_scale_f32_16x16x128_f8f6f4 product of the row's e2m1 nibbles (A: 0, 1
+// or 2) with the query's (B: +-2 or +-1), chosen so that every product is 2 r_k (1 - 2 q_k)
+// (spreadNibbles, signNibbles). Every value is a small integer (|acc| <= 2 d, far below 2^24), so
+// the fp32 accumulator and h are exact; the score is the reference's IEEE division (d - 2h) / d.
+// A threshold phase compares h itself with the integer threshold equivalent to the query's key
+// threshold (scores are strictly decreasing in h), so the division runs only for keys that pass.
 //
-// Expansion. Each lane turns one 32-bit word of its row into 16 bytes per k-step, half of the
-// word per step: dword j of step half p holds bit 8e + 4p + j of the word in byte e. That is a
-// fixed permutation of the word's dims, and the query's B operand uses the same one; a dot
-// product does not depend on the order of its dims. With s = 4p + j < 7 the dword is
-// word & (0x01010101 << s), bytes of 0 or 2^s, and the query's bytes are (1 - 2 q_k) 2^(6 - s);
-// with s = 7 it is (word >> 7) & 0x01010101 against (1 - 2 q_k) 64. So one AND per dword (and a
-// shift for s = 7), shared by the two query groups of 16 a wavefront serves, and every product
-// is 64 r_k (1 - 2 q_k) (|acc| <= 64 d fits int32 easily).
-//
-// fp4 form (mfmaBinaryStreamKernel). The same identity on v_mfma_scale_f32_16x16x128_f8f6f4 with
-// e2m1 operands: row bits become nibbles of 0, 1 or 2 and query bits +-2 or +-1 (spreadNibbles,
-// signNibbles), every product is 2 r_k (1 - 2 q_k), and the fp32 accumulator holds
-// 2 (popc(r) - 2 r.q) exactly (|acc| <= 2 d, far below 2^24). A step covers 128 dims, one word
-// per lane, twice the int8 form's 64 for the same matrix-core cycles.
+// Expansion. Each lane turns one 32-bit word of its row into 32 nibbles per k-step: nibble e of
+// dword j holds bit 4e + j of the word. That is a fixed permutation of the word's dims, and the
+// query's B operand uses the same one; a dot product does not depend on the order of its dims.
+// Four ANDs and two shifts per word, shared by the two query groups of 16 a wavefront serves. (An
+// int8 form on v_mfma_i32_16x16x64_i8 takes two steps and eight ANDs per word for the same
+// matrix-core cycles per step.)
 //
 // Work split. Launches of up to 32 queries (one set, two MFMA query groups of 16) run
 // mfmaBinaryStreamKernel: the B operands sit in LDS and each of 16 wavefronts streams its own
@@ -36,11 +27,10 @@
 // queries) run mfmaBinaryScanKernel: 8 wavefronts, each with one set's B operands in registers,
 // share the tiles below and split each tile's 16-row blocks among the wavefronts of a set.
 //
-// MFMA layout (v_mfma_i32_16x16x64_i8). Lane l supplies row (A) / query (B) l % 16 and 16 dims
-// of lane group h = l / 16 per step: 16-byte chunk h + 4j of the row covers steps 8j .. 8j + 7,
-// each of its words in turn, in two halves (above); A and B use the same assignment, so every
-// dim is counted once. D: lane l holds query l % 16 and rows 4h + i, i < 4. The fp4 form assigns
-// 32 dims per lane and step: chunk h + 4j covers steps 4j .. 4j + 3, one word each; D as above.
+// MFMA layout (16x16x128, fp4 operands). Lane l supplies row (A) / query (B) l % 16 and 32 dims
+// of lane group h = l / 16 per step: 16-byte chunk h + 4j of the row covers steps 4j .. 4j + 3,
+// one word each; A and B use the same assignment, so every dim is counted once. D: lane l holds
+// query l % 16 and rows 4h + i, i < 4.
 //
 // Corpus streaming as in the other MFMA scans (lds_copy.hpp): 48 KB tiles HBM -> LDS by
 // global_load_lds_dwordx4 in a 3-deep ring (smaller tiles in deeper rings measured slower: the
@@ -76,7 +66,6 @@ struct BinaryTile {
     static constexpr int kRowBytes = kWords * 4;
     static constexpr int kChunks = kRowBytes / 16;
     static constexpr int kLaneChunks = kChunks / 4;  // chunks per lane group
-    static constexpr int kSteps = kLaneChunks * 8;   // 64 dims per step
     static constexpr int kRows = kTileBytesTarget / kRowBytes;
     static constexpr int kRowBlocks = kRows / 16;
     static constexpr int kTileBytes = kRows * kRowBytes;
@@ -91,37 +80,9 @@ struct BinaryTile {
     }
 };
 
-// Half p of a row word -> 16 bytes: byte e of dword j is bit 8e + s (s = 4p + j) of the word,
-// times 2^s for s < 7 and times 1 for s = 7.
-__device__ __forceinline__ v4i spreadWord(std::uint32_t word, int p) {
-    v4i out;
-#pragma unroll
-    for (int j = 0; j < 4; ++j) {
-        const int shift = 4 * p + j;
-        out[j] = static_cast<int>(shift < 7 ? word & (0x01010101u << shift) : (word >> 7) & 0x01010101u);
-    }
-    return out;
-}
-
-// The same 16 dims of a query word as spreadWord, as bytes of (1 - 2 bit) w with w = 2^(6 - s)
-// for s < 7 and w = 64 for s = 7, so that every product with spreadWord's byte is 64 r (1 - 2 q).
-__device__ __forceinline__ v4i signWord(std::uint32_t word, int p) {
-    v4i out;
-#pragma unroll
-    for (int j = 0; j < 4; ++j) {
-        const int shift = 4 * p + j;
-        const std::uint32_t w = shift < 7 ? 1u << (6 - shift) : 64u;
-        const std::uint32_t bits = (word >> shift) & 0x01010101u;
-        // per byte w (bit clear) or 256 - w (bit set, i.e. -w as int8); no carries between bytes
-        out[j] = static_cast<int>(w * 0x01010101u + bits * (256u - 2u * w));
-    }
-    return out;
-}
-
-// fp4 (e2m1) operands of the stream kernel: nibble 0010 is 1, 0100 is 2 and bit 3 is the sign
-// (every value used is a normal number). A row word becomes 32 nibbles: nibble e of dword j holds
-// bit 4e + j of the word, as 0 or 1 (j < 2, the bit moved to nibble bit 1) or 0 or 2 (j >= 2, moved
-// to nibble bit 2). Four ANDs and two shifts per 32 dims, against eight ANDs for the int8 form.
+// fp4 (e2m1) operands: nibble 0010 is 1, 0100 is 2 and bit 3 is the sign (every value used is a
+// normal number). A row word becomes 32 nibbles: nibble e of dword j holds bit 4e + j of the word,
+// as 0 or 1 (j < 2, the bit moved to nibble bit 1) or 0 or 2 (j >= 2, moved to nibble bit 2).
 __device__ __forceinline__ v4i spreadNibbles(std::uint32_t word) {
     v4i out;
     out[0] = static_cast<int>((word << 1) & 0x22222222u);
@@ -152,13 +113,6 @@ __device__ __forceinline__ v4f mfmaNibbles(const v4i& a, const v4i& b, const v4f
     const v8i a8 = __builtin_shufflevector(a, a, 0, 1, 2, 3, 0, 1, 2, 3);
     const v8i b8 = __builtin_shufflevector(b, b, 0, 1, 2, 3, 0, 1, 2, 3);
     return __builtin_amdgcn_mfma_scale_f32_16x16x128_f8f6f4(a8, b8, c, kFp4, kFp4, 0, kScaleOne, 0, kScaleOne);
-}
-
-// The word of step t (lane group h) from the lane's chunk words: chunk jc = t / 8, word
-// (t % 8) / 2; the step takes its half t % 2.
-template <int kLaneChunks>
-__device__ __forceinline__ std::uint32_t stepWord(const u32x4 (&chunk)[kLaneChunks], int t) {
-    return chunk[t / 8][(t % 8) / 2];
 }
 
 // The integer form of query q's key threshold in a threshold phase: a key passes when h < h_limit,
@@ -192,7 +146,7 @@ void mfmaBinaryScanKernel(ScanArgs scan, PhaseArgs phase, EmitArgs emit, int q_o
     constexpr int kRowBytes = Tile::kRowBytes;
     constexpr int kChunks = Tile::kChunks;
     constexpr int kLaneChunks = Tile::kLaneChunks;
-    constexpr int kSteps = Tile::kSteps;
+    constexpr int kSteps = kLaneChunks * 4;  // one word (32 dims) per lane and step, 128 per step
     constexpr int kDepth = Tile::kDepth;
     constexpr int kCopies = Tile::kCopies;
     constexpr int kRowBlocks = Tile::kRowBlocks;
@@ -249,7 +203,7 @@ void mfmaBinaryScanKernel(ScanArgs scan, PhaseArgs phase, EmitArgs emit, int q_o
         popq[g] = pop;
 #pragma unroll
         for (int t = 0; t < kSteps; ++t) {
-            qb[g][t] = valid_of[g] ? signWord(stepWord<kLaneChunks>(chunk, t), t % 2) : v4i{0, 0, 0, 0};
+            qb[g][t] = valid_of[g] ? signNibbles(chunk[t / 4][t % 4]) : v4i{0, 0, 0, 0};
         }
         h_limit[g] = kDim + 1;  // no threshold: every h passes
         row_limit[g] = 0xFFFFFFFFu;
@@ -257,11 +211,11 @@ void mfmaBinaryScanKernel(ScanArgs scan, PhaseArgs phase, EmitArgs emit, int q_o
             binaryThreshold<kDim>(emit, q, h_limit[g], row_limit[g]);
         }
     }
-    // acc threshold of the fast reject (acc = 64 (h - popc(q)); invalid queries never pass)
-    int acc_limit[2];
+    // acc threshold of the fast reject (acc = 2 (h - popc(q)); invalid queries never pass)
+    float acc_limit[2];
 #pragma unroll
     for (int g = 0; g < 2; ++g) {
-        acc_limit[g] = 64 * (valid_of[g] ? h_limit[g] - popq[g] : -(kDim + 1));
+        acc_limit[g] = static_cast<float>(2 * (valid_of[g] ? h_limit[g] - popq[g] : -(kDim + 1)));
     }
     for (int i = tid; i < kQueriesPerLaunch; i += kThreads) {
         lds_count[i] = 0u;
@@ -325,7 +279,7 @@ void mfmaBinaryScanKernel(ScanArgs scan, PhaseArgs phase, EmitArgs emit, int q_o
         a_off[jc] = static_cast<std::uint32_t>(r16 * kRowBytes + ((h + 4 * jc) ^ Tile::swizzle(r16)) * 16);
     }
 
-    auto emitKeys = [&](const v4i& acc, int g, long long row0, int block, long long item_) {
+    auto emitKeys = [&](const v4f& acc, int g, long long row0, int block, long long item_) {
         if (!valid_of[g]) {
             return;
         }
@@ -334,7 +288,7 @@ void mfmaBinaryScanKernel(ScanArgs scan, PhaseArgs phase, EmitArgs emit, int q_o
         for (int i = 0; i < 4; ++i) {
             const int local = block * 16 + 4 * h + i;
             const long long row = row0 + local;
-            const int hd = (acc[i] >> 6) + popq[g];  // acc is 64 times the +-1 dot, exactly
+            const int hd = (static_cast<int>(acc[i]) >> 1) + popq[g];  // acc = 2 (h - popc(q)), exactly
             if constexpr (kDense) {
                 std::uint64_t key = 0ull;
                 if (row < doc_count) {
@@ -371,8 +325,8 @@ void mfmaBinaryScanKernel(ScanArgs scan, PhaseArgs phase, EmitArgs emit, int q_o
                 for (int jc = 0; jc < kLaneChunks; ++jc) {
                     chunk[jc] = *reinterpret_cast<const u32x4*>(rows + a_off[jc]);
                 }
-                v4i acc0 = {0, 0, 0, 0};
-                v4i acc1 = {0, 0, 0, 0};
+                v4f acc0 = {0.0f, 0.0f, 0.0f, 0.0f};
+                v4f acc1 = {0.0f, 0.0f, 0.0f, 0.0f};
                 // One path for one or two query groups (the second group's B operands are zero
                 // when it has no queries), so the compiler has no two copies of the expansion
                 // to hoist. The A operand is double-buffered: step t's MFMAs are issued first,
@@ -380,13 +334,13 @@ void mfmaBinaryScanKernel(ScanArgs scan, PhaseArgs phase, EmitArgs emit, int q_o
                 // not reading, so the VALU work runs under the MFMAs instead of waiting for them
                 // to read their operands; a sched_barrier per step pins that order.
                 v4i a[2];
-                a[0] = spreadWord(stepWord<kLaneChunks>(chunk, 0), 0);
+                a[0] = spreadNibbles(chunk[0][0]);
 #pragma unroll
                 for (int t = 0; t < kSteps; ++t) {
-                    acc0 = __builtin_amdgcn_mfma_i32_16x16x64_i8(a[t % 2], qb[0][t], acc0, 0, 0, 0);
-                    acc1 = __builtin_amdgcn_mfma_i32_16x16x64_i8(a[t % 2], qb[1][t], acc1, 0, 0, 0);
+                    acc0 = mfmaNibbles(a[t % 2], qb[0][t], acc0);
+                    acc1 = mfmaNibbles(a[t % 2], qb[1][t], acc1);
                     if (t + 1 < kSteps) {
-                        a[(t + 1) % 2] = spreadWord(stepWord<kLaneChunks>(chunk, t + 1), (t + 1) % 2);
+                        a[(t + 1) % 2] = spreadNibbles(chunk[(t + 1) / 4][(t + 1) % 4]);
                         // keeps step t's operand allocated until the expansion is written, so
                         // the two buffers never share registers
                         asm volatile("" ::"v"(a[t % 2]));
@@ -399,10 +353,10 @@ void mfmaBinaryScanKernel(ScanArgs scan, PhaseArgs phase, EmitArgs emit, int q_o
                         emitKeys(acc1, 1, row0, block, item);
                     }
                 } else {
-                    // Fast reject: a key can pass only if acc <= 64 (h_limit - popc(q)) (h = acc / 64 +
+                    // Fast reject: a key can pass only if acc <= 2 (h_limit - popc(q)) (h = acc / 2 +
                     // popc(q)); one ballot over the wavefront's 8 products usually ends here.
-                    const int m0 = min(min(acc0[0], acc0[1]), min(acc0[2], acc0[3]));
-                    const int m1 = min(min(acc1[0], acc1[1]), min(acc1[2], acc1[3]));
+                    const float m0 = fminf(fminf(acc0[0], acc0[1]), fminf(acc0[2], acc0[3]));
+                    const float m1 = fminf(fminf(acc1[0], acc1[1]), fminf(acc1[2], acc1[3]));
                     const bool maybe = m0 <= acc_limit[0] || m1 <= acc_limit[1];
                     if (__builtin_amdgcn_ballot_w64(maybe) != 0) {
                         emitKeys(acc0, 0, row0, block, item);
