@@ -21,10 +21,10 @@
 //
 // Work split. Launches of up to 32 queries (one set, two MFMA query groups of 16) run
 // mfmaBinaryStreamKernel: the B operands sit in LDS and each of 16 wavefronts streams its own
-// rows through LDS slots of its own (no shared tile, no barrier). It also serves the sketch plan of a search of
-// at most 32 queries: a sketch mode (the least distance of each query per pair of wavefronts, no
-// keys) and a rerun mode (the device list of flagged queries). Larger launches (up to 4 sets, 128
-// queries) run mfmaBinaryScanKernel: 8 wavefronts, each with one set's B operands in registers,
+// rows through LDS slots of its own (no shared tile, no barrier). Batches of up to 64 queries
+// run it once per set, and it serves their sketch plan: a sketch mode (the least distance of each
+// query per pair of wavefronts, no keys) and a rerun mode (the device list of flagged queries).
+// Larger batches launch up to 4 sets (128 queries) at a time on mfmaBinaryScanKernel: 8 wavefronts, each with one set's B operands in registers,
 // share the tiles below and split each tile's 16-row blocks among the wavefronts of a set.
 //
 // MFMA layout (16x16x128, fp4 operands). Lane l supplies row (A) / query (B) l % 16 and 32 dims
@@ -58,6 +58,9 @@ constexpr int kThreads = 512;
 constexpr int kWaves = kThreads / kWave;
 constexpr int kSetQueries = 32;  // two MFMA query groups of 16 per wavefront
 constexpr int kQueriesPerLaunch = 4 * kSetQueries;
+// Batches up to this size run the stream kernel once per set (and so the sketch plan); larger
+// ones the tile kernel, which reads each row once for up to four sets.
+constexpr int kStreamMaxBatch = 2 * kSetQueries;
 constexpr int kTileBytesTarget = 48 * 1024;
 constexpr int kMinBatch = 4;  // below this the VALU popcount scan does less work per row
 
@@ -740,8 +743,9 @@ int launchShape(const ScanArgs& scan, const PhaseArgs& phase, const EmitArgs& em
                 hipStream_t stream) {
     const long long wanted = phase.dense ? std::min<long long>(phase.items, workgroups) : workgroups;
     const dim3 grid(static_cast<unsigned>(std::max(1LL, wanted)));
-    for (int q0 = 0; q0 < scan.batch; q0 += kQueriesPerLaunch) {
-        const int count = std::min(kQueriesPerLaunch, scan.batch - q0);
+    const int per_launch = scan.batch <= kStreamMaxBatch ? kSetQueries : kQueriesPerLaunch;
+    for (int q0 = 0; q0 < scan.batch; q0 += per_launch) {
+        const int count = std::min(per_launch, scan.batch - q0);
         if (count <= kSetQueries) {
             // one query set: the streaming kernel
             if (phase.dense) {
@@ -782,7 +786,7 @@ bool mfmaBinarySupported(const ScanArgs& scan) {
     return scan.dim == 512 || scan.dim == 1024;
 }
 
-bool mfmaBinaryStreams(const ScanArgs& scan) { return scan.batch <= kSetQueries; }
+bool mfmaBinaryStreams(const ScanArgs& scan) { return scan.batch <= kStreamMaxBatch; }
 
 int mfmaBinarySketchSlotsPerWorkgroup() { return kStreamSketchSlots; }
 
