@@ -207,7 +207,7 @@ BIN_N, BIN_DIM = 2_000_003, 1024
 def binary_corpus(gpu):
     capi = gpu
     words = np.random.default_rng(94).integers(0, 2**32, size=(BIN_N, BIN_DIM // 32), dtype=np.uint32)
-    queries = normalized(32, BIN_DIM, 95)
+    queries = normalized(64, BIN_DIM, 95)
     return dict(words=words, qwords=oracle.pack_binary(queries), d_words=capi.DeviceArray.from_host(words),
                 d_queries=capi.DeviceArray.from_host(queries))
 
@@ -217,8 +217,10 @@ def _binary_desc(capi, c, batch, k, flags=0):
     return capi.search_desc(store, c["d_queries"], batch, k, capi.COSINE, flags=flags)
 
 
-@pytest.mark.parametrize("batch,k", [(32, 100), (20, 1000)])
+@pytest.mark.parametrize("batch,k", [(32, 100), (20, 1000), (64, 100), (48, 1000)])
 def test_binary_sketch_plan(gpu, binary_corpus, batch, k):
+    # up to 32 queries one stream launch per phase, 33-64 one per set of 32 (and reruns of more
+    # than 32 flagged queries in two list launches)
     capi = gpu
     c = binary_corpus
     desc = _binary_desc(capi, c, batch, k)
@@ -234,7 +236,7 @@ def test_binary_sketch_plan(gpu, binary_corpus, batch, k):
             assert int(np.count_nonzero(got_flags)) > batch // 2, f"{name}: expected most queries flagged"
         assert np.array_equal(got_idx, idx), f"{name}: ids differ from the speculative path's"
         assert np.array_equal(got_val, val), f"{name}: scores differ from the speculative path's"
-    sample = [0, 7, 16, batch - 1]
+    sample = sorted({0, 7, 16, batch // 2 + 3, batch - 1})
     ref = oracle.scores_hamming(c["words"], c["qwords"][sample], BIN_DIM)
     assert_topk_equivalent(idx[sample], val[sample], ref, k)
 
