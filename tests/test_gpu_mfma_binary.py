@@ -1,8 +1,9 @@
 """Batched binary (Hamming) searches, the matrix-core scan, against the CPU oracle: ids and
 scores bit-exact under the lowest-index tie-break.
 
-Batches of 4 or more queries over 512- or 1024-dim sign-packed rows take the MFMA scan. The cases
-cover both row sizes, partial query groups and sets (17, 33, 100), a batch over two launches (130),
+Batches of 4 or more queries over 512- or 1024-dim sign-packed rows take the MFMA scans: up to 64
+queries the stream kernel, once per set of 32, and more the tile kernel. The cases cover both row
+sizes on both kernels, partial query groups and sets (17, 33, 100), a batch over two launches (130),
 k from 1 to 1000 (Hamming scores tie massively at the k-th place), a partial last tile, queries
 whose bits are all clear or all set, and duplicated rows."""
 
@@ -27,6 +28,7 @@ def search(capi, words, dim, queries, k):
 @pytest.mark.parametrize("n,dim,batch,k", [
     (70_001, 512, 4, 10),
     (70_001, 512, 33, 100),
+    (70_001, 512, 100, 10),      # the tile kernel at 512 bits
     (70_001, 1024, 17, 1),
     (120_007, 1024, 32, 10),
     (120_007, 1024, 100, 100),
