@@ -184,12 +184,12 @@ def test_sketch_plan_samples_then_scans_everything(capi, n, batch, k, stride):
     (50_000_000, 32, 1000, 64, True),   # the binary 50M x 1024 configuration's Hamming stage
     (2_000_003, 20, 100, 4, True),      # every 4th 384-row block, ragged tail
     (50_000_000, 64, 1000, 64, True),   # two sets of 32, streamed one launch per set
-    (50_000_000, 65, 1000, 0, False),   # more than 64 queries: the tile scan, threshold phases
+    (50_000_000, 128, 1000, 64, True),  # more than 64: sketched set by set, the full scan on the tile kernel
     (1_000_000, 32, 100, 0, False),     # under 4 sampled blocks per workgroup: threshold phases
 ])
 def test_binary_sketch_plan(capi, n, batch, k, stride, sketched):
-    # The binary streaming scan (batches of at most 64 queries, one launch per set of 32) takes the
-    # sketch plan with 384-row blocks of 1024-bit rows.
+    # A binary search takes the sketch plan (the streaming kernel's sketch launches, one per set of
+    # 32 queries) with 384-row blocks of 1024-bit rows, when every workgroup sees 4 sampled blocks.
     rows = capi.search_phase_rows(_desc(capi, n=n, dim=1024, dtype=capi.BINARY, batch=batch, k=k))
     if sketched:
         blocks = (n + 383) // 384

@@ -176,8 +176,8 @@ int launchMfmaSplitScan(const ScanArgs& scan, const PhaseArgs& phase, const Emit
 // dim 512 or 1024).
 bool mfmaBinarySupported(const ScanArgs& scan);
 int mfmaBinaryBlockRows(const ScanArgs& scan);
-// Whether the batch runs the streaming kernel (at most 32 queries), the binary scan with sketch
-// and rerun modes; its sketch slots per workgroup.
+// Whether the binary scan can take the sketch plan (its streaming kernel has the sketch and rerun
+// modes, one launch per set of 32 queries, at any batch size); its sketch slots per workgroup.
 bool mfmaBinaryStreams(const ScanArgs& scan);
 int mfmaBinarySketchSlotsPerWorkgroup();
 int launchMfmaBinaryScan(const ScanArgs& scan, const PhaseArgs& phase, const EmitArgs& emit,

@@ -21,11 +21,13 @@
 //
 // Work split. Launches of up to 32 queries (one set, two MFMA query groups of 16) run
 // mfmaBinaryStreamKernel: the B operands sit in LDS and each of 16 wavefronts streams its own
-// rows through LDS slots of its own (no shared tile, no barrier). Batches of up to 64 queries
-// run it once per set, and it serves their sketch plan: a sketch mode (the least distance of each
-// query per pair of wavefronts, no keys) and a rerun mode (the device list of flagged queries).
-// Larger batches launch up to 4 sets (128 queries) at a time on mfmaBinaryScanKernel: 8 wavefronts, each with one set's B operands in registers,
-// share the tiles below and split each tile's 16-row blocks among the wavefronts of a set.
+// rows through LDS slots of its own (no shared tile, no barrier). It serves the sketch plan of
+// any batch, one launch per set: a sketch mode (the least distance of each query per pair of
+// wavefronts, no keys) and a rerun mode (the device list of flagged queries); batches of up to 64
+// queries also run their scans on it. Larger batches scan up to 4 sets (128 queries) at a time on
+// mfmaBinaryScanKernel: 8 wavefronts, each with two sets' B operands in registers (four query
+// groups, so each row expansion feeds four MFMAs), share the tiles below and split each tile's
+// 16-row blocks among the wavefronts that serve the same queries.
 //
 // MFMA layout (16x16x128, fp4 operands). Lane l supplies row (A) / query (B) l % 16 and 32 dims
 // of lane group h = l / 16 per step: 16-byte chunk h + 4j of the row covers steps 4j .. 4j + 3,
@@ -58,8 +60,9 @@ constexpr int kThreads = 512;
 constexpr int kWaves = kThreads / kWave;
 constexpr int kSetQueries = 32;  // two MFMA query groups of 16 per wavefront
 constexpr int kQueriesPerLaunch = 4 * kSetQueries;
-// Batches up to this size run the stream kernel once per set (and so the sketch plan); larger
-// ones the tile kernel, which reads each row once for up to four sets.
+constexpr int kTileSetsPerWave = 2;  // the tile kernel's wavefronts serve 64 queries each
+// Batches up to this size scan on the stream kernel once per set; larger ones on the tile kernel,
+// which reads each row once for up to four sets.
 constexpr int kStreamMaxBatch = 2 * kSetQueries;
 constexpr int kTileBytesTarget = 48 * 1024;
 constexpr int kMinBatch = 4;  // below this the VALU popcount scan does less work per row
@@ -154,6 +157,7 @@ void mfmaBinaryScanKernel(ScanArgs scan, PhaseArgs phase, EmitArgs emit, int q_o
     constexpr int kCopies = Tile::kCopies;
     constexpr int kRowBlocks = Tile::kRowBlocks;
     constexpr int kDim = kWords * 32;
+    constexpr int kGroups = 2 * kTileSetsPerWave;  // query groups of 16 per wavefront
 
     __shared__ __attribute__((aligned(16))) std::uint8_t ring[kDepth][Tile::kTileBytes];
     __shared__ std::uint32_t lds_count[kQueriesPerLaunch];
@@ -163,26 +167,32 @@ void mfmaBinaryScanKernel(ScanArgs scan, PhaseArgs phase, EmitArgs emit, int q_o
     const int wave = __builtin_amdgcn_readfirstlane(tid / kWave);  // wave-uniform: scalar indexing
     const int r16 = lane & 15;
     const int h = lane >> 4;
-    const int sets = (q_count + kSetQueries - 1) / kSetQueries;
-    const int waves_per_set = kWaves / sets;
-    const bool wave_active = wave < sets * waves_per_set;
-    const int set = wave % sets;
-    const int first_block = wave / sets;
-    const bool two_groups = set * kSetQueries + 16 < q_count;  // wave-uniform
+    // wavefront sets of kTileSetsPerWave query sets each; the launch's wavefronts split among them
+    const int wave_sets = (q_count + kTileSetsPerWave * kSetQueries - 1) / (kTileSetsPerWave * kSetQueries);
+    const int waves_per_set = kWaves / wave_sets;
+    const bool wave_active = wave < wave_sets * waves_per_set;
+    const int wave_set = wave % wave_sets;
+    const int first_block = wave / wave_sets;
+    const int first_query = wave_set * kTileSetsPerWave * kSetQueries;
+    bool live[kGroups];  // the group has queries (wave-uniform)
+#pragma unroll
+    for (int g = 0; g < kGroups; ++g) {
+        live[g] = first_query + g * 16 < q_count;
+    }
     const long long doc_count = scan.doc_count;
     const std::uint8_t* corpus = static_cast<const std::uint8_t*>(scan.corpus);
     const std::uint32_t* qwords = static_cast<const std::uint32_t*>(scan.queries);
 
-    // ---- per query group g of the set: B operands, popc(q), integer threshold ----
-    v4i qb[2][kSteps];
-    int popq[2];
-    int q_of[2];
-    bool valid_of[2];
-    int h_limit[2];          // keys pass when h < h_limit, or h == h_limit and row < row_limit
-    std::uint32_t row_limit[2];
+    // ---- per query group g of the wavefront: B operands, popc(q), integer threshold ----
+    v4i qb[kGroups][kSteps];
+    int popq[kGroups];
+    int q_of[kGroups];
+    bool valid_of[kGroups];
+    int h_limit[kGroups];  // keys pass when h < h_limit, or h == h_limit and row < row_limit
+    std::uint32_t row_limit[kGroups];
 #pragma unroll
-    for (int g = 0; g < 2; ++g) {
-        const int qlocal = set * kSetQueries + g * 16 + r16;
+    for (int g = 0; g < kGroups; ++g) {
+        const int qlocal = first_query + g * 16 + r16;
         valid_of[g] = wave_active && qlocal < q_count;
         const int q = q_offset + min(qlocal, q_count - 1);
         q_of[g] = q;
@@ -215,9 +225,9 @@ void mfmaBinaryScanKernel(ScanArgs scan, PhaseArgs phase, EmitArgs emit, int q_o
         }
     }
     // acc threshold of the fast reject (acc = 2 (h - popc(q)); invalid queries never pass)
-    float acc_limit[2];
+    float acc_limit[kGroups];
 #pragma unroll
-    for (int g = 0; g < 2; ++g) {
+    for (int g = 0; g < kGroups; ++g) {
         acc_limit[g] = static_cast<float>(2 * (valid_of[g] ? h_limit[g] - popq[g] : -(kDim + 1)));
     }
     for (int i = tid; i < kQueriesPerLaunch; i += kThreads) {
@@ -328,11 +338,14 @@ void mfmaBinaryScanKernel(ScanArgs scan, PhaseArgs phase, EmitArgs emit, int q_o
                 for (int jc = 0; jc < kLaneChunks; ++jc) {
                     chunk[jc] = *reinterpret_cast<const u32x4*>(rows + a_off[jc]);
                 }
-                v4f acc0 = {0.0f, 0.0f, 0.0f, 0.0f};
-                v4f acc1 = {0.0f, 0.0f, 0.0f, 0.0f};
-                // One path for one or two query groups (the second group's B operands are zero
-                // when it has no queries), so the compiler has no two copies of the expansion
-                // to hoist. The A operand is double-buffered: step t's MFMAs are issued first,
+                v4f acc[kGroups];
+#pragma unroll
+                for (int g = 0; g < kGroups; ++g) {
+                    acc[g] = v4f{0.0f, 0.0f, 0.0f, 0.0f};
+                }
+                // One path for any number of live query groups (a group without queries has zero
+                // B operands), so the compiler has no several copies of the expansion to hoist;
+                // each expansion feeds every group's MFMA. The A operand is double-buffered: step t's MFMAs are issued first,
                 // then step t + 1's expansion into the other buffer, which the matrix core is
                 // not reading, so the VALU work runs under the MFMAs instead of waiting for them
                 // to read their operands; a sched_barrier per step pins that order.
@@ -340,8 +353,10 @@ void mfmaBinaryScanKernel(ScanArgs scan, PhaseArgs phase, EmitArgs emit, int q_o
                 a[0] = spreadNibbles(chunk[0][0]);
 #pragma unroll
                 for (int t = 0; t < kSteps; ++t) {
-                    acc0 = mfmaNibbles(a[t % 2], qb[0][t], acc0);
-                    acc1 = mfmaNibbles(a[t % 2], qb[1][t], acc1);
+#pragma unroll
+                    for (int g = 0; g < kGroups; ++g) {
+                        acc[g] = mfmaNibbles(a[t % 2], qb[g][t], acc[g]);
+                    }
                     if (t + 1 < kSteps) {
                         a[(t + 1) % 2] = spreadNibbles(chunk[(t + 1) / 4][(t + 1) % 4]);
                         // keeps step t's operand allocated until the expansion is written, so
@@ -351,20 +366,27 @@ void mfmaBinaryScanKernel(ScanArgs scan, PhaseArgs phase, EmitArgs emit, int q_o
                     __builtin_amdgcn_sched_barrier(0);
                 }
                 if constexpr (kDense) {
-                    emitKeys(acc0, 0, row0, block, item);
-                    if (two_groups) {
-                        emitKeys(acc1, 1, row0, block, item);
+#pragma unroll
+                    for (int g = 0; g < kGroups; ++g) {
+                        if (live[g]) {
+                            emitKeys(acc[g], g, row0, block, item);
+                        }
                     }
                 } else {
                     // Fast reject: a key can pass only if acc <= 2 (h_limit - popc(q)) (h = acc / 2 +
-                    // popc(q)); one ballot over the wavefront's 8 products usually ends here.
-                    const float m0 = fminf(fminf(acc0[0], acc0[1]), fminf(acc0[2], acc0[3]));
-                    const float m1 = fminf(fminf(acc1[0], acc1[1]), fminf(acc1[2], acc1[3]));
-                    const bool maybe = m0 <= acc_limit[0] || m1 <= acc_limit[1];
+                    // popc(q)); one ballot over the wavefront's products usually ends here.
+                    bool maybe = false;
+#pragma unroll
+                    for (int g = 0; g < kGroups; ++g) {
+                        const float m = fminf(fminf(acc[g][0], acc[g][1]), fminf(acc[g][2], acc[g][3]));
+                        maybe = maybe || m <= acc_limit[g];
+                    }
                     if (__builtin_amdgcn_ballot_w64(maybe) != 0) {
-                        emitKeys(acc0, 0, row0, block, item);
-                        if (two_groups) {
-                            emitKeys(acc1, 1, row0, block, item);
+#pragma unroll
+                        for (int g = 0; g < kGroups; ++g) {
+                            if (live[g]) {
+                                emitKeys(acc[g], g, row0, block, item);
+                            }
                         }
                     }
                 }
@@ -743,7 +765,10 @@ int launchShape(const ScanArgs& scan, const PhaseArgs& phase, const EmitArgs& em
                 hipStream_t stream) {
     const long long wanted = phase.dense ? std::min<long long>(phase.items, workgroups) : workgroups;
     const dim3 grid(static_cast<unsigned>(std::max(1LL, wanted)));
-    const int per_launch = scan.batch <= kStreamMaxBatch ? kSetQueries : kQueriesPerLaunch;
+    // sketch and rerun launches always stream, set by set; threshold and dense phases stream up to
+    // kStreamMaxBatch queries and run the tile kernel beyond
+    const bool streamed = scan.batch <= kStreamMaxBatch || phase.sketch != 0 || emit.q_list != nullptr;
+    const int per_launch = streamed ? kSetQueries : kQueriesPerLaunch;
     for (int q0 = 0; q0 < scan.batch; q0 += per_launch) {
         const int count = std::min(per_launch, scan.batch - q0);
         if (count <= kSetQueries) {
@@ -786,7 +811,7 @@ bool mfmaBinarySupported(const ScanArgs& scan) {
     return scan.dim == 512 || scan.dim == 1024;
 }
 
-bool mfmaBinaryStreams(const ScanArgs& scan) { return scan.batch <= kStreamMaxBatch; }
+bool mfmaBinaryStreams(const ScanArgs& scan) { return scan.dtype == ZCGVS_DTYPE_BINARY; }
 
 int mfmaBinarySketchSlotsPerWorkgroup() { return kStreamSketchSlots; }
 
