@@ -334,7 +334,7 @@ size_t zcgvs_search_workspace_bytes(const zcgvs_search_desc* desc);
  * zcgvs_search_workspace_bytes(desc) bytes; its contents need no initialization. Capture safe.
  * The result is the exact top-k for every input: the scan keeps only candidates above a sampled
  * threshold in bounded per-workgroup buffers. A per-vector int8 search on the matrix cores, or a
- * binary search, over a large corpus is sketch-planned: a first launch over
+ * binary search of 4 or more queries at 512 or 1024 bits, over a large corpus is sketch-planned: a first launch over
  * every 32nd block (64th for binary) records per slot (a row half of an int8 workgroup, a pair of a binary
  * workgroup's wavefronts) the best score of each query, and one scan of the whole corpus keeps
  * the keys at or above the j-th best of those scores (a threshold that is likely, not certain, to
