@@ -242,9 +242,9 @@ def scan_kernel_name(w):
         lexical = "true" if w["kind"] == "hybrid" else "false"
         return f"mfmaFloatScanKernel<{kind}, {w['dim']}, false, {lexical}>"
     if w["kind"] == "binary" and w["batch"] >= 4 and w["dim"] in (512, 1024):
-        # batches of up to 64 queries: the streaming kernel, one launch per set of 32 (mode 0:
-        # threshold scan); more: the shared-tile kernel
-        if w["batch"] <= 64:
+        # one set of up to 32 queries: the streaming kernel (mode 0: threshold scan); more: the
+        # shared-tile kernel
+        if w["batch"] <= 32:
             return f"mfmaBinaryStreamKernel<{w['dim'] // 32}, 0>"
         return f"mfmaBinaryScanKernel<{w['dim'] // 32}, false>"
     if w["batch"] <= 4:

@@ -183,7 +183,7 @@ def test_sketch_plan_samples_then_scans_everything(capi, n, batch, k, stride):
 @pytest.mark.parametrize("n,batch,k,stride,sketched", [
     (50_000_000, 32, 1000, 64, True),   # the binary 50M x 1024 configuration's Hamming stage
     (2_000_003, 20, 100, 4, True),      # every 4th 384-row block, ragged tail
-    (50_000_000, 64, 1000, 64, True),   # two sets of 32, streamed one launch per set
+    (50_000_000, 64, 1000, 64, True),   # two sets of 32: sketch launches per set
     (50_000_000, 128, 1000, 64, True),  # more than 64: sketched set by set, the full scan on the tile kernel
     (1_000_000, 32, 100, 0, False),     # under 4 sampled blocks per workgroup: threshold phases
 ])

@@ -65,7 +65,7 @@ def _binary_desc(capi, n, dim, batch, k, seed):
     (_int8_desc, 1_000_000, 256, 256, 100),     # sketch plan: sketch, thresholds, one scan, merge
     (_int8_tiny_desc, 1_000_000, 256, 256, 100),  # sketch plan with every query rerun
     (_binary_desc, 2_000_003, 1024, 32, 100),   # binary sketch plan
-    (_binary_desc, 2_000_003, 1024, 64, 100),   # two stream launches per phase
+    (_binary_desc, 2_000_003, 1024, 64, 100),   # two sketch launches, the full scan on the tile kernel
     (_binary_desc, 2_000_003, 1024, 128, 100),  # sketch streamed set by set, full scan on the tile kernel
 ])
 def test_graph_replays_match_direct_calls(gpu, make, n, dim, batch, k):

@@ -219,8 +219,8 @@ def _binary_desc(capi, c, batch, k, flags=0):
 
 @pytest.mark.parametrize("batch,k", [(32, 100), (20, 1000), (64, 100), (48, 1000)])
 def test_binary_sketch_plan(gpu, binary_corpus, batch, k):
-    # up to 32 queries one stream launch per phase, 33-64 one per set of 32 (and reruns of more
-    # than 32 flagged queries in two list launches)
+    # up to 32 queries one stream launch per phase; 33-64 one sketch launch per set of 32, the full
+    # scan on the tile kernel, and reruns of more than 32 flagged queries in two list launches
     capi = gpu
     c = binary_corpus
     desc = _binary_desc(capi, c, batch, k)

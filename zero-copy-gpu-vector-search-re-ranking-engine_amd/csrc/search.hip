@@ -465,7 +465,7 @@ Plan makePlan(const zcgvs_search_desc& d) {
     plan.full.items = blocks;
     plan.full.block_rows = plan.block_rows;
     // (the binary scan runs the sketch and the rerun in its streaming kernel, one launch per set of 32
-    // queries; its full scan streams too up to 64 queries and runs the tile kernel beyond)
+    // queries; its full scan streams too for one set and runs the tile kernel beyond)
     const bool binary_sketch = plan.use_mfma_binary && mfmaBinaryStreams(probe);
     plan.rerun = plan.use_mfma;
     // Segment capacity: 4x the expected candidates per (segment, query) of the widest phase.
