@@ -24,10 +24,10 @@
 // rows through LDS slots of its own (no shared tile, no barrier). It serves the sketch plan of
 // any batch, one launch per set: a sketch mode (the least distance of each query per pair of
 // wavefronts, no keys) and a rerun mode (the device list of flagged queries). Larger batches scan
-// up to 4 sets (128 queries) at a time on mfmaBinaryScanKernel: 8 wavefronts, each with two sets'
-// B operands in registers (four query groups, so each row expansion feeds four MFMAs), share the
-// tiles below and split each tile's 16-row blocks among the wavefronts that serve the same
-// queries.
+// up to 4 sets (128 queries) at a time on mfmaBinaryScanKernel: 12 wavefronts, three per SIMD,
+// each with one set's B operands in registers, share the tiles below and split each tile's 16-row
+// blocks among the wavefronts of a set. (Eight wavefronts serving two sets each, four query groups
+// per row expansion, measured 1-16% slower: at 96 queries a third of their groups are empty.)
 //
 // MFMA layout (16x16x128, fp4 operands). Lane l supplies row (A) / query (B) l % 16 and 32 dims
 // of lane group h = l / 16 per step: 16-byte chunk h + 4j of the row covers steps 4j .. 4j + 3,
@@ -56,11 +56,11 @@ typedef int v8i __attribute__((ext_vector_type(8)));
 typedef float v4f __attribute__((ext_vector_type(4)));
 typedef unsigned int u32x4 __attribute__((ext_vector_type(4)));
 
-constexpr int kThreads = 512;
+constexpr int kThreads = 768;  // the tile kernel: 12 wavefronts
 constexpr int kWaves = kThreads / kWave;
 constexpr int kSetQueries = 32;  // two MFMA query groups of 16 per wavefront
 constexpr int kQueriesPerLaunch = 4 * kSetQueries;
-constexpr int kTileSetsPerWave = 2;  // the tile kernel's wavefronts serve 64 queries each
+constexpr int kTileSetsPerWave = 1;  // query sets per tile-kernel wavefront
 constexpr int kTileBytesTarget = 48 * 1024;
 constexpr int kMinBatch = 4;  // below this the VALU popcount scan does less work per row
 
@@ -142,7 +142,7 @@ __device__ __forceinline__ void binaryThreshold(const EmitArgs& emit, int q, int
 }
 
 template <int kWords, bool kDense>
-__global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(2, 2)))
+__global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(3, 3)))
 void mfmaBinaryScanKernel(ScanArgs scan, PhaseArgs phase, EmitArgs emit, int q_offset, int q_count) {
     using Tile = BinaryTile<kWords>;
     constexpr int kRows = Tile::kRows;
@@ -342,10 +342,11 @@ void mfmaBinaryScanKernel(ScanArgs scan, PhaseArgs phase, EmitArgs emit, int q_o
                 }
                 // One path for any number of live query groups (a group without queries has zero
                 // B operands), so the compiler has no several copies of the expansion to hoist;
-                // each expansion feeds every group's MFMA. The A operand is double-buffered: step t's MFMAs are issued first,
-                // then step t + 1's expansion into the other buffer, which the matrix core is
-                // not reading, so the VALU work runs under the MFMAs instead of waiting for them
-                // to read their operands; a sched_barrier per step pins that order.
+                // each expansion feeds every group's MFMA. The A operand is double-buffered: step
+                // t's MFMAs are issued first, then step t + 1's expansion into the other buffer,
+                // which the matrix core is not reading, so the VALU work runs under the MFMAs
+                // instead of waiting for them to read their operands; a sched_barrier per step pins
+                // that order.
                 v4i a[2];
                 a[0] = spreadNibbles(chunk[0][0]);
 #pragma unroll
