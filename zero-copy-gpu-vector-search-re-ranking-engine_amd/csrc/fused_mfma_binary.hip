@@ -5,8 +5,8 @@
 //
 // Arithmetic. With r the row's bits and q the query's bits as 0/1 values,
 //   sum_k r_k (1 - 2 q_k) = popc(r) - 2 r.q,  so  h = popc(r) + popc(q) - 2 r.q = acc / 2 + popc(q)
-// where acc is the v_mfma_scale_f32_16x16x128_f8f6f4 product of the row's e2m1 nibbles (A: 0, 1
-// or 2) with the query's (B: +-2 or +-1), chosen so that every product is 2 r_k (1 - 2 q_k)
+// where acc is the v_mfma_scale_f32_16x16x128_f8f6f4 product of the row's e2m1 nibbles (A: 0, 0.5,
+// 1 or 2) with the query's (B: +-4, +-2 or +-1), chosen so that every product is 2 r_k (1 - 2 q_k)
 // (spreadNibbles, signNibbles). Every value is a small integer (|acc| <= 2 d, far below 2^24), so
 // the fp32 accumulator and h are exact; the score is the reference's IEEE division (d - 2h) / d.
 // A threshold phase compares h itself with the integer threshold equivalent to the query's key
@@ -15,7 +15,7 @@
 // Expansion. Each lane turns one 32-bit word of its row into 32 nibbles per k-step: nibble e of
 // dword j holds bit 4e + j of the word. That is a fixed permutation of the word's dims, and the
 // query's B operand uses the same one; a dot product does not depend on the order of its dims.
-// Four ANDs and two shifts per word, shared by the two query groups of 16 a wavefront serves. (An
+// Four ANDs and one shift per word, shared by the two query groups of 16 a wavefront serves. (An
 // int8 form on v_mfma_i32_16x16x64_i8 takes two steps and eight ANDs per word for the same
 // matrix-core cycles per step.)
 //
@@ -83,33 +83,34 @@ struct BinaryTile {
     }
 };
 
-// fp4 (e2m1) operands: nibble 0010 is 1, 0100 is 2 and bit 3 is the sign (every value used is a
-// normal number). A row word becomes 32 nibbles: nibble e of dword j holds bit 4e + j of the word,
-// as 0 or 1 (j < 2, the bit moved to nibble bit 1) or 0 or 2 (j >= 2, moved to nibble bit 2).
+// fp4 (e2m1) operands: nibble 0001 is 0.5 (the format's one subnormal, which the matrix core takes
+// exactly: the scans are bit-exact against the oracle), 0010 is 1, 0100 is 2, 0110 is 4 and bit 3
+// is the sign. A row word becomes 32 nibbles: nibble e of dword j holds bit 4e + j of the word in
+// place (j < 3: 0 or 0.5, 1, 2) or moved to nibble bit 2 (j = 3: 0 or 2), four ANDs and one shift.
 __device__ __forceinline__ v4i spreadNibbles(std::uint32_t word) {
     v4i out;
-    out[0] = static_cast<int>((word << 1) & 0x22222222u);
+    out[0] = static_cast<int>(word & 0x11111111u);
     out[1] = static_cast<int>(word & 0x22222222u);
     out[2] = static_cast<int>(word & 0x44444444u);
     out[3] = static_cast<int>((word >> 1) & 0x44444444u);
     return out;
 }
 
-// The same 32 dims of a query word as spreadNibbles, as (1 - 2 bit) 2 (j < 2) or (1 - 2 bit)
-// (j >= 2), so that every product with spreadNibbles' nibble is 2 r (1 - 2 q).
+// The same 32 dims of a query word as spreadNibbles, as (1 - 2 bit) times 4, 2, 1, 1 for j = 0..3,
+// so that every product with spreadNibbles' nibble is 2 r (1 - 2 q).
 __device__ __forceinline__ v4i signNibbles(std::uint32_t word) {
     v4i out;
 #pragma unroll
     for (int j = 0; j < 4; ++j) {
-        const std::uint32_t magnitude = j < 2 ? 0x44444444u : 0x22222222u;
+        const std::uint32_t magnitude = j == 0 ? 0x66666666u : (j == 1 ? 0x44444444u : 0x22222222u);
         out[j] = static_cast<int>((((word >> j) & 0x11111111u) << 3) | magnitude);
     }
     return out;
 }
 
 // v_mfma_scale_f32_16x16x128_f8f6f4 with both operands fp4 (format code 4; the instruction reads
-// the low four registers of each) and unit scales (E8M0 127 = 2^0). Products of +-1 and +-2 and
-// their sums below 2^24 are exact in the fp32 accumulators.
+// the low four registers of each) and unit scales (E8M0 127 = 2^0). Products of +-2 and their sums
+// below 2^24 are exact in the fp32 accumulators.
 __device__ __forceinline__ v4f mfmaNibbles(const v4i& a, const v4i& b, const v4f& c) {
     constexpr int kFp4 = 4;
     constexpr int kScaleOne = 127;
