@@ -401,7 +401,6 @@ void mfmaBinaryScanKernel(ScanArgs scan, PhaseArgs phase, EmitArgs emit, int q_o
     }
 }
 
-
 constexpr int kStreamThreads = 1024;
 constexpr int kStreamWaves = kStreamThreads / kWave;
 constexpr int kStreamSlots = 2;  // LDS pair slots per wavefront
@@ -414,9 +413,8 @@ constexpr int kStreamSlots = 2;  // LDS pair slots per wavefront
 // the registers four wavefronts fit a SIMD, whose copies hide each other's latency. (Loading the
 // MFMA layout straight into registers reads half cache lines per quarter-wave: measured 8%
 // slower for 50M x 1024, B = 32.) Each B fragment read from LDS feeds two MFMAs (the pair's two
-// blocks). Wavefront w of
-// workgroup b takes pairs w * gridDim.x + b, + 16 * gridDim.x, ... of the phase's items (an
-// item's pairs in order), so the pairs spread over the workgroups first.
+// blocks). Wavefront w of workgroup b takes pairs w * gridDim.x + b, + 16 * gridDim.x, ... of the
+// phase's items (an item's pairs in order), so the pairs spread over the workgroups first.
 //
 // Modes: kStreamThreshold (keys above the threshold to the workgroup's segment), kStreamDense
 // (every key to its fixed slot), kStreamSketch (no keys: per pair of wavefronts the least Hamming
@@ -578,7 +576,7 @@ void mfmaBinaryStreamKernel(ScanArgs scan, PhaseArgs phase, EmitArgs emit, int q
     // that land at slot position l % kChunks, so every copy reads 1 KB of consecutive rows (whole
     // cache lines per quarter-wave). Rows past the corpus re-read its last row (their keys are never
     // emitted). Pair indices stay below 2^31: 32-bit division by the constant kPairs.
-    // this lane's byte offset within a pair for each copy
+    // copy_offset[k]: this lane's source byte offset within the pair for copy k
     std::uint32_t copy_offset[kPairCopies];
 #pragma unroll
     for (int k = 0; k < kPairCopies; ++k) {
