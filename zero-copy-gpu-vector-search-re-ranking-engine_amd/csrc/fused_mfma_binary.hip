@@ -20,8 +20,8 @@
 // matrix-core cycles per step.)
 //
 // Work split. Launches of up to 32 queries (one set, two MFMA query groups of 16) run
-// mfmaBinaryStreamKernel: the B operands sit in LDS and each of 16 wavefronts streams its own
-// rows through LDS slots of its own (no shared tile, no barrier). It serves the sketch plan of
+// mfmaBinaryStreamKernel: each of 12 wavefronts holds the set's B operands in registers and
+// streams its own rows through LDS slots of its own (no shared tile, no barrier). It serves the sketch plan of
 // any batch, one launch per set: a sketch mode (the least distance of each query per pair of
 // wavefronts, no keys) and a rerun mode (the device list of flagged queries). Larger batches scan
 // up to 4 sets (128 queries) at a time on mfmaBinaryScanKernel: 12 wavefronts, three per SIMD,
@@ -401,24 +401,24 @@ void mfmaBinaryScanKernel(ScanArgs scan, PhaseArgs phase, EmitArgs emit, int q_o
     }
 }
 
-constexpr int kStreamThreads = 1024;
+constexpr int kStreamThreads = 768;
 constexpr int kStreamWaves = kStreamThreads / kWave;
-constexpr int kStreamSlots = 2;  // LDS pair slots per wavefront
+constexpr int kStreamSlots = 3;  // LDS pair slots per wavefront
 
-// One query set (<= 32 queries): the set's B operands sit in LDS, shared by the workgroup's 16
-// wavefronts, and each wavefront streams its own rows, 32 rows (two 16-row blocks) at a time,
-// through two LDS pair slots of its own: global_load_lds copies of whole cache lines land a pair
-// two pairs ahead, and the pair being multiplied is read from its slot into registers in the
-// MFMA layout. No tile is shared, so there is no barrier in the loop, and with the queries out of
-// the registers four wavefronts fit a SIMD, whose copies hide each other's latency. (Loading the
-// MFMA layout straight into registers reads half cache lines per quarter-wave: measured 8%
-// slower for 50M x 1024, B = 32.) Each B fragment read from LDS feeds two MFMAs (the pair's two
-// blocks). Wavefront w of workgroup b takes pairs w * gridDim.x + b, + 16 * gridDim.x, ... of the
-// phase's items (an item's pairs in order), so the pairs spread over the workgroups first.
+// One query set (<= 32 queries): each of the workgroup's 12 wavefronts (three per SIMD) holds the
+// set's B operands in registers and streams its own rows, 32 rows (two 16-row blocks) at a time,
+// through three LDS pair slots of its own (144 KB per workgroup at 1024 bits): global_load_lds
+// copies of whole cache lines land a pair three pairs ahead, and the pair being multiplied is read
+// from its slot into registers in the MFMA layout. No tile is shared, so there is no barrier in
+// the loop. (Loading the MFMA layout straight into registers reads half cache lines per
+// quarter-wave: measured 8% slower for 50M x 1024, B = 32; 16 wavefronts with the B operands in
+// LDS and two slots each, 1.5-2% slower.) Each B operand feeds two MFMAs (the pair's two blocks).
+// Wavefront w of workgroup b takes pairs w * gridDim.x + b, + 12 * gridDim.x, ... of the phase's
+// items (an item's pairs in order), so the pairs spread over the workgroups first.
 //
 // Modes: kStreamThreshold (keys above the threshold to the workgroup's segment), kStreamDense
 // (every key to its fixed slot), kStreamSketch (no keys: per pair of wavefronts the least Hamming
-// distance of each query, as a score, to sketch slot 8 * workgroup + wave / 2) and kStreamRerun
+// distance of each query, as a score, to sketch slot 6 * workgroup + wave / 2) and kStreamRerun
 // (kStreamThreshold over the queries of EmitArgs::q_list, in the list's segment layout; a kernel
 // of its own, so profiles tell the fallback's launches apart).
 constexpr int kStreamThreshold = 0;
@@ -446,7 +446,6 @@ void mfmaBinaryStreamKernel(ScanArgs scan, PhaseArgs phase, EmitArgs emit, int q
     constexpr int kPairBytes = 32 * kRowBytes;
     constexpr int kPairCopies = kPairBytes / 1024;  // one 1 KB global_load_lds_dwordx4 per 1024 / kRowBytes rows
     constexpr int kRowsPerCopy = 1024 / kRowBytes;
-    __shared__ v4i qlds[kSteps][2][kWave];  // B operand of (step, query group, lane)
     // each wavefront's two pair slots; slot position s of pair row r holds chunk s ^ swizzle(r)
     __shared__ __attribute__((aligned(16))) std::uint8_t pair_lds[kStreamWaves][kStreamSlots][kPairBytes];
     __shared__ std::uint32_t lds_count[kSetQueries];
@@ -486,18 +485,20 @@ void mfmaBinaryStreamKernel(ScanArgs scan, PhaseArgs phase, EmitArgs emit, int q
 
     // B operands: lane l of group g at step t supplies query g * 16 + l % 16, word t % 4 of its
     // chunk l / 16 + 4 (t / 4) (as the A operand's lanes do for their rows)
-    for (int e = tid; e < kSteps * 2 * kWave; e += kStreamThreads) {
-        const int t = e / (2 * kWave);
-        const int g = (e / kWave) % 2;
-        const int l = e % kWave;
-        const int qlocal = g * 16 + (l & 15);
-        v4i value = {0, 0, 0, 0};
-        if (qlocal < q_count) {
-            const std::uint32_t word = qwords[static_cast<std::size_t>(queryOf(qlocal)) * kWords +
-                                              4 * ((l >> 4) + 4 * (t / 4)) + t % 4];
-            value = signNibbles(word);
+    v4i qreg[kSteps][2];
+#pragma unroll
+    for (int g = 0; g < 2; ++g) {
+        const int qlocal = g * 16 + r16;
+#pragma unroll
+        for (int t = 0; t < kSteps; ++t) {
+            v4i value = {0, 0, 0, 0};
+            if (qlocal < q_count) {
+                const std::uint32_t word = qwords[static_cast<std::size_t>(queryOf(qlocal)) * kWords +
+                                                  4 * (h + 4 * (t / 4)) + t % 4];
+                value = signNibbles(word);
+            }
+            qreg[t][g] = value;
         }
-        qlds[t][g][l] = value;
     }
     for (int i = tid; i < kSetQueries; i += kStreamThreads) {
         lds_count[i] = 0u;
@@ -632,18 +633,10 @@ void mfmaBinaryStreamKernel(ScanArgs scan, PhaseArgs phase, EmitArgs emit, int q
         // The B operands of step t + 1 are read from LDS during step t. The lane's index is
         // opaque to the compiler, which would otherwise keep every step's B operands in registers
         // across pairs (64 more registers, and spills).
-        int ql = lane;
-        asm volatile("" : "+v"(ql));
-        v4i b0 = qlds[0][0][ql];
-        v4i b1 = qlds[0][1][ql];
 #pragma unroll
         for (int t = 0; t < kSteps; ++t) {
-            v4i nb0 = b0;
-            v4i nb1 = b1;
-            if (t + 1 < kSteps) {
-                nb0 = qlds[t + 1][0][ql];
-                nb1 = qlds[t + 1][1][ql];
-            }
+            const v4i b0 = qreg[t][0];
+            const v4i b1 = qreg[t][1];
             acc[0][0] = mfmaNibbles(a[0], b0, acc[0][0]);
             acc[0][1] = mfmaNibbles(a[0], b1, acc[0][1]);
             acc[1][0] = mfmaNibbles(a[1], b0, acc[1][0]);
@@ -652,9 +645,6 @@ void mfmaBinaryStreamKernel(ScanArgs scan, PhaseArgs phase, EmitArgs emit, int q
                 a[0] = spreadNibbles(cur[0][(t + 1) / 4][(t + 1) % 4]);
                 a[1] = spreadNibbles(cur[1][(t + 1) / 4][(t + 1) % 4]);
             }
-            b0 = nb0;
-            b1 = nb1;
-            // step by step: the compiler would otherwise hoist every step's B reads up front
             __builtin_amdgcn_sched_barrier(0);
         }
         // every product is finished here: block 1's are otherwise sunk past block 0's emission,
@@ -700,25 +690,26 @@ void mfmaBinaryStreamKernel(ScanArgs scan, PhaseArgs phase, EmitArgs emit, int q
     const long long stride = static_cast<long long>(gridDim.x) * kStreamWaves;
     // workgroup-first: with few pairs every workgroup (candidate segment) still gets its share
     long long p = static_cast<long long>(wave) * gridDim.x + blockIdx.x;
-    // Two pairs in flight while one is multiplied, with no registers held for them: pair i waits in
-    // slot i % 2 of the wavefront's LDS, copied there two pairs ahead. Every iteration issues one
-    // pair's copies (past the phase's end, its last pair again), so before pair i is read only pair
-    // i + 1's copies may still be pending (later global stores of the emission only make the
-    // wait stricter). The copies are inline assembly the compiler does not count, hence the
+    // Three pairs in flight while one is multiplied, with no registers held for them: pair i waits
+    // in slot i % 3 of the wavefront's LDS, copied there three pairs ahead. Every iteration issues
+    // one pair's copies (past the phase's end, its last pair again), so before pair i is read only
+    // pairs i + 1 and i + 2 may still be pending (later global stores of the emission only make
+    // the wait stricter). The copies are inline assembly the compiler does not count, hence the
     // explicit waits; the memory clobbers keep the LDS reads between them.
     const long long mine = p < pairs ? (pairs - p + stride - 1) / stride : 0;  // this wave's pairs
     if (mine > 0) {
         copyPair(p, 0);
         copyPair(min(p + stride, pairs - 1), 1);
+        copyPair(min(p + 2 * stride, pairs - 1), 2);
     }
     for (long long i = 0; i < mine; ++i) {
-        const int slot = static_cast<int>(i & 1);
-        asm volatile("s_waitcnt vmcnt(%0)" : : "n"(kPairCopies) : "memory");
+        const int slot = static_cast<int>(i % 3);
+        asm volatile("s_waitcnt vmcnt(%0)" : : "n"(2 * kPairCopies) : "memory");
         u32x4 cur[2][kLaneChunks];
         readPair(slot, cur);
         // the slot's reads are done before its next copy is issued
         asm volatile("s_waitcnt lgkmcnt(0)" : : : "memory");
-        copyPair(min(p + 2 * stride, pairs - 1), slot);
+        copyPair(min(p + 3 * stride, pairs - 1), slot);
         processPair(cur, p);
         p += stride;
     }
@@ -727,7 +718,7 @@ void mfmaBinaryStreamKernel(ScanArgs scan, PhaseArgs phase, EmitArgs emit, int q
 
     if constexpr (kSketch) {
         // the least distance per query over the lane groups h, then over each pair of
-        // wavefronts, written as a score to slot 8 * workgroup + wave / 2
+        // wavefronts, written as a score to slot 6 * workgroup + wave / 2
 #pragma unroll
         for (int g = 0; g < 2; ++g) {
             best_hd[g] = min(best_hd[g], waveXor(best_hd[g], 16));
